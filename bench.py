@@ -1,0 +1,256 @@
+"""Benchmark of the weight-only quantized linear layer on one MI355X.
+
+python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-sweep] [--no-cpu]
+
+Headline workload (one JSON line, `value`): INT8 per-output-channel decode GEMV at the
+Qwen2.5-7B MLP shape, W int8 [18944, 3584], x bf16 [1, 3584] -> y bf16 [1, 18944].
+A step is one forward of the layer. `value` is algorithmic GB/s = (W + scales + x + y
+bytes) / time per step, with inputs resident in HBM. The timed region is a HIP graph of
+K back-to-back launches bracketed by events on the launch stream; successive launches
+cycle through enough distinct weight copies (> 256 MB) that every launch streams its
+weights from HBM rather than from the 256 MB Infinity Cache.
+
+`sweep` reports the other shapes of the same metric (INT8 M in {8,32,64}, INT4 group-128
+decode M in {1,16,64} at 18944x3584, INT4 group-128 prefill M in {256,2048,8192} at
+14336x4096 in TFLOP/s); `cpu_baseline` times the reference's CPU path (dequantize, then
+F.linear, on the host cores) on the headline shape.
+"""
+
+from __future__ import annotations
+
+import argparse
+import hashlib
+import json
+import os
+import platform
+import statistics
+import sys
+import time
+
+import torch
+
+METRIC = "W-only INT4/INT8 GEMM: decode GB/s (% HBM peak); prefill TFLOP/s (% MFMA)"
+HBM_PEAK_GBS = 8000.0       # MI355X HBM3E, vendor spec
+MFMA_BF16_PEAK_TF = 2500.0  # MI355X dense bf16, vendor spec
+MALL_BYTES = 256 << 20
+
+
+# ----------------------------------------------------------------------------- inputs
+
+
+def _gen(seed: int) -> torch.Generator:
+    return torch.Generator().manual_seed(seed)
+
+
+def sha(t: torch.Tensor) -> str:
+    return hashlib.sha256(t.contiguous().view(torch.uint8).numpy().tobytes()).hexdigest()[:16]
+
+
+def make_int8(n: int, k: int, m: int, x_dtype=torch.bfloat16, seed: int = 0,
+              s_lo: float = 0.001, s_hi: float = 0.02):
+    """INT8 per-channel inputs on the CPU, draw order W -> scale -> x:
+    W uniform int in [-127, 127], fp32 scale U[s_lo, s_hi] [N, 1], x ~ N(0, 1)."""
+    g = _gen(seed)
+    w = torch.randint(-127, 128, (n, k), generator=g, dtype=torch.int8)
+    s = torch.rand((n, 1), generator=g) * (s_hi - s_lo) + s_lo
+    x = torch.randn((m, k), generator=g).to(x_dtype)
+    return w, s, x
+
+
+def make_int4(n: int, k: int, m: int, group: int = 128, x_dtype=torch.bfloat16, seed: int = 0,
+              s_lo: float = 0.001, s_hi: float = 0.05):
+    """INT4 group-wise inputs on the CPU, draw order W -> scale -> x:
+    q uniform int in [-8, 7] packed two per byte (low nibble = even column), bf16 scales
+    U[s_lo, s_hi] [N, K/group], x ~ N(0, 1)."""
+    from localstrm_amd.quantization import pack_int4
+
+    g = _gen(seed)
+    q = torch.randint(-8, 8, (n, k), generator=g, dtype=torch.int8)
+    s = (torch.rand((n, -(-k // group)), generator=g) * (s_hi - s_lo) + s_lo).to(torch.bfloat16)
+    x = torch.randn((m, k), generator=g).to(x_dtype)
+    return pack_int4(q), s, x
+
+
+def decode_bytes(kind: str, n: int, k: int, m: int, group: int = 128) -> int:
+    """Algorithmic bytes per call: W + scales + x + y (bf16 activations)."""
+    if kind == "int8":
+        return n * k + n * 4 + m * k * 2 + m * n * 2
+    return n * k // 2 + n * (-(-k // group)) * 2 + m * k * 2 + m * n * 2
+
+
+# ----------------------------------------------------------------------------- timing
+
+
+def _layers(kind, w, s, group, copies, device):
+    from localstrm_amd import QuantizedLinear
+
+    out = []
+    for i in range(copies):
+        wc = w.to(device)
+        if i:
+            wc = wc.clone()
+        if kind == "int8":
+            out.append(QuantizedLinear.from_quantized(wc, s.to(device), quant_type="int8"))
+        else:
+            out.append(QuantizedLinear.from_quantized(wc, s.to(device), quant_type="int4",
+                                                      in_features=w.shape[1] * 2, group_size=group))
+    return out
+
+
+def time_layers(layers, x, steps: int, warmup: int) -> float:
+    """Mean ms per forward over `steps` launches replayed from one HIP graph, cycling the
+    weight copies; bracketed by events on the launch stream."""
+    stream = torch.cuda.Stream()
+    with torch.no_grad():
+        y = layers[0](x)
+        for i in range(max(warmup, 1)):
+            layers[i % len(layers)](x)
+        torch.cuda.synchronize()
+        stream.wait_stream(torch.cuda.current_stream())
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(stream):
+            with torch.cuda.graph(graph, stream=stream):
+                for i in range(steps):
+                    y = layers[i % len(layers)](x)
+        graph.replay()  # warm replay
+        torch.cuda.synchronize()
+        start = torch.cuda.Event(enable_timing=True)
+        stop = torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(stream):
+            start.record(stream)
+            graph.replay()
+            stop.record(stream)
+        stop.synchronize()
+        del graph
+    return start.elapsed_time(stop) / steps
+
+
+def copies_for(nbytes: int) -> int:
+    return max(2, min(32, -(-2 * MALL_BYTES // max(nbytes, 1)) + 1))
+
+
+def bench_decode(kind: str, n: int, k: int, m: int, steps: int, warmup: int, device, group=128):
+    if kind == "int8":
+        w, s, x = make_int8(n, k, m)
+    else:
+        w, s, x = make_int4(n, k, m, group)
+    wbytes = w.numel()
+    copies = copies_for(wbytes)
+    layers = _layers(kind, w, s, group, copies, device)
+    ms = time_layers(layers, x.to(device), steps, warmup)
+    nbytes = decode_bytes(kind, n, k, m, group)
+    flops = 2.0 * m * n * k
+    del layers
+    torch.cuda.empty_cache()
+    return {
+        "kind": kind, "M": m, "N": n, "K": k, "group": None if kind == "int8" else group,
+        "us_per_call": ms * 1e3, "GB_s": nbytes / (ms * 1e-3) / 1e9,
+        "TFLOP_s": flops / (ms * 1e-3) / 1e12, "bytes": nbytes, "weight_copies": copies,
+        "frac_hbm": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+        "frac_mfma": flops / (ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TF,
+    }
+
+
+# ----------------------------------------------------------------------------- CPU baseline
+
+
+def cpu_baseline(n: int, k: int, m: int, budget_s: float = 15.0):
+    """The reference's CPU path (dequantize in the activation dtype, then F.linear) on the
+    host cores, on the headline shape, for about `budget_s` seconds."""
+    from oracle import torch_ref
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    w, s, x = make_int8(n, k, m)
+    times = []
+    with torch.no_grad():
+        for _ in range(2):
+            torch_ref.forward_int8(x, w, s)
+        t_end = time.perf_counter() + budget_s
+        while time.perf_counter() < t_end and len(times) < 50:
+            t0 = time.perf_counter()
+            torch_ref.forward_int8(x, w, s)
+            times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    cpu_model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    cpu_model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {
+        "value": decode_bytes("int8", n, k, m) / med / 1e9, "unit": "GB/s",
+        "cores": torch.get_num_threads(), "kind": "port",
+        "sample": (f"int8 decode {n}x{k} M={m}, bf16: torch CPU dequantize + F.linear, "
+                   f"median of {len(times)} runs ({med * 1e3:.1f} ms/call), cpu '{cpu_model}', "
+                   f"os.cpu_count()={os.cpu_count()}"),
+    }
+
+
+# ----------------------------------------------------------------------------- main
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-sweep", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this layer's multi-GPU sharding is not built "
+              "(run with --gpus 1)", file=sys.stderr)
+        return 2
+    if not torch.cuda.is_available():
+        print("bench.py needs a HIP device", file=sys.stderr)
+        return 2
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    device = torch.device("cuda:0")
+    torch.cuda.set_device(device)
+
+    N, K, M = 18944, 3584, 1
+    head = bench_decode("int8", N, K, M, args.steps, args.warmup, device)
+    sweep = []
+    if not args.no_sweep:
+        for m in (8, 32, 64):
+            sweep.append(bench_decode("int8", N, K, m, args.steps, args.warmup, device))
+        for m in (1, 16, 64):
+            sweep.append(bench_decode("int4", N, K, m, args.steps, args.warmup, device))
+    cpu = None if args.no_cpu else cpu_baseline(N, K, M)
+
+    ms = head["us_per_call"] / 1e3
+    line = {
+        "metric": METRIC,
+        "value": round(head["GB_s"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: seeded torch.Generator(0) inputs of the stated shapes",
+        "config": {
+            "workload": "int8 per-channel decode GEMV, W int8 18944x3584, x bf16 [1,3584]",
+            "M": M, "N": N, "K": K, "weight_copies": head["weight_copies"],
+            "timing": "HIP graph of `steps` launches, events on the launch stream",
+        },
+        "roofline": {
+            "bound": "hbm", "achieved": round(head["GB_s"], 2), "peak": HBM_PEAK_GBS,
+            "unit": "GB/s", "frac": round(head["frac_hbm"], 4), "traffic": None,
+        },
+        "cpu_baseline": cpu,
+        "sweep": sweep,
+        "host": platform.node(),
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

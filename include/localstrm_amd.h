@@ -1,0 +1,111 @@
+/*
+ * localstrm_amd: weight-only quantized linear layer for AMD Instinct MI355X (gfx950).
+ *
+ * C ABI of liblsq.so. Every entry point takes plain device pointers, sizes and a
+ * hipStream_t (passed as void* so this header needs no HIP include), enqueues its
+ * kernels on that stream and returns without synchronizing. The return value is a
+ * status: 0 on success, a negative LSQ_E* code for a rejected argument, or a positive
+ * hipError_t from the launch. lsq_status_string() turns either into text.
+ *
+ * Shapes follow the reference's QuantizedLinear (src/kernels/quantization.py:34-149):
+ *   N = out_features (weight rows), K = in_features, M = tokens (rows of x).
+ *   INT8: weight_q int8 [N, K] row-major, scale [N] (the [N,1] buffer; fp32 in the
+ *         reference, any of the three dtype codes after a module dtype cast).
+ *   INT4: weight_packed uint8 [N, (K+1)/2] row-major; byte j of row n holds
+ *         (q[n,2j]+8) | (q[n,2j+1]+8) << 4   (quantization.py:86-91);
+ *         scale [N, G] in fp32 or bf16 with G = ceil(K / group_size). A group_size
+ *         >= K is the reference's per-output-channel INT4 (quantization.py:80-83).
+ * Activation / output dtype T is one of LSQ_F32, LSQ_F16, LSQ_BF16. Dequantization is
+ * the closed form of quantization.py:106-122 evaluated in T:
+ *   W[n,k] = round_T( T(q[n,k]) * round_T(scale[n, k / group_size]) )
+ * and the linear layer is F.linear (quantization.py:141): y = x W^T + round_T(bias),
+ * fp32 accumulation, one rounding to T at the end.
+ */
+#ifndef LOCALSTRM_AMD_H
+#define LOCALSTRM_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* dtype codes for activations, outputs, scales and bias */
+#define LSQ_F32 0
+#define LSQ_F16 1
+#define LSQ_BF16 2
+
+/* argument errors (negative); positive values are hipError_t */
+#define LSQ_OK 0
+#define LSQ_E_NULL (-1)        /* a required pointer is NULL */
+#define LSQ_E_SHAPE (-2)       /* M, N or K out of range, or a leading dim < row length */
+#define LSQ_E_DTYPE (-3)       /* unsupported dtype code */
+#define LSQ_E_GROUP (-4)       /* group_size < 1 */
+#define LSQ_E_LAYOUT (-5)      /* tiled INT4 layout needs K % 128 == 0 */
+#define LSQ_E_ALIGN (-6)       /* pointer or leading dim not aligned as the kernel needs */
+
+/* Library version (major*10000 + minor*100 + patch). No reference counterpart. */
+int lsq_version(void);
+
+/* Text for a status code returned by any entry point. Never NULL. */
+const char* lsq_status_string(int status);
+
+/* Dequantize INT8 per-output-channel weights to dtype out_dtype.
+ * Replaces QuantizedLinear.dequantize for quant_type "int8"
+ * (src/kernels/quantization.py:104-108): W = weight_q.to(T) * scale.to(T). */
+int lsq_dequant_w8(const int8_t* weight_q, const void* scale, int scale_dtype, void* w_out,
+                   int out_dtype, int64_t N, int64_t K, void* stream);
+
+/* Dequantize packed INT4 weights (group-wise scales) to dtype out_dtype.
+ * Replaces QuantizedLinear.dequantize for quant_type "int4"
+ * (src/kernels/quantization.py:109-122); group_size >= K is the reference's per-channel
+ * case, smaller groups are the group-wise extension W[n,k] = q * scale[n, k/group_size]. */
+int lsq_dequant_w4(const uint8_t* weight_packed, const void* scale, int scale_dtype,
+                   int64_t group_size, void* w_out, int out_dtype, int64_t N, int64_t K,
+                   void* stream);
+
+/* Unpack INT4 nibbles to int8 q in [-8, 7], [N, K] row-major.
+ * The integer half of quantization.py:113-121 (the `unpacked` tensor). */
+int lsq_unpack_w4(const uint8_t* weight_packed, int8_t* q_out, int64_t N, int64_t K,
+                  void* stream);
+
+/* Bytes of the tiled INT4 layout for an [N, K] weight (0 if K % 128 != 0).
+ * No reference counterpart: the reference keeps only the canonical layout. */
+int64_t lsq_w4_tiled_bytes(int64_t N, int64_t K);
+
+/* Re-tile canonical packed INT4 weights into the decode layout: 16-row x 128-column
+ * tiles of 1024 contiguous bytes, each 64-lane wavefront load reading one tile with
+ * 16 bytes per lane, nibbles ordered for the in-register bf16/fp16 unpack. Rows past N
+ * are zero-filled. Derived from weight_packed as produced by
+ * src/kernels/quantization.py:86-91; the canonical buffer is left untouched. */
+int lsq_w4_retile(const uint8_t* weight_packed, uint8_t* tiled, int64_t N, int64_t K,
+                  void* stream);
+
+/* Inverse of lsq_w4_retile (for round-trip checks). */
+int lsq_w4_untile(const uint8_t* tiled, uint8_t* weight_packed, int64_t N, int64_t K,
+                  void* stream);
+
+/* y[M, N] = x[M, K] @ dequant(W8)^T + round_T(bias).
+ * Replaces QuantizedLinear.forward for quant_type "int8"
+ * (src/kernels/quantization.py:129-141). x and y have dtype `dtype`, row strides ldx and
+ * ldy (elements); bias is NULL or [N] of bias_dtype (rounded to `dtype` first, as
+ * quantization.py:135-140 casts it). */
+int lsq_w8_linear(const void* x, int64_t ldx, const int8_t* weight_q, const void* scale,
+                  int scale_dtype, const void* bias, int bias_dtype, void* y, int64_t ldy,
+                  int dtype, int64_t M, int64_t N, int64_t K, void* stream);
+
+/* y[M, N] = x[M, K] @ dequant(W4)^T + round_T(bias).
+ * Replaces QuantizedLinear.forward for quant_type "int4"
+ * (src/kernels/quantization.py:129-141), extended with group-wise scales.
+ * `tiled` is NULL or the output of lsq_w4_retile for the same weights; when given, the
+ * decode kernels stream it instead of weight_packed. */
+int lsq_w4_linear(const void* x, int64_t ldx, const uint8_t* weight_packed,
+                  const uint8_t* tiled, const void* scale, int scale_dtype,
+                  int64_t group_size, const void* bias, int bias_dtype, void* y, int64_t ldy,
+                  int dtype, int64_t M, int64_t N, int64_t K, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LOCALSTRM_AMD_H */

@@ -1,0 +1,103 @@
+// Shared device helpers for the gfx950 weight-only quantized linear kernels.
+//
+// Numeric contract (reference: src/kernels/quantization.py:104-141):
+//   dequant:  W[n,k] = round_T( float(q) * round_T(scale) )   -- one product, no FMA
+//   linear:   y[m,n] = round_T( sum_k x[m,k] * W[n,k]  (fp32)  + round_T(bias[n]) )
+// round_T is IEEE round-to-nearest-even into the activation type T; on gfx950 the
+// fp32->bf16 conversion is the hardware v_cvt_pk_bf16_f32 (RNE, NaN-preserving) and
+// fp32->fp16 is v_cvt_f16_f32 under the default RNE mode.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_bf16.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+
+#include "../../include/localstrm_amd.h"
+
+namespace lsq {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+// ---------------------------------------------------------------- scalar conversions
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) {
+  return __uint_as_float(static_cast<uint32_t>(b) << 16);
+}
+
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  __hip_bfloat16 h = __float2bfloat16(f);
+  return __builtin_bit_cast(uint16_t, h);
+}
+
+__device__ __forceinline__ float f16_to_f32(uint16_t b) {
+  return __half2float(__builtin_bit_cast(__half, b));
+}
+
+__device__ __forceinline__ uint16_t f32_to_f16(float f) {
+  return __builtin_bit_cast(uint16_t, __float2half(f));
+}
+
+// Activation/output dtype traits. `storage` is the element type in memory.
+template <int DT> struct Act;
+
+template <> struct Act<LSQ_F32> {
+  using storage = float;
+  static __device__ __forceinline__ float load(const storage* p) { return *p; }
+  static __device__ __forceinline__ float to_f32(storage v) { return v; }
+  static __device__ __forceinline__ storage from_f32(float v) { return v; }
+  static __device__ __forceinline__ float round(float v) { return v; }
+};
+
+template <> struct Act<LSQ_F16> {
+  using storage = uint16_t;
+  static __device__ __forceinline__ float to_f32(storage v) { return f16_to_f32(v); }
+  static __device__ __forceinline__ storage from_f32(float v) { return f32_to_f16(v); }
+  static __device__ __forceinline__ float round(float v) { return f16_to_f32(f32_to_f16(v)); }
+};
+
+template <> struct Act<LSQ_BF16> {
+  using storage = uint16_t;
+  static __device__ __forceinline__ float to_f32(storage v) { return bf16_to_f32(v); }
+  static __device__ __forceinline__ storage from_f32(float v) { return f32_to_bf16(v); }
+  static __device__ __forceinline__ float round(float v) { return bf16_to_f32(f32_to_bf16(v)); }
+};
+
+// Read element i of a scale / bias array stored with dtype code `dt`, as fp32.
+__device__ __forceinline__ float load_as_f32(const void* p, int dt, int64_t i) {
+  if (dt == LSQ_F32) return static_cast<const float*>(p)[i];
+  const uint16_t v = static_cast<const uint16_t*>(p)[i];
+  return dt == LSQ_BF16 ? bf16_to_f32(v) : f16_to_f32(v);
+}
+
+// Product q * s with a single rounding to fp32 (never contracted into an FMA).
+__device__ __forceinline__ float mul_rn(float a, float b) { return __fmul_rn(a, b); }
+
+// The reference dequant closed form for one element, returned as the fp32 value of the
+// T-typed result: round_T( float(q) * s_T ), s_T already rounded to T.
+template <int DT>
+__device__ __forceinline__ float dequant_elem(int q, float s_T) {
+  return Act<DT>::round(mul_rn(static_cast<float>(q), s_T));
+}
+
+// ---------------------------------------------------------------- wavefront helpers
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+// Non-temporal 16-byte global load: weights are streamed exactly once per call.
+__device__ __forceinline__ u32x4 load_nt_u32x4(const void* p) {
+  return __builtin_nontemporal_load(static_cast<const u32x4*>(p));
+}
+
+__device__ __forceinline__ u32x4 load_u32x4(const void* p) {
+  return *static_cast<const u32x4*>(p);
+}
+
+}  // namespace lsq

@@ -1,0 +1,199 @@
+"""CPU oracle for the weight-only quantized linear layer. TEST INFRASTRUCTURE ONLY.
+
+Only tests/, __graft_entry__.smoke() and bench.py's CPU-baseline leg may import this
+module, and only as the checker. The product (localstrm_amd) never imports it.
+
+A numpy restatement of LocalStrm's src/kernels/quantization.py, written from the
+reference's behaviour (no code copied):
+
+  quantize_int8       quantization.py:72-78   per-row symmetric INT8
+  quantize_int4       quantization.py:80-94   per-row symmetric INT4 + nibble pack;
+                      group_size < K is the group-wise extension (same steps per group,
+                      quantized against the stored, dtype-rounded scale)
+  pack_int4           quantization.py:86-91   byte j = (q[2j]+8) | (q[2j+1]+8) << 4
+  unpack_int4         quantization.py:113-121 the int8 `unpacked` tensor
+  dequant_int8        quantization.py:106-108 round_T(T(q) * round_T(s))
+  dequant_int4        quantization.py:109-122 same closed form, s[n, k // group_size]
+  linear              quantization.py:129-141 F.linear(x, W_T, bias_T), evaluated in
+                      float64 then rounded once to T
+
+How each part is pinned (tests/test_oracle.py):
+  * round_bf16 / round_f16 against torch's dtype casts on every bf16 boundary case,
+    plus hand-computed ties;
+  * quantizers against hand-computed known answers, round-half-even tie cases built
+    so that w / s is exactly .5, and torch's own op sequence on random data;
+  * pack/unpack against a hand-written byte vector, all 256 byte values, round trip;
+  * dequant exhaustively over all q values x random scales against torch casts;
+  * linear against float64 closed forms (one-hot x, identity W) and torch's CPU GEMM;
+  * group-wise dequant reduces to the per-channel form when group_size = K.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+F32, F16, BF16 = "f32", "f16", "bf16"
+
+
+# ----------------------------------------------------------------------------- rounding
+
+
+def round_bf16(a) -> np.ndarray:
+    """fp32 -> nearest bf16 (ties to even), returned as fp32. NaN stays NaN.
+
+    IEEE-754 round-to-nearest-even on the upper 16 bits: add 0x7FFF plus the lowest kept
+    bit, then truncate. Infinities and overflow to infinity fall out of the same carry.
+    """
+    f = np.ascontiguousarray(a, dtype=np.float32)
+    u = f.view(np.uint32).astype(np.uint64)
+    lsb = (u >> 16) & 1
+    r = ((u + 0x7FFF + lsb) >> 16) << 16
+    out = r.astype(np.uint32).view(np.float32).copy()
+    nan = np.isnan(f)
+    out[nan] = np.float32("nan")
+    return out
+
+
+def round_f16(a) -> np.ndarray:
+    """fp32 -> nearest fp16 (numpy's correctly rounded conversion), back to fp32."""
+    return np.asarray(a, dtype=np.float32).astype(np.float16).astype(np.float32)
+
+
+def round_to(a, dt: str) -> np.ndarray:
+    if dt == F32:
+        return np.asarray(a, dtype=np.float32)
+    if dt == F16:
+        return round_f16(a)
+    if dt == BF16:
+        return round_bf16(a)
+    raise ValueError(dt)
+
+
+def bf16_bits(a) -> np.ndarray:
+    """uint16 bit patterns of already-bf16-representable fp32 values."""
+    return (np.ascontiguousarray(round_bf16(a)).view(np.uint32) >> 16).astype(np.uint16)
+
+
+def from_bf16_bits(b) -> np.ndarray:
+    return (np.asarray(b, dtype=np.uint32) << 16).view(np.float32)
+
+
+# ----------------------------------------------------------------------------- quantizers
+
+
+def _row_scale(w32: np.ndarray, qmax: float) -> np.ndarray:
+    """clamp(max|w| / qmax, min=1e-8) in fp32, [N, 1] (quantization.py:74-75, :82-83)."""
+    max_val = np.max(np.abs(w32), axis=-1, keepdims=True).astype(np.float32)
+    return np.maximum(max_val / np.float32(qmax), np.float32(1e-8)).astype(np.float32)
+
+
+def quantize_int8(w) -> tuple[np.ndarray, np.ndarray]:
+    """(q int8 [N,K], scale fp32 [N,1]) per quantization.py:72-78; np.rint is half-to-even
+    like torch.round."""
+    w32 = np.asarray(w, dtype=np.float32)
+    s = _row_scale(w32, 127.0)
+    q = np.clip(np.rint(w32 / s), -128, 127).astype(np.int8)
+    return q, s
+
+
+def quantize_int4(w, group_size: int | None = None, scale_dt: str = F32):
+    """(packed uint8 [N, ceil(K/2)], scale [N, G] as fp32 values of dtype scale_dt).
+
+    group_size None (or >= K): quantization.py:80-94 exactly, fp32 scale.
+    group_size < K: per group of columns, scale = clamp(max|w|/7, 1e-8) rounded to
+    scale_dt, q = clamp(round(w / scale_stored), -8, 7).
+    """
+    w32 = np.asarray(w, dtype=np.float32)
+    n, k = w32.shape
+    if group_size is None or group_size >= k:
+        s = _row_scale(w32, 7.0)
+        q = np.clip(np.rint(w32 / s), -8, 7).astype(np.int8)
+        return pack_int4(q), s
+    g = -(-k // group_size)
+    pad = g * group_size - k
+    wa = np.abs(w32)
+    if pad:
+        wa = np.pad(wa, ((0, 0), (0, pad)))
+    max_val = wa.reshape(n, g, group_size).max(axis=-1).astype(np.float32)
+    s = round_to(np.maximum(max_val / np.float32(7.0), np.float32(1e-8)), scale_dt)
+    s_full = np.repeat(s, group_size, axis=1)[:, :k]
+    q = np.clip(np.rint(w32 / s_full), -8, 7).astype(np.int8)
+    return pack_int4(q), s
+
+
+def pack_int4(q) -> np.ndarray:
+    """int8 q in [-8,7] [N,K] -> uint8 [N, ceil(K/2)], low nibble = even column,
+    odd K pads the last high nibble with 0 (quantization.py:86-91)."""
+    q = np.asarray(q)
+    n, k = q.shape
+    u = (q.astype(np.int16) + 8).astype(np.uint8)
+    if k % 2:
+        u = np.concatenate([u, np.zeros((n, 1), np.uint8)], axis=1)
+    return (u[:, 0::2] | (u[:, 1::2] << 4)).astype(np.uint8)
+
+
+def unpack_int4(packed, k: int) -> np.ndarray:
+    """uint8 [N, ceil(K/2)] -> int8 q [N, K] (quantization.py:113-121)."""
+    p = np.asarray(packed, dtype=np.uint8)
+    n = p.shape[0]
+    out = np.empty((n, k), dtype=np.int8)
+    out[:, 0::2] = ((p & 0x0F).astype(np.int16) - 8)[:, : (k + 1) // 2]
+    out[:, 1::2] = ((p >> 4).astype(np.int16) - 8)[:, : k // 2]
+    return out
+
+
+# ----------------------------------------------------------------------------- dequant
+
+
+def dequant_int8(q, scale, dt: str) -> np.ndarray:
+    """round_T(T(q) * round_T(scale)) as fp32 values (quantization.py:106-108).
+    T(q) is exact for |q| <= 128 in all three types; the fp32 product is exact for bf16
+    and fp16 scales, and is the single fp32 rounding for T = fp32."""
+    qf = np.asarray(q, dtype=np.float32)
+    s = round_to(np.asarray(scale, dtype=np.float32).reshape(-1, 1), dt)
+    return round_to(qf * s, dt)
+
+
+def dequant_int4(packed, scale, k: int, group_size: int | None, dt: str) -> np.ndarray:
+    """round_T(T(q) * round_T(scale[n, k // g])) (quantization.py:109-122 + groups)."""
+    q = unpack_int4(packed, k).astype(np.float32)
+    s = np.asarray(scale, dtype=np.float32)
+    s = s.reshape(s.shape[0], -1)
+    if group_size is None or group_size >= k or s.shape[1] == 1:
+        s_full = np.broadcast_to(s[:, :1], q.shape)
+    else:
+        s_full = np.repeat(s, group_size, axis=1)[:, :k]
+    return round_to(q * round_to(s_full, dt), dt)
+
+
+# ----------------------------------------------------------------------------- linear
+
+
+def linear(x, w_deq, bias=None, dt: str = BF16) -> np.ndarray:
+    """y = round_T(x @ W^T + round_T(bias)) with the sum in float64 (quantization.py:141).
+
+    x and w_deq hold the T-valued inputs as fp32/float64. The reference's own GEMM
+    accumulates in fp32 in an unspecified order; float64 is the order-free target the
+    1e-2 relative bound is measured against.
+    """
+    x64 = np.asarray(x, dtype=np.float64)
+    acc = x64 @ np.asarray(w_deq, dtype=np.float64).T
+    if bias is not None:
+        acc = acc + round_to(np.asarray(bias, dtype=np.float32), dt).astype(np.float64)
+    return round_to(acc.astype(np.float32), dt)
+
+
+def linear_f64(x, w_deq, bias=None, dt: str = BF16) -> np.ndarray:
+    """Same as linear() but without the final rounding (for error budgets)."""
+    acc = np.asarray(x, dtype=np.float64) @ np.asarray(w_deq, dtype=np.float64).T
+    if bias is not None:
+        acc = acc + round_to(np.asarray(bias, dtype=np.float32), dt).astype(np.float64)
+    return acc
+
+
+def rel_err(a, b) -> float:
+    """max|a - b| / max(max|b|, 1e-6), the reference's convention
+    (tests/test_int8_multi_step.py:184-188)."""
+    a = np.asarray(a, dtype=np.float64)
+    b = np.asarray(b, dtype=np.float64)
+    return float(np.max(np.abs(a - b)) / max(float(np.max(np.abs(b))), 1e-6))

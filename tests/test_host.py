@@ -1,0 +1,245 @@
+"""Host-side tests (no GPU): loader routing and accounting, quantizer parity with the
+oracle, error behaviour, and the C ABI of liblsq.so (loads, exports every declared
+symbol, rejects bad arguments before touching the GPU).
+
+Mirrors the offline tier of the reference's tests/test_quantized_loader.py (routing
+:125-180, placement :185-206, invalid modes :360-372, failure cleanup :377-388, 'none'
+mode :393-407, mocked from_pretrained :412-433, unsupported architecture :468-486,
+trust_remote_code :491-507).
+"""
+
+import ctypes
+import os
+import re
+from unittest.mock import MagicMock, patch
+
+import numpy as np
+import pytest
+import torch
+import torch.nn as nn
+
+from localstrm_amd import QuantizedLinear, apply_optional_quantization, load_and_quantize_model
+from localstrm_amd import _lib
+from oracle import quant_oracle as qo
+from tests.synthetic import seeded_model
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "localstrm_amd.h")
+PROJS = ("q_proj", "k_proj", "v_proj", "o_proj")
+MLPS = ("gate_proj", "up_proj", "down_proj")
+
+
+# ----------------------------------------------------------------------------- loader
+
+
+@pytest.mark.parametrize("mode,min_savings", [("int8", 30.0), ("int4", 50.0)])
+def test_cpu_staged_loading_routes_all_projections(mode, min_savings):
+    model, orig, quant = load_and_quantize_model(seeded_model(), device="cpu", quantization=mode)
+    for layer in model.model.layers:
+        for p in PROJS:
+            m = getattr(layer.self_attn, p)
+            assert isinstance(m, QuantizedLinear) and m.quant_type == mode
+        for p in MLPS:
+            assert isinstance(getattr(layer.mlp, p), QuantizedLinear)
+        q = layer.self_attn.q_proj
+        if mode == "int8":
+            assert q.weight_q.dtype == torch.int8 and q.weight_q.shape == (64, 64)
+        else:
+            assert q.weight_packed.dtype == torch.uint8
+            assert q.weight_packed.shape == (q.out_features, (q.in_features + 1) // 2)
+    assert not isinstance(model.lm_head, QuantizedLinear)
+    assert (1.0 - quant / orig) * 100 > min_savings
+
+
+def test_group_wise_loading_and_accounting():
+    model, orig, quant = load_and_quantize_model(
+        seeded_model(), device="cpu", quantization="int4", group_size=32
+    )
+    q = model.model.layers[0].mlp.down_proj  # in_features 128 -> 4 groups
+    assert q.group_size == 32 and q.scale.shape == (64, 4) and q.scale.dtype == torch.bfloat16
+    assert quant < orig
+
+
+def test_cpu_device_placement():
+    model, _, _ = load_and_quantize_model(seeded_model(), device="cpu", quantization="int8")
+    assert all(p.device.type == "cpu" for p in model.parameters())
+    assert all(b.device.type == "cpu" for b in model.buffers())
+
+
+def test_invalid_modes():
+    model = seeded_model()
+    for mode in ["int16", "fp8", "awq", "gptq", "unknown_mode", "123"]:
+        with pytest.raises(ValueError, match="Invalid quantization mode"):
+            load_and_quantize_model(model, device="cpu", quantization=mode)
+        with pytest.raises(ValueError, match="Invalid quantization type"):
+            apply_optional_quantization(model, quant_type=mode)
+
+
+def test_failure_cleanup():
+    model = seeded_model()
+    with patch("localstrm_amd.quantization.apply_optional_quantization",
+               side_effect=RuntimeError("Simulated OOM")):
+        with patch("torch.cuda.empty_cache") as empty:
+            with pytest.raises(RuntimeError, match="Simulated OOM"):
+                load_and_quantize_model(model, device="cpu", quantization="int8")
+            if torch.cuda.is_available():
+                empty.assert_called()
+
+
+def test_none_mode_unchanged():
+    model, orig, quant = load_and_quantize_model(seeded_model(), device="cpu", quantization="none")
+    assert orig == quant
+    assert type(model.model.layers[0].self_attn.q_proj) is nn.Linear
+
+
+def test_mocked_from_pretrained_stages_on_cpu():
+    mock_model = seeded_model()
+    mock_model.to = MagicMock(return_value=mock_model)
+    with patch("transformers.AutoModelForCausalLM.from_pretrained", return_value=mock_model) as fp:
+        target = torch.device("cuda")
+        load_and_quantize_model("mock/model", device=target, quantization="int8")
+        fp.assert_called_once()
+        mock_model.to.assert_any_call("cpu")
+        mock_model.to.assert_any_call(target)
+
+
+@pytest.mark.parametrize("mode", ["int8", "int4", "hybrid_int8"])
+def test_unsupported_architecture(mode):
+    seq = nn.Sequential(nn.Linear(64, 128), nn.ReLU(), nn.Linear(128, 64))
+    with pytest.raises(ValueError) as ei:
+        apply_optional_quantization(seq, quant_type=mode)
+    msg = str(ei.value)
+    assert f"Quantization '{mode}' failed" in msg
+    assert "no compatible linear layers found" in msg
+    assert "Supported architectures require transformer blocks" in msg
+
+
+def test_hybrid_int8_is_rejected_loudly():
+    with pytest.raises(NotImplementedError):
+        apply_optional_quantization(seeded_model(), quant_type="hybrid_int8")
+
+
+@pytest.mark.parametrize("flag", [True, False])
+def test_trust_remote_code_pass_through(flag):
+    with patch("transformers.AutoModelForCausalLM.from_pretrained", return_value=seeded_model()) as fp:
+        load_and_quantize_model("custom/model-id", device="cpu", quantization="none",
+                                trust_remote_code=flag)
+        fp.assert_called_once()
+        assert fp.call_args[1].get("trust_remote_code") is flag
+
+
+# ----------------------------------------------------------------------------- quantizer parity
+
+
+def _linear(n, k, seed, bias=True):
+    torch.manual_seed(seed)
+    return nn.Linear(k, n, bias=bias)
+
+
+@pytest.mark.parametrize("k", [32, 33, 128, 1536])
+def test_from_float_int4_matches_oracle(k):
+    lin = _linear(64, k, k)
+    ql = QuantizedLinear.from_float(lin, "int4")
+    p, s = qo.quantize_int4(lin.weight.detach().numpy())
+    assert np.array_equal(ql.weight_packed.numpy(), p)
+    assert np.array_equal(ql.scale.numpy(), s)
+    assert ql.weight_packed.shape == (64, (k + 1) // 2)
+
+
+@pytest.mark.parametrize("shape", [(32, 32), (64, 32), (32, 64), (128, 64), (64, 128), (4864, 896)])
+def test_from_float_int8_matches_oracle(shape):
+    n, k = shape
+    lin = _linear(n, k, n + k)
+    ql = QuantizedLinear.from_float(lin, "int8")
+    q, s = qo.quantize_int8(lin.weight.detach().numpy())
+    assert np.array_equal(ql.weight_q.numpy(), q) and np.array_equal(ql.scale.numpy(), s)
+
+
+@pytest.mark.parametrize("group,sdt", [(128, torch.bfloat16), (64, torch.float32), (100, torch.bfloat16)])
+def test_from_float_int4_grouped_matches_oracle(group, sdt):
+    lin = _linear(48, 384, group)
+    ql = QuantizedLinear.from_float(lin, "int4", group_size=group, scale_dtype=sdt)
+    p, s = qo.quantize_int4(lin.weight.detach().numpy(), group_size=group,
+                            scale_dt="bf16" if sdt == torch.bfloat16 else "f32")
+    assert ql.scale.dtype == sdt
+    assert np.array_equal(ql.weight_packed.numpy(), p)
+    assert np.array_equal(ql.scale.float().numpy(), s)
+
+
+def test_from_quantized_validates_shapes():
+    w = torch.zeros(8, 16, dtype=torch.uint8)
+    ql = QuantizedLinear.from_quantized(w, torch.ones(8, 1), quant_type="int4")
+    assert ql.in_features == 32 and ql.scale.shape == (8, 1)
+    ql = QuantizedLinear.from_quantized(w, torch.ones(8, 2, dtype=torch.bfloat16), quant_type="int4",
+                                        in_features=31, group_size=16)
+    assert ql.in_features == 31 and ql.group_size == 16
+    with pytest.raises(ValueError):
+        QuantizedLinear.from_quantized(w, torch.ones(8, 3), quant_type="int4", group_size=16)
+    with pytest.raises(ValueError):
+        QuantizedLinear.from_quantized(w, torch.ones(8, 1), quant_type="int4", in_features=40)
+    q8 = QuantizedLinear.from_quantized(torch.zeros(8, 16, dtype=torch.int8), torch.ones(8),
+                                        bias=torch.zeros(8), quant_type="int8")
+    assert q8.scale.shape == (8, 1) and q8.bias is not None
+
+
+def test_state_dict_matches_reference_buffers():
+    ql = QuantizedLinear.from_float(_linear(16, 64, 0), "int4")
+    assert set(ql.state_dict().keys()) == {"weight_packed", "scale", "bias"}
+    q8 = QuantizedLinear.from_float(_linear(16, 64, 0, bias=False), "int8")
+    assert set(q8.state_dict().keys()) == {"weight_q", "scale"}
+
+
+def test_unknown_quant_type_is_float_layer():
+    ql = QuantizedLinear(8, 4, quant_type="fp8")
+    assert isinstance(ql.weight, nn.Parameter) and ql.weight.shape == (4, 8)
+
+
+# ----------------------------------------------------------------------------- no CPU path
+
+
+def test_cpu_forward_and_dequantize_raise():
+    for mode in ("int8", "int4"):
+        ql = QuantizedLinear.from_float(_linear(16, 32, 1), mode)
+        with pytest.raises(RuntimeError, match="GPU only"):
+            ql(torch.randn(2, 32))
+        with pytest.raises(RuntimeError, match="GPU only"):
+            ql.dequantize()
+
+
+# ----------------------------------------------------------------------------- C ABI
+
+
+def _declared_symbols():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\w[\w\s\*]*?\b(lsq_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_header_declares_what_the_binding_binds():
+    assert _declared_symbols() == sorted(_lib.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    for name in _declared_symbols():
+        assert hasattr(lib, name), name
+    assert lib.lsq_version() >= 100
+
+
+def test_library_rejects_bad_arguments_without_gpu():
+    lib = _lib.load()
+    # NULL pointers and bad shapes/dtypes are rejected before any HIP call
+    assert lib.lsq_w8_linear(None, 16, None, None, 0, None, 0, None, 16, 2, 1, 16, 16, None) == -1
+    assert lib.lsq_w4_linear(1 << 20, 8, 1 << 20, None, 1 << 20, 0, 128, None, 0, 1 << 20, 16, 2,
+                             1, 16, 16, None) == -2  # ldx < K
+    assert lib.lsq_w4_linear(1 << 20, 16, 1 << 20, None, 1 << 20, 0, 0, None, 0, 1 << 20, 16, 2,
+                             1, 16, 16, None) == -4  # group_size 0
+    assert lib.lsq_w4_linear(1 << 20, 16, 1 << 20, None, 1 << 20, 0, 16, None, 0, 1 << 20, 16, 7,
+                             1, 16, 16, None) == -3  # dtype 7
+    assert lib.lsq_w4_retile(1 << 20, 1 << 20, 16, 100, None) == -5  # K % 128 != 0
+    assert lib.lsq_w4_tiled_bytes(18944, 3584) == 18944 * 3584 // 2
+    assert lib.lsq_w4_tiled_bytes(17, 128) == 2 * 1024  # rows padded to 16
+    assert lib.lsq_w4_tiled_bytes(16, 100) == 0
+    for code in (-1, -2, -3, -4, -5, -6):
+        assert lib.lsq_status_string(code).startswith(b"lsq:")
+    with pytest.raises(_lib.LsqError, match="group_size"):
+        _lib.check(-4, "probe")

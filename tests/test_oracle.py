@@ -1,0 +1,261 @@
+"""Pins the CPU oracle (oracle/quant_oracle.py) before anything is checked against it.
+
+Every oracle function is checked against something other than its own formula:
+exact-rational golden vectors, torch's dtype casts and ops, hand-computed known answers,
+brute force over every q value / byte value, and mathematical special cases. A planted
+mistake (wrong nibble order, truncation instead of RNE, dropped round_T of the scale,
+a transposed operand, a missing bias) fails at least one test here.
+"""
+
+import os
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import quant_oracle as qo
+from oracle import torch_ref
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "quant_golden.npz")
+TORCH_DT = {"f32": torch.float32, "f16": torch.float16, "bf16": torch.bfloat16}
+
+
+# ----------------------------------------------------------------------------- rounding
+
+
+def test_round_bf16_matches_torch_on_boundaries():
+    rng = np.random.default_rng(0)
+    bits = np.concatenate([
+        rng.integers(0, 2**32, size=200000, dtype=np.uint64).astype(np.uint32),
+        # exact ties (low half = 0x8000) with even and odd kept lsb, and near-ties
+        (rng.integers(0, 2**16, size=5000, dtype=np.uint64).astype(np.uint32) << 16) | 0x8000,
+        (rng.integers(0, 2**16, size=5000, dtype=np.uint64).astype(np.uint32) << 16) | 0x7FFF,
+        (rng.integers(0, 2**16, size=5000, dtype=np.uint64).astype(np.uint32) << 16) | 0x8001,
+        np.array([0x7F7FFFFF, 0xFF7FFFFF, 0x00000001, 0x80000001, 0x007FFFFF, 0x7F800000,
+                  0xFF800000, 0x00000000, 0x80000000], dtype=np.uint32),
+    ])
+    f = bits.view(np.float32)
+    f = f[~np.isnan(f)]
+    ours = qo.round_bf16(f)
+    theirs = torch.from_numpy(f.copy()).to(torch.bfloat16).float().numpy()
+    assert np.array_equal(ours.view(np.uint32), theirs.view(np.uint32))
+
+
+def test_round_bf16_known_ties():
+    # 1 + 2^-8 is the exact midpoint of 1 and 1 + 2^-7: ties to the even mantissa (1.0)
+    assert qo.round_bf16(np.float32(1.0 + 2**-8))[()] == 1.0
+    # 1 + 3*2^-8 lies between 1 + 2^-7 (odd) and 1 + 2^-6 (even): rounds up
+    assert qo.round_bf16(np.float32(1.0 + 3 * 2**-8))[()] == np.float32(1.0 + 2**-6)
+    assert np.isnan(qo.round_bf16(np.float32("nan"))[()])
+    assert qo.round_bf16(np.float32(3.4e38))[()] == np.inf
+
+
+def test_round_f16_matches_torch():
+    rng = np.random.default_rng(1)
+    f = np.concatenate([rng.standard_normal(100000) * 100, rng.standard_normal(10000) * 1e-5]).astype(np.float32)
+    ours = qo.round_f16(f)
+    theirs = torch.from_numpy(f).to(torch.float16).float().numpy()
+    assert np.array_equal(ours, theirs)
+
+
+# ----------------------------------------------------------------------------- pack / unpack
+
+
+def test_pack_known_answer():
+    # byte j = (q[2j]+8) | (q[2j+1]+8) << 4; odd K pads the high nibble with 0
+    q = np.array([[-8, 7, 0, 1, -1]], dtype=np.int8)
+    assert qo.pack_int4(q).tolist() == [[0xF0, 0x98, 0x07]]
+
+
+def test_unpack_every_byte_value():
+    packed = np.arange(256, dtype=np.uint8).reshape(1, 256)
+    q = qo.unpack_int4(packed, 512)
+    b = np.arange(256)
+    assert np.array_equal(q[0, 0::2], (b % 16) - 8)
+    assert np.array_equal(q[0, 1::2], (b // 16) - 8)
+
+
+@pytest.mark.parametrize("k", [32, 33, 128, 1536])
+def test_pack_unpack_round_trip_and_torch(k):
+    # the reference's own regression widths (tests/test_quantized_loader.py:442)
+    rng = np.random.default_rng(k)
+    q = rng.integers(-8, 8, size=(64, k)).astype(np.int8)
+    p = qo.pack_int4(q)
+    assert p.shape == (64, (k + 1) // 2) and p.dtype == np.uint8
+    assert np.array_equal(qo.unpack_int4(p, k), q)
+    assert np.array_equal(torch_ref.unpack_int4(torch.from_numpy(p), k).numpy(), q)
+
+
+# ----------------------------------------------------------------------------- quantizers
+
+
+def test_quantize_int8_known_answer():
+    # max|w| = 254 -> scale 2; q = round(w / 2)
+    w = np.array([[254.0, -128.0, 0.0, 2.0, 5.2, -3.0]], dtype=np.float32)
+    q, s = qo.quantize_int8(w)
+    assert s[0, 0] == 2.0
+    assert q.tolist() == [[127, -64, 0, 1, 3, -2]]
+    p, s4 = qo.quantize_int4(np.array([[14.0, -6.0, 1.0, 0.0]], np.float32))
+    assert s4[0, 0] == 2.0
+    assert qo.unpack_int4(p, 4).tolist() == [[7, -3, 0, 0]]
+
+
+def test_quantize_round_half_even_ties():
+    # scale = 7/7 = 1 exactly; w = k + 0.5 are exact ties and must go to the even integer
+    w = np.array([[7.0, 0.5, 1.5, 2.5, -0.5, -1.5, -2.5, 3.5]], dtype=np.float32)
+    p, s = qo.quantize_int4(w)
+    assert s[0, 0] == 1.0
+    assert qo.unpack_int4(p, 8).tolist() == [[7, 0, 2, 2, 0, -2, -2, 4]]
+    w8 = np.array([[127.0, 0.5, 1.5, 2.5, -0.5, -1.5, -126.5, 125.5]], dtype=np.float32)
+    q8, s8 = qo.quantize_int8(w8)
+    assert s8[0, 0] == 1.0
+    assert q8.tolist() == [[127, 0, 2, 2, 0, -2, -126, 126]]
+
+
+def test_quantize_zero_row_clamps_scale():
+    q, s = qo.quantize_int8(np.zeros((2, 8), np.float32))
+    assert np.all(s == np.float32(1e-8)) and np.all(q == 0)
+
+
+def test_quantizers_match_torch_op_sequence():
+    g = torch.Generator().manual_seed(5)
+    w = torch.randn(64, 96, generator=g) * 0.05
+    q, s = qo.quantize_int8(w.numpy())
+    ts = torch.clamp(w.abs().max(dim=-1, keepdim=True)[0] / 127.0, min=1e-8)
+    tq = torch.clamp(torch.round(w / ts), -128, 127).to(torch.int8)
+    assert np.array_equal(q, tq.numpy()) and np.array_equal(s, ts.numpy())
+    p, s4 = qo.quantize_int4(w.numpy())
+    ts4 = torch.clamp(w.abs().max(dim=-1, keepdim=True)[0] / 7.0, min=1e-8)
+    tq4 = torch.clamp(torch.round(w / ts4), -8, 7).to(torch.int8)
+    assert np.array_equal(qo.unpack_int4(p, 96), tq4.numpy()) and np.array_equal(s4, ts4.numpy())
+
+
+def test_group_quantizer_reduces_to_per_channel():
+    rng = np.random.default_rng(3)
+    w = (rng.standard_normal((16, 256)) * 0.02).astype(np.float32)
+    p1, s1 = qo.quantize_int4(w, group_size=None)
+    p2, s2 = qo.quantize_int4(w, group_size=256, scale_dt="f32")
+    assert np.array_equal(p1, p2) and np.array_equal(s1, s2)
+    # a group quantizer on a matrix whose groups are row-constant copies is per-channel
+    wg = np.tile(w[:, :64], (1, 4))
+    pg, sg = qo.quantize_int4(wg, group_size=64, scale_dt="f32")
+    assert np.all(sg == sg[:, :1])
+    pc, sc = qo.quantize_int4(wg)
+    assert np.array_equal(pg, pc)
+
+
+# ----------------------------------------------------------------------------- dequant
+
+
+@pytest.mark.parametrize("dt", ["f32", "f16", "bf16"])
+def test_dequant_int8_exhaustive_vs_torch(dt):
+    rng = np.random.default_rng(11)
+    q = np.tile(np.arange(-128, 128, dtype=np.int8), (300, 1))
+    s = rng.uniform(1e-8, 0.5, size=(300, 1)).astype(np.float32)
+    ours = qo.dequant_int8(q, s, dt)
+    theirs = torch_ref.dequant_int8(torch.from_numpy(q), torch.from_numpy(s), TORCH_DT[dt]).float().numpy()
+    assert np.array_equal(ours.view(np.uint32), theirs.view(np.uint32))
+
+
+@pytest.mark.parametrize("dt", ["f32", "f16", "bf16"])
+@pytest.mark.parametrize("scale_dt", ["f32", "bf16"])
+def test_dequant_int4_grouped_exhaustive_vs_torch(dt, scale_dt):
+    rng = np.random.default_rng(12)
+    k, g = 64, 16
+    q = np.tile(np.arange(-8, 8, dtype=np.int8), (200, k // 16))
+    p = qo.pack_int4(q)
+    s = qo.round_to(rng.uniform(0.001, 0.05, size=(200, k // g)), scale_dt)
+    ours = qo.dequant_int4(p, s, k, g, dt)
+    ts = torch.from_numpy(s)
+    if scale_dt == "bf16":
+        ts = ts.to(torch.bfloat16)
+    theirs = torch_ref.dequant_int4(torch.from_numpy(p), ts, k, g, TORCH_DT[dt]).float().numpy()
+    assert np.array_equal(ours.view(np.uint32), theirs.view(np.uint32))
+
+
+def test_dequant_scale_is_rounded_before_the_product():
+    # a scale that is not bf16-representable: round_bf16(q*s) != round_bf16(q*round_bf16(s))
+    s = np.array([[np.float32(0.0123456)]], np.float32)
+    q = np.arange(-128, 128, dtype=np.int8).reshape(1, -1)
+    ours = qo.dequant_int8(q, s, "bf16")
+    wrong = qo.round_bf16(q.astype(np.float32) * s)
+    assert not np.array_equal(ours, wrong)
+    assert np.array_equal(ours, qo.round_bf16(q.astype(np.float32) * qo.round_bf16(s)))
+
+
+def test_group_dequant_reduces_to_per_channel():
+    rng = np.random.default_rng(13)
+    q = rng.integers(-8, 8, size=(8, 256)).astype(np.int8)
+    p = qo.pack_int4(q)
+    s = rng.uniform(0.001, 0.05, size=(8, 1)).astype(np.float32)
+    a = qo.dequant_int4(p, s, 256, None, "bf16")
+    b = qo.dequant_int4(p, np.repeat(s, 2, axis=1), 256, 128, "bf16")
+    assert np.array_equal(a, b)
+
+
+# ----------------------------------------------------------------------------- linear
+
+
+def test_linear_closed_forms():
+    rng = np.random.default_rng(14)
+    w = qo.round_bf16(rng.standard_normal((24, 40)).astype(np.float32))
+    # one-hot rows of x pick out columns of W^T exactly
+    x = np.eye(40, dtype=np.float32)[:5]
+    y = qo.linear(x, w, None, "f32")
+    assert np.array_equal(y, w[:, :5].T)
+    # identity weight returns x (+ bias); bias is rounded to T first
+    xi = qo.round_bf16(rng.standard_normal((3, 40)).astype(np.float32))
+    b = np.full(40, 0.1, np.float32)
+    y2 = qo.linear(xi, np.eye(40, dtype=np.float32), b, "bf16")
+    assert np.array_equal(y2, qo.round_bf16(xi.astype(np.float64) + float(qo.round_bf16(b)[0])))
+
+
+def test_linear_vs_torch_cpu_gemm():
+    g = torch.Generator().manual_seed(15)
+    x = torch.randn(7, 96, generator=g)
+    w = torch.randn(33, 96, generator=g)
+    b = torch.randn(33, generator=g)
+    ours = qo.linear(x.numpy(), w.numpy(), b.numpy(), "f32")
+    theirs = F.linear(x.double(), w.double(), b.double()).float().numpy()
+    assert qo.rel_err(ours, theirs) < 1e-6
+    # a transposed operand is caught
+    bad = qo.linear(x.numpy(), w.numpy()[::-1], b.numpy(), "f32")
+    assert qo.rel_err(bad, theirs) > 1e-2
+
+
+def test_rel_err_convention():
+    assert qo.rel_err([1.0, 2.0], [1.0, 2.0]) == 0.0
+    assert qo.rel_err([1.0, 2.1], [1.0, 2.0]) == pytest.approx(0.05)
+
+
+# ----------------------------------------------------------------------------- golden
+
+
+def _golden():
+    return np.load(GOLDEN, allow_pickle=False)
+
+
+GOLDEN_CASES = ["int8_pc", "int4_pc_oddk", "int4_g16", "int4_g128", "int8_k256", "int4_pc_k128"]
+
+
+@pytest.mark.parametrize("name", GOLDEN_CASES)
+@pytest.mark.parametrize("dt", ["f32", "f16", "bf16"])
+def test_oracle_matches_exact_golden(name, dt):
+    z = _golden()
+    n, k, g = (int(v) for v in z[f"{name}/meta"])
+    g = None if g < 0 else g
+    q = z[f"{name}/q"]
+    s = z[f"{name}/scale"]
+    if name.startswith("int8"):
+        w = qo.dequant_int8(q, s, dt)
+    else:
+        w = qo.dequant_int4(qo.pack_int4(q), s, k, g, dt)
+    assert np.array_equal(w.view(np.uint32), z[f"{name}/w_{dt}"].view(np.uint32))
+    x_t = qo.round_to(z[f"{name}/x"], dt)
+    assert np.array_equal(x_t, z[f"{name}/x_{dt}"])
+    y = qo.linear_f64(x_t, w, z[f"{name}/bias"], dt)
+    assert np.max(np.abs(y - z[f"{name}/y_{dt}_exact"])) < 1e-9
+    yr = qo.linear(x_t, w, z[f"{name}/bias"], dt)
+    # float64 sums can straddle a rounding boundary of T only at exact-ties; none here
+    assert np.array_equal(yr, z[f"{name}/y_{dt}"])
