@@ -374,7 +374,10 @@ static int launch_generic(bool w4, const void* x, int64_t ldx, const void* w, co
 static int check_common(const void* x, int64_t ldx, const void* w, const void* scale, void* y,
                         int64_t ldy, int dtype, int bias_dt, const void* bias, int64_t M,
                         int64_t N, int64_t K) {
-  if (!x || !w || !scale || !y) return LSQ_E_NULL;
+  // An empty x or y (M, N or K zero) may come with a NULL data pointer, as torch gives
+  // for zero-element tensors; such a pointer is never dereferenced.
+  if (!w || !scale) return LSQ_E_NULL;
+  if ((!x && M > 0 && K > 0) || (!y && M > 0 && N > 0)) return LSQ_E_NULL;
   if (M < 0 || N < 0 || K < 0 || ldx < K || ldy < N) return LSQ_E_SHAPE;
   if (N > INT32_MAX / 2 || K > INT32_MAX / 2 || M > INT32_MAX / 2) return LSQ_E_SHAPE;
   if (dtype != LSQ_F32 && dtype != LSQ_F16 && dtype != LSQ_BF16) return LSQ_E_DTYPE;

@@ -236,6 +236,13 @@ def test_library_rejects_bad_arguments_without_gpu():
     assert lib.lsq_w4_linear(1 << 20, 16, 1 << 20, None, 1 << 20, 0, 16, None, 0, 1 << 20, 16, 7,
                              1, 16, 16, None) == -3  # dtype 7
     assert lib.lsq_w4_retile(1 << 20, 1 << 20, 16, 100, None) == -5  # K % 128 != 0
+    # an empty batch (M = 0) may carry NULL x / y, as torch gives for zero-element tensors
+    assert lib.lsq_w4_linear(None, 16, 1 << 20, None, 1 << 20, 0, 16, None, 0, None, 16, 2,
+                             0, 16, 16, None) == 0
+    assert lib.lsq_w8_linear(None, 16, 1 << 20, 1 << 20, 0, None, 0, None, 16, 2, 0, 16, 16,
+                             None) == 0
+    assert lib.lsq_w8_linear(None, 16, 1 << 20, 1 << 20, 0, None, 0, 1 << 20, 16, 2, 1, 16, 16,
+                             None) == -1  # M > 0 needs x
     assert lib.lsq_w4_tiled_bytes(18944, 3584) == 18944 * 3584 // 2
     assert lib.lsq_w4_tiled_bytes(17, 128) == 2 * 1024  # rows padded to 16
     assert lib.lsq_w4_tiled_bytes(16, 100) == 0
