@@ -41,7 +41,7 @@ extern "C" {
 #define LSQ_E_SHAPE (-2)       /* M, N or K out of range, or a leading dim < row length */
 #define LSQ_E_DTYPE (-3)       /* unsupported dtype code */
 #define LSQ_E_GROUP (-4)       /* group_size < 1 */
-#define LSQ_E_LAYOUT (-5)      /* tiled INT4 layout needs K % 128 == 0 */
+#define LSQ_E_LAYOUT (-5)      /* tiled layouts need K % 128 == 0 */
 #define LSQ_E_ALIGN (-6)       /* pointer or leading dim not aligned as the kernel needs */
 
 /* Library version (major*10000 + minor*100 + patch). No reference counterpart. */
@@ -85,14 +85,28 @@ int lsq_w4_retile(const uint8_t* weight_packed, uint8_t* tiled, int64_t N, int64
 int lsq_w4_untile(const uint8_t* tiled, uint8_t* weight_packed, int64_t N, int64_t K,
                   void* stream);
 
+/* Bytes of the tiled INT8 layout for an [N, K] weight (0 if K % 128 != 0).
+ * No reference counterpart: the reference keeps only the row-major weight_q. */
+int64_t lsq_w8_tiled_bytes(int64_t N, int64_t K);
+
+/* Re-tile row-major int8 weights into the decode layout: 16-row x 128-column tiles of
+ * 2048 contiguous bytes (two 1 KB halves, each read by one 64-lane wavefront load with
+ * 16 bytes per lane). Rows past N are zero-filled. Derived from weight_q as produced by
+ * src/kernels/quantization.py:72-78; weight_q is left untouched. */
+int lsq_w8_retile(const int8_t* weight_q, int8_t* tiled, int64_t N, int64_t K, void* stream);
+
+/* Inverse of lsq_w8_retile (for round-trip checks). */
+int lsq_w8_untile(const int8_t* tiled, int8_t* weight_q, int64_t N, int64_t K, void* stream);
+
 /* y[M, N] = x[M, K] @ dequant(W8)^T + round_T(bias).
  * Replaces QuantizedLinear.forward for quant_type "int8"
  * (src/kernels/quantization.py:129-141). x and y have dtype `dtype`, row strides ldx and
  * ldy (elements); bias is NULL or [N] of bias_dtype (rounded to `dtype` first, as
- * quantization.py:135-140 casts it). */
-int lsq_w8_linear(const void* x, int64_t ldx, const int8_t* weight_q, const void* scale,
-                  int scale_dtype, const void* bias, int bias_dtype, void* y, int64_t ldy,
-                  int dtype, int64_t M, int64_t N, int64_t K, void* stream);
+ * quantization.py:135-140 casts it). `tiled` is NULL or the output of lsq_w8_retile for
+ * the same weights; when given, the decode kernels stream it instead of weight_q. */
+int lsq_w8_linear(const void* x, int64_t ldx, const int8_t* weight_q, const int8_t* tiled,
+                  const void* scale, int scale_dtype, const void* bias, int bias_dtype, void* y,
+                  int64_t ldy, int dtype, int64_t M, int64_t N, int64_t K, void* stream);
 
 /* y[M, N] = x[M, K] @ dequant(W4)^T + round_T(bias).
  * Replaces QuantizedLinear.forward for quant_type "int4"

@@ -32,9 +32,12 @@ SIGNATURES = {
     "lsq_w4_tiled_bytes": (_i64, [_i64, _i64]),
     "lsq_w4_retile": (_int, [_vp, _vp, _i64, _i64, _vp]),
     "lsq_w4_untile": (_int, [_vp, _vp, _i64, _i64, _vp]),
+    "lsq_w8_tiled_bytes": (_i64, [_i64, _i64]),
+    "lsq_w8_retile": (_int, [_vp, _vp, _i64, _i64, _vp]),
+    "lsq_w8_untile": (_int, [_vp, _vp, _i64, _i64, _vp]),
     "lsq_w8_linear": (
         _int,
-        [_vp, _i64, _vp, _vp, _int, _vp, _int, _vp, _i64, _int, _i64, _i64, _i64, _vp],
+        [_vp, _i64, _vp, _vp, _vp, _int, _vp, _int, _vp, _i64, _int, _i64, _i64, _i64, _vp],
     ),
     "lsq_w4_linear": (
         _int,

@@ -1,0 +1,39 @@
+// Decode-shaped (small M) weight-only GEMV kernels: declarations shared with the
+// dispatcher in lsq_linear.hip.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace lsq {
+
+// How the weight operand is stored in HBM.
+enum WeightKind : int {
+  kW8 = 0,       // int8 [N, K] row-major (QuantizedLinear.weight_q)
+  kW4Tiled = 1,  // INT4 re-tiled by lsq_w4_retile (16x128 tiles of 1 KB)
+  kW4Canon = 2,  // INT4 canonical packed [N, K/2] (QuantizedLinear.weight_packed)
+  kW8Tiled = 3,  // int8 re-tiled by lsq_w8_retile (16x128 tiles of 2 KB)
+};
+
+struct LinearArgs {
+  const void* x;       // activations [M, K], row stride ldx (elements)
+  int64_t ldx;
+  const uint8_t* w;    // weights, layout per WeightKind
+  const void* scale;   // [N, ngroups] (per-channel: ngroups == 1)
+  int scale_dt;
+  const void* bias;    // [N] or nullptr
+  int bias_dt;
+  void* y;             // output [M, N], row stride ldy (elements)
+  int64_t ldy;
+  int64_t M, N, K;
+  int64_t group;       // columns per scale group (== K for per-channel)
+  int64_t ngroups;
+};
+
+// Launches the LDS-staged decode kernel when the shape fits it (M <= 16, K % 128 == 0,
+// group % 128 == 0, activations small enough to stage in LDS). Returns LSQ_E_LAYOUT
+// without launching anything when it does not fit.
+template <int DT>
+int launch_decode(int kind, const LinearArgs& a, hipStream_t s);
+
+}  // namespace lsq

@@ -1,0 +1,619 @@
+// Decode-shaped weight-only GEMV, M <= 16 tokens (gfx950).
+//
+// GPU form of QuantizedLinear.forward (src/kernels/quantization.py:129-141) for the
+// decode step, where the reference dequantizes the whole [N, K] weight and calls
+// F.linear. Here the weights are streamed from HBM exactly once and never materialized.
+//
+// Work split. Output rows are cut into 16-row tiles (the N side of one
+// v_mfma_f32_16x16x32 MFMA) and K into 128-column tiles. The weights are read from the
+// tiled layouts (lsq_internal.h: one contiguous 1 KB per wavefront load, each wave
+// streaming a contiguous run of tiles, which HBM serves near its streaming rate) or, for
+// callers without a tiled copy, from the canonical row-major layouts. A workgroup owns RG x RT row
+// tiles and all of K; its RG x KS waves each take RT row tiles and one of KS contiguous
+// K slices. Partial sums of the KS slices are added through LDS at the end, in slice
+// order, so results do not depend on timing.
+//
+// Prologue. Before the first MFMA each workgroup stages, once, the activations
+// x[0:M, 0:K] into LDS (row stride K + 8 elements, already in the column order the
+// weight unpack produces, plus one all-zero row) and per (128-column tile, token) sums of
+// x, used to remove the INT4 nibble bias. The per-channel scale and bias of each lane's
+// rows are loaded into registers and decoded only in the epilogue. The first D weight
+// steps are issued before the activation staging completes, so their HBM latency
+// overlaps it; after the prologue only the weight stream (and, for grouped INT4, the
+// group scales riding with it) uses the in-order vmcnt counter.
+//
+// Main loop. Each lane streams 16 bytes (INT4: 32 weights) or 2 x 16 bytes (INT8: 32
+// weights) per (row tile, k tile) with non-temporal loads, D steps ahead of use, and
+// turns them into the B operand of 4 MFMAs in registers:
+//   * INT8: v_cvt_f32_i32 with SDWA byte sign-extension, then v_cvt_pk_bf16_f32 (fp16:
+//     v_cvt_pkrtz_f16_f32); integers |q| <= 128 are exact in both types.
+//   * INT4: a nibble u = q + 8 OR-ed into the mantissa of 128.0 (bf16 0x4300; fp16
+//     1024.0, 0x6400) is exactly 128 + u; the constant part, off = 136 (fp16: 1032),
+//     is removed per 128-column tile as s * (acc - off * sum(x)), or once at the end for
+//     per-channel scales.
+// The activation (A operand) comes from LDS; lanes of token rows >= M read an all-zero
+// row (all such lanes of a quad read the same address, an LDS broadcast).
+//
+// Numerics: every weight product q * x is exact in the fp32 MFMA accumulator; the scale
+// is applied in fp32 per group (or per row), then the bias rounded to T, then one
+// rounding to T. The reference rounds each dequantized weight round_T(q * s) first and
+// then sums in its BLAS order; the two differ by bf16 rounding of the weights, far
+// inside the 1e-2 relative contract.
+
+#include "lsq_common.h"
+#include "lsq_internal.h"
+#include "lsq_decode.h"
+
+#include <atomic>
+#include <type_traits>
+#include <cstdlib>
+#include <cstring>
+
+namespace lsq {
+namespace {
+
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+template <int DT> struct Mma;
+
+template <> struct Mma<LSQ_BF16> {
+  static constexpr uint32_t kMagic = 0x43004300u;  // bf16 pair (128, 128)
+  static constexpr float kOff4 = 136.f;            // 128 + the nibble bias 8
+  static __device__ __forceinline__ f32x4 mma(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                    __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ uint32_t pack2(float a, float b) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){a, b}, bf16x2));
+  }
+  static __device__ __forceinline__ float lo(uint32_t v) { return __uint_as_float(v << 16); }
+  static __device__ __forceinline__ float hi(uint32_t v) { return __uint_as_float(v & 0xFFFF0000u); }
+};
+
+template <> struct Mma<LSQ_F16> {
+  static constexpr uint32_t kMagic = 0x64006400u;  // fp16 pair (1024, 1024)
+  static constexpr float kOff4 = 1032.f;           // 1024 + the nibble bias 8
+  static __device__ __forceinline__ f32x4 mma(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                   __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+  // Round-toward-zero is exact here: the inputs are integers with |v| <= 128.
+  static __device__ __forceinline__ uint32_t pack2(float a, float b) {
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(a, b));
+  }
+  static __device__ __forceinline__ float lo(uint32_t v) { return f16_to_f32(v & 0xFFFFu); }
+  static __device__ __forceinline__ float hi(uint32_t v) { return f16_to_f32(v >> 16); }
+};
+
+// 8 nibbles of one dword -> B operand of one MFMA: pair j = (nibble j, nibble j + 4),
+// each as the exact value 128 + u (bf16) / 1024 + u (fp16). `mask` = 0x000F000F and
+// `magic` = Mma<DT>::kMagic are passed in registers (see the main loop).
+__device__ __forceinline__ u32x4 unpack_w4(uint32_t w, uint32_t mask, uint32_t magic) {
+  u32x4 b;
+  b[0] = (w & mask) | magic;
+  b[1] = ((w >> 4) & mask) | magic;
+  b[2] = ((w >> 8) & mask) | magic;
+  b[3] = ((w >> 12) & mask) | magic;
+  return b;
+}
+
+// 8 signed bytes (two dwords, column order) -> B operand, exact.
+template <int DT>
+__device__ __forceinline__ u32x4 convert_w8(uint32_t w0, uint32_t w1) {
+  u32x4 b;
+  b[0] = Mma<DT>::pack2(static_cast<float>(static_cast<int8_t>(w0)),
+                        static_cast<float>(static_cast<int8_t>(w0 >> 8)));
+  b[1] = Mma<DT>::pack2(static_cast<float>(static_cast<int8_t>(w0 >> 16)),
+                        static_cast<float>(static_cast<int8_t>(w0 >> 24)));
+  b[2] = Mma<DT>::pack2(static_cast<float>(static_cast<int8_t>(w1)),
+                        static_cast<float>(static_cast<int8_t>(w1 >> 8)));
+  b[3] = Mma<DT>::pack2(static_cast<float>(static_cast<int8_t>(w1 >> 16)),
+                        static_cast<float>(static_cast<int8_t>(w1 >> 24)));
+  return b;
+}
+
+// 8 activations (x0..x7) reordered to (x0,x4,x1,x5,x2,x6,x3,x7), the order unpack_w4
+// yields for a canonical dword, where nibble p is column p.
+__device__ __forceinline__ u32x4 permute_canon(u32x4 a) {
+  u32x4 r;
+  r[0] = __builtin_amdgcn_perm(a[2], a[0], 0x05040100u);
+  r[1] = __builtin_amdgcn_perm(a[2], a[0], 0x07060302u);
+  r[2] = __builtin_amdgcn_perm(a[3], a[1], 0x05040100u);
+  r[3] = __builtin_amdgcn_perm(a[3], a[1], 0x07060302u);
+  return r;
+}
+
+// Column (within a 128-column k tile) of the first of the 8 activations lane-quad q
+// feeds to MFMA d. INT4 and tiled INT8: lane quad q owns columns [32q, 32q + 32), MFMA d
+// takes columns 32q + 8d .. +7. Canonical INT8: the two 16-byte loads cover columns
+// [16q, 16q + 16) and [64 + 16q, 64 + 16q + 16).
+template <int KIND>
+__device__ __forceinline__ int a_col(int q, int d) {
+  return KIND == kW8 ? (d >> 1) * 64 + q * 16 + (d & 1) * 8 : q * 32 + d * 8;
+}
+
+constexpr int kXB = 8;  // activation chunks (16 B) per thread per batch, large-M staging
+constexpr int kSB = 4;  // scale dwords in flight per thread while staging
+
+__host__ __device__ constexpr int64_t align16(int64_t v) { return (v + 15) & ~int64_t(15); }
+
+// LDS layout, shared by kernel and host: staged activations (M rows + one zero row),
+// per-(k tile, token) activation sums, per-token totals, the workgroup's scales and bias
+// as fp32 (already rounded to the activation type), cross-slice partial sums.
+struct DecodeLds {
+  int64_t xs, xsum, xtot, ss, sb, red, total;
+};
+
+__host__ __device__ inline DecodeLds decode_lds(int64_t M, int64_t K, int rows, int64_t ngs,
+                                                int red_floats) {
+  DecodeLds l;
+  const int64_t nkt = K / kTileK;
+  l.xs = 0;
+  l.xsum = align16((M + 1) * (K + 8) * 2);
+  l.xtot = l.xsum + nkt * 16 * 4;
+  l.ss = l.xtot + 16 * 4;
+  l.sb = l.ss + align16(rows * ngs * 4);
+  l.red = l.sb + align16(rows * 4);
+  l.total = l.red + static_cast<int64_t>(red_floats) * 4;
+  return l;
+}
+
+// ---- buffer loads. Every global read of the kernel goes through a buffer descriptor
+// bounding a region the workgroup owns; a load at an offset past the bound returns zero
+// without touching memory. Out-of-range rows, activation chunks past the end and the
+// pipeline's refills past the end of a slice therefore cost no memory traffic and need
+// no clamping or branches.
+using rsrc_t = __amdgpu_buffer_rsrc_t;
+constexpr int kRsrcWord3 = 0x00020000;  // gfx9-family descriptor word 3: raw 32-bit dwords
+constexpr uint32_t kOOB = 0x80000000u;  // past every descriptor's range
+constexpr int kNT = 2;                  // cache policy: non-temporal (weights, read once)
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, kRsrcWord3);
+}
+
+template <int AUX>
+__device__ __forceinline__ u32x4 bload16(rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, AUX);
+}
+
+__device__ __forceinline__ uint32_t bload4(rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+}
+
+// Workgroup barrier that orders LDS only: the compiler's __syncthreads() also waits for
+// every outstanding global load, which would drain the weight pipeline.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// fp32 value of element `half` (0 or 1) of a dword of 16-bit floats, or of an fp32 dword.
+__device__ __forceinline__ float dword_elem(uint32_t w, int half, int dt) {
+  if (dt == LSQ_F32) return __uint_as_float(w);
+  const uint32_t h = half ? (w >> 16) : (w & 0xFFFFu);
+  return dt == LSQ_BF16 ? __uint_as_float(h << 16) : f16_to_f32(static_cast<uint16_t>(h));
+}
+
+// Decode `nd` staged dwords (kSB per thread in `v`, dword index u * NT + tid + t0) of a
+// float array with dtype `dt` holding `nelem` elements into dst[] as round_T fp32.
+template <int DT, int NT>
+__device__ __forceinline__ void put_floats(const uint32_t (&v)[kSB], int t0, int tid, int dt,
+                                           int nelem, float* dst) {
+#pragma unroll
+  for (int u = 0; u < kSB; ++u) {
+    const int t = t0 + u * NT + tid;
+    if (dt == LSQ_F32) {
+      if (t < nelem) dst[t] = Act<DT>::round(dword_elem(v[u], 0, dt));
+    } else {
+      if (2 * t < nelem) dst[2 * t] = Act<DT>::round(dword_elem(v[u], 0, dt));
+      if (2 * t + 1 < nelem) dst[2 * t + 1] = Act<DT>::round(dword_elem(v[u], 1, dt));
+    }
+  }
+}
+
+template <int DT, int KIND, int RT, int RG, int KS, int D, bool GROUPED>
+__global__ void __launch_bounds__(64 * RG * KS) decode_kernel(LinearArgs p) {
+  constexpr int NT = 64 * RG * KS;
+  constexpr bool W4 = KIND == kW4Tiled || KIND == kW4Canon;
+  constexpr bool TILED = KIND == kW4Tiled || KIND == kW8Tiled;
+  constexpr int LPT = W4 ? 1 : 2;  // 16-byte weight loads per lane per (row tile, k tile)
+  constexpr int kTileB = W4 ? kTileBytes : kTileBytes8;
+  // bytes between consecutive k tiles of one lane, and between a lane's two INT8 loads
+  constexpr int kStride = TILED ? kTileB : (W4 ? kTileK / 2 : kTileK);
+  constexpr int kHalf = KIND == kW8Tiled ? kTileBytes8 / 2 : 64;
+  constexpr int ROWS = RG * RT * kTileN;
+  constexpr int RED = KS > 1 ? (KS - 1) * RG * RT * 4 * 64 : 0;
+  extern __shared__ __align__(16) unsigned char smem[];
+  using S = typename Act<DT>::storage;
+
+  const int M = static_cast<int>(p.M), N = static_cast<int>(p.N), K = static_cast<int>(p.K);
+  const int nkt = K / kTileK;
+  const int nrt = (N + kTileN - 1) / kTileN;
+  const int ng = static_cast<int>(p.ngroups);
+  const int ngs = GROUPED ? ng : 1;  // scale columns per row
+  const int gtiles = static_cast<int>(p.group / kTileK);
+  const int ldxs = K + 8;
+
+  const DecodeLds L = decode_lds(M, K, ROWS, ngs, RED);
+  uint16_t* xs = reinterpret_cast<uint16_t*>(smem + L.xs);
+  float* xsum = reinterpret_cast<float*>(smem + L.xsum);
+  float* xtot = reinterpret_cast<float*>(smem + L.xtot);
+  float* ss = reinterpret_cast<float*>(smem + L.ss);
+  float* sb = reinterpret_cast<float*>(smem + L.sb);
+  float* red = reinterpret_cast<float*>(smem + L.red);
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform per wave
+  const int rg = wid % RG;
+  const int ks = wid / RG;
+  const int r = lane & 15;
+  const int q = lane >> 4;
+  const int rt_wg = blockIdx.x * RG * RT;  // first row tile of the workgroup
+  const int row0 = rt_wg * kTileN;
+  const int rows_valid = min(ROWS, N - row0);
+  const int rtl = rg * RT;  // first row tile of this wave, counted within the workgroup
+  const int k_lo = ks * nkt / KS;
+  const int nsteps = (ks + 1) * nkt / KS - k_lo;
+
+  // ---- descriptors over what this workgroup reads
+  const int es_s = p.scale_dt == LSQ_F32 ? 4 : 2;
+  const int es_b = p.bias_dt == LSQ_F32 ? 4 : 2;
+  const rsrc_t rx = make_rsrc(p.x, static_cast<uint32_t>(((M - 1) * p.ldx + K) * 2));
+  const uint8_t* wbase;
+  uint32_t wbytes;
+  if (TILED) {
+    wbase = p.w + static_cast<int64_t>(rt_wg) * nkt * kTileB;
+    wbytes = static_cast<uint32_t>(min(RG * RT, nrt - rt_wg) * nkt * kTileB);
+  } else {
+    const int row_bytes = W4 ? K / 2 : K;
+    wbase = p.w + static_cast<int64_t>(row0) * row_bytes;
+    wbytes = static_cast<uint32_t>(rows_valid * row_bytes);
+  }
+  const rsrc_t rw = make_rsrc(wbase, wbytes);
+  const int nsc = rows_valid * ngs;  // scale elements of this workgroup
+  const int nsd = (nsc * es_s + 3) / 4;
+  // The dword holding the last 16-bit element may extend 2 bytes past the array; an
+  // aligned dword never crosses a page, so reading it is always safe.
+  const rsrc_t rs = make_rsrc(static_cast<const uint8_t*>(p.scale) +
+                                  static_cast<int64_t>(row0) * ngs * es_s,
+                              static_cast<uint32_t>(nsd * 4));
+  const int nbd = p.bias ? (rows_valid * es_b + 3) / 4 : 0;
+  const rsrc_t rb = make_rsrc(p.bias ? static_cast<const uint8_t*>(p.bias) +
+                                           static_cast<int64_t>(row0) * es_b
+                                     : static_cast<const uint8_t*>(p.scale),
+                              static_cast<uint32_t>(nbd * 4));
+
+  // ---- prologue loads, in the order their data is needed: activations, scales, bias,
+  // then the first D weight steps.
+  const int K8 = K / 8;
+  const int nchunks = M * K8;
+  auto x_off = [&](int c) -> uint32_t {
+    const int m = c / K8;
+    return c < nchunks ? static_cast<uint32_t>((m * p.ldx + (c - m * K8) * 8) * 2) : kOOB;
+  };
+  // First batch: XS chunks per thread, 2048 chunks per workgroup (M * K / 8 <= 2048 covers
+  // M <= 4 at K = 4096); larger inputs take the staging path before the weight stream.
+  constexpr int XS = NT >= 2048 ? 1 : 2048 / NT;
+  u32x4 xv[XS];
+#pragma unroll
+  for (int u = 0; u < XS; ++u) xv[u] = bload16<0>(rx, x_off(u * NT + tid));
+  uint32_t sv[kSB];
+#pragma unroll
+  for (int u = 0; u < kSB; ++u) {
+    const int t = u * NT + tid;
+    sv[u] = bload4(rs, t < nsd ? t * 4 : kOOB);
+  }
+  const uint32_t bv = bload4(rb, tid < nbd ? tid * 4 : kOOB);  // ROWS * 4 bytes <= 4 * NT
+  // ---- activations -> LDS (in the unpack's column order) and per-(tile, token) sums
+  auto put_x = [&](const auto& v, int c0, auto nb) {
+#pragma unroll
+    for (int u = 0; u < decltype(nb)::value; ++u) {
+      if (c0 + u * NT >= nchunks) break;  // uniform
+      const int c = c0 + u * NT + tid;
+      const int m = c / K8;
+      const int c8 = c - m * K8;
+      float sum = 0.f;
+      if (c < nchunks) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sum += Mma<DT>::lo(v[u][e]) + Mma<DT>::hi(v[u][e]);
+        *reinterpret_cast<u32x4*>(xs + m * ldxs + c8 * 8) =
+            KIND == kW4Canon ? permute_canon(v[u]) : v[u];
+      }
+      // 16 consecutive lanes hold the 16 chunks of one (token, k tile); all valid or none.
+      sum += __shfl_xor(sum, 1, 64);
+      sum += __shfl_xor(sum, 2, 64);
+      sum += __shfl_xor(sum, 4, 64);
+      sum += __shfl_xor(sum, 8, 64);
+      if (W4 && c < nchunks && (lane & 15) == 0) xsum[(c8 / 16) * 16 + m] = sum;
+    }
+  };
+  // Staging of what the prologue loaded. A workgroup with more activations or scales
+  // than one batch of loads (many tokens, or many scale groups) stages everything before
+  // issuing any weight load; the common case stages after, so that code between the
+  // weight issue and the main loop is straight-line and the compiler waits precisely.
+  auto stage_first = [&]() {
+    put_x(xv, 0, std::integral_constant<int, XS>());
+    put_floats<DT, NT>(sv, 0, tid, p.scale_dt, nsc, ss);
+    if (p.bias && tid < nbd) {
+      if (es_b == 4) {
+        sb[tid] = Act<DT>::round(dword_elem(bv, 0, LSQ_F32));
+      } else {
+        if (2 * tid < rows_valid) sb[2 * tid] = Act<DT>::round(dword_elem(bv, 0, p.bias_dt));
+        if (2 * tid + 1 < rows_valid) sb[2 * tid + 1] = Act<DT>::round(dword_elem(bv, 1, p.bias_dt));
+      }
+    }
+  };
+  const bool big = nchunks > NT * XS || nsd > NT * kSB;  // uniform
+  if (big) {
+    stage_first();
+    for (int c0 = NT * XS; c0 < nchunks; c0 += NT * kXB) {
+      u32x4 xb[kXB];
+#pragma unroll
+      for (int u = 0; u < kXB; ++u) xb[u] = bload16<0>(rx, x_off(c0 + u * NT + tid));
+      put_x(xb, c0, std::integral_constant<int, kXB>());
+    }
+    for (int t0 = NT * kSB; t0 < nsd; t0 += NT * kSB) {
+#pragma unroll
+      for (int u = 0; u < kSB; ++u) {
+        const int t = t0 + u * NT + tid;
+        sv[u] = bload4(rs, t < nsd ? t * 4 : kOOB);
+      }
+      put_floats<DT, NT>(sv, t0, tid, p.scale_dt, nsc, ss);
+    }
+  }
+  // Keep the scheduler from moving any of the loads above below the weight stream:
+  // their consumers then wait only for them, not for the weights.
+  __builtin_amdgcn_sched_barrier(0);
+
+  // Weight stream: a ring of D k-tile steps per wave; refills past the end of the slice
+  // are out-of-range loads (no memory traffic), so every load is unconditional and the
+  // compiler waits for exactly the step being consumed while D - 1 stay in flight.
+  u32x4 wbuf[D][RT][LPT];
+  auto issue = [&](u32x4 (&wv)[RT][LPT], int st) {
+    const int kt = k_lo + st;
+    const bool real = st < nsteps;
+#pragma unroll
+    for (int i = 0; i < RT; ++i) {
+      const int lt = rtl + i;
+      const uint32_t off = TILED ? static_cast<uint32_t>((lt * nkt + kt) * kTileB + lane * 16)
+                                 : static_cast<uint32_t>((lt * kTileN + r) * (W4 ? K / 2 : K) +
+                                                         kt * kStride + q * 16);
+      wv[i][0] = bload16<kNT>(rw, real ? off : kOOB);
+      if (LPT == 2) wv[i][LPT - 1] = bload16<kNT>(rw, real ? off + kHalf : kOOB);
+    }
+  };
+#pragma unroll
+  for (int s = 0; s < D; ++s) issue(wbuf[s], s);
+
+  if (!big) stage_first();
+  for (int c = tid; c < K8; c += NT)  // row M: zeros, read by lanes of token rows >= M
+    *reinterpret_cast<u32x4*>(xs + M * ldxs + c * 8) = u32x4{0u, 0u, 0u, 0u};
+  lds_barrier();
+  if (W4 && !GROUPED) {
+    if (tid < 16) {
+      float t = 0.f;
+      if (tid < M)
+        for (int kt = 0; kt < nkt; ++kt) t += xsum[kt * 16 + tid];
+      xtot[tid] = t;
+    }
+    lds_barrier();
+  }
+
+  // ---- main loop
+  f32x4 acc[RT];
+#pragma unroll
+  for (int i = 0; i < RT; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const uint16_t* xrow = xs + min(r, M) * ldxs;  // token rows >= M read the zero row
+  // Constants of the INT4 unpack in registers, so it selects v_and_or_b32 (VOP3 has no
+  // literal operands on gfx9).
+  uint32_t nib_mask, magic;
+  asm volatile("v_mov_b32 %0, 0x000f000f" : "=v"(nib_mask));
+  asm volatile("v_mov_b32 %0, %1" : "=v"(magic) : "i"(Mma<DT>::kMagic));
+
+  const int nblocks = (nsteps + D - 1) / D;
+  for (int b = 0; b < nblocks; ++b) {
+#pragma unroll
+    for (int s = 0; s < D; ++s) {
+      const int st = b * D + s;
+      if (st < nsteps) {  // uniform; dead steps of the last block only refill below
+        const int kt = k_lo + st;
+        u32x4 a[4];
+#pragma unroll
+        for (int d = 0; d < 4; ++d)
+          a[d] = *reinterpret_cast<const u32x4*>(xrow + kt * kTileK + a_col<KIND>(q, d));
+        f32x4 xo = f32x4{0.f, 0.f, 0.f, 0.f};
+        if (W4 && GROUPED) xo = *reinterpret_cast<const f32x4*>(xsum + kt * 16 + 4 * q);
+#pragma unroll
+        for (int i = 0; i < RT; ++i) {
+          u32x4 bb[4];
+#pragma unroll
+          for (int d = 0; d < 4; ++d)
+            bb[d] = W4 ? unpack_w4(wbuf[s][i][0][d], nib_mask, magic)
+                       : convert_w8<DT>(wbuf[s][i][d >> 1][2 * (d & 1)],
+                                        wbuf[s][i][d >> 1][2 * (d & 1) + 1]);
+          if (W4 && GROUPED) {
+            f32x4 dacc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int d = 0; d < 4; ++d) dacc = Mma<DT>::mma(a[d], bb[d], dacc);
+            const int g = gtiles == 1 ? kt : kt / gtiles;
+            const float sc = ss[((rtl + i) * kTileN + r) * ngs + g];
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              acc[i][e] = fmaf(sc, fmaf(-Mma<DT>::kOff4, xo[e], dacc[e]), acc[i][e]);
+          } else {
+#pragma unroll
+            for (int d = 0; d < 4; ++d) acc[i] = Mma<DT>::mma(a[d], bb[d], acc[i]);
+          }
+        }
+      }
+      issue(wbuf[s], st + D);
+    }
+  }
+
+  // ---- cross-slice reduction (fixed slice order), epilogue
+  if (KS > 1) {
+    if (ks > 0) {
+#pragma unroll
+      for (int i = 0; i < RT; ++i)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          red[((((ks - 1) * RG + rg) * RT + i) * 4 + e) * 64 + lane] = acc[i][e];
+    }
+    lds_barrier();
+    if (ks > 0) return;
+#pragma unroll
+    for (int kk = 0; kk < KS - 1; ++kk)
+#pragma unroll
+      for (int i = 0; i < RT; ++i)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          acc[i][e] += red[(((kk * RG + rg) * RT + i) * 4 + e) * 64 + lane];
+  }
+
+  S* y = static_cast<S*>(p.y);
+#pragma unroll
+  for (int i = 0; i < RT; ++i) {
+    const int rl = (rtl + i) * kTileN + r;  // row within the workgroup
+    const int n = row0 + rl;
+    const float sc = GROUPED ? 1.f : ss[rl];
+    const float bias = p.bias ? sb[rl] : 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int m = 4 * q + e;
+      if (m < M && n < N) {
+        float v = acc[i][e];
+        if (W4 && !GROUPED) v = fmaf(-Mma<DT>::kOff4, xtot[m], v);
+        if (!GROUPED) v *= sc;
+        y[static_cast<int64_t>(m) * p.ldy + n] = Act<DT>::from_f32(v + bias);
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------------ launch
+
+struct Cfg {
+  int rt, rg, ks, d;
+};
+
+// Configurations compiled in (rt, rg, ks, d). The first one is the fallback default.
+#define LSQ_DECODE_CONFIGS(X) \
+  X(1, 8, 1, 4)               \
+  X(1, 4, 2, 8)               \
+  X(1, 2, 4, 4)               \
+  X(1, 1, 8, 4)               \
+  X(1, 2, 2, 8)               \
+  X(1, 2, 4, 8)               \
+  X(1, 1, 4, 8)               \
+  X(1, 4, 4, 4)
+
+int g_max_lds = -1;
+
+int max_lds_bytes() {
+  int v = g_max_lds;
+  if (v < 0) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess)
+      v = 64 * 1024;
+    g_max_lds = v;
+  }
+  return v;
+}
+
+// LSQ_DECODE_CFG="rt,rg,ks,d" overrides the heuristic with a compiled-in configuration
+// (for tuning sweeps); read once.
+bool env_cfg(Cfg* out) {
+  static int state = 0;  // 0 unread, 1 none, 2 set
+  static Cfg c{};
+  if (state == 0) {
+    const char* e = std::getenv("LSQ_DECODE_CFG");
+    state = 1;
+    if (e && std::sscanf(e, "%d,%d,%d,%d", &c.rt, &c.rg, &c.ks, &c.d) == 4) state = 2;
+  }
+  if (state == 2) *out = c;
+  return state == 2;
+}
+
+// Every wave streams one row tile over one K slice. Large layers: one slice per row
+// tile, 8 row tiles per workgroup (1184 waves at N = 18944 already keep enough bytes in
+// flight). Small layers: split K so that there are at least ~1024 waves, each with at
+// least a few k tiles.
+Cfg pick_cfg(int kind, int64_t M, int64_t N, int64_t K) {
+  Cfg c;
+  if (env_cfg(&c)) return c;
+  (void)kind;
+  (void)M;
+  const int64_t nrt = (N + kTileN - 1) / kTileN;
+  const int64_t nkt = K / kTileK;
+  if (nrt >= 1024 || nkt < 8) return Cfg{1, 8, 1, 4};
+  if (nrt * 2 >= 1024 || nkt < 16) return Cfg{1, 4, 2, 8};
+  if (nrt * 4 >= 1024 || nkt < 32) return Cfg{1, 2, 4, 4};
+  return Cfg{1, 1, 8, 4};
+}
+
+template <int DT, int KIND, int RT, int RG, int KS, int D, bool GROUPED>
+int launch_one(const LinearArgs& a, hipStream_t s) {
+  constexpr int RED = KS > 1 ? (KS - 1) * RG * RT * 4 * 64 : 0;
+  const bool grouped = a.group < a.K;
+  const DecodeLds L = decode_lds(a.M, a.K, RG * RT * kTileN, grouped ? a.ngroups : 1, RED);
+  if (L.total > max_lds_bytes()) return LSQ_E_LAYOUT;
+  auto kern = decode_kernel<DT, KIND, RT, RG, KS, D, GROUPED>;
+  if (L.total > 64 * 1024) {
+    static std::atomic<int> attr_set{0};
+    if (!attr_set.load(std::memory_order_acquire)) {
+      const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                               hipFuncAttributeMaxDynamicSharedMemorySize,
+                                               max_lds_bytes());
+      if (e != hipSuccess) return static_cast<int>(e);
+      attr_set.store(1, std::memory_order_release);
+    }
+  }
+  const int64_t nrt = (a.N + kTileN - 1) / kTileN;
+  const dim3 grid(static_cast<unsigned>((nrt + RG * RT - 1) / (RG * RT)));
+  kern<<<grid, dim3(64 * RG * KS), static_cast<size_t>(L.total), s>>>(a);
+  return static_cast<int>(hipGetLastError());
+}
+
+template <int DT, int KIND, bool GROUPED>
+int launch_kind(const LinearArgs& a, hipStream_t s) {
+  const Cfg c = pick_cfg(KIND, a.M, a.N, a.K);
+#define LSQ_TRY(RT_, RG_, KS_, D_)                                        \
+  if (c.rt == RT_ && c.rg == RG_ && c.ks == KS_ && c.d == D_)             \
+    return launch_one<DT, KIND, RT_, RG_, KS_, D_, GROUPED>(a, s);
+  LSQ_DECODE_CONFIGS(LSQ_TRY)
+#undef LSQ_TRY
+  return launch_one<DT, KIND, 1, 8, 1, 4, GROUPED>(a, s);
+}
+
+}  // namespace
+
+template <int DT>
+int launch_decode(int kind, const LinearArgs& a, hipStream_t s) {
+  if (a.M < 1 || a.M > 16 || a.K % kTileK != 0 || a.K < kTileK) return LSQ_E_LAYOUT;
+  const bool grouped = kind != kW8 && a.group < a.K;
+  if (grouped && a.group % kTileK != 0) return LSQ_E_LAYOUT;
+  // Buffer descriptors: 4-byte aligned scale / bias bases, 32-bit byte ranges.
+  auto aligned4 = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 3) == 0; };
+  if (!aligned4(a.scale) || (a.bias && !aligned4(a.bias))) return LSQ_E_LAYOUT;
+  if (((a.M - 1) * a.ldx + a.K) * 2 >= (int64_t(1) << 31)) return LSQ_E_LAYOUT;
+  if (int64_t(128) * a.K >= (int64_t(1) << 31)) return LSQ_E_LAYOUT;
+  switch (kind) {
+    case kW8: return launch_kind<DT, kW8, false>(a, s);
+    case kW8Tiled: return launch_kind<DT, kW8Tiled, false>(a, s);
+    case kW4Tiled:
+      return grouped ? launch_kind<DT, kW4Tiled, true>(a, s) : launch_kind<DT, kW4Tiled, false>(a, s);
+    case kW4Canon:
+      return grouped ? launch_kind<DT, kW4Canon, true>(a, s) : launch_kind<DT, kW4Canon, false>(a, s);
+    default: return LSQ_E_LAYOUT;
+  }
+}
+
+template int launch_decode<LSQ_BF16>(int, const LinearArgs&, hipStream_t);
+template int launch_decode<LSQ_F16>(int, const LinearArgs&, hipStream_t);
+
+}  // namespace lsq

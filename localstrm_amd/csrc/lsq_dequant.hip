@@ -130,6 +130,44 @@ __global__ void __launch_bounds__(256) untile_w4_kernel(const uint32_t* __restri
   }
 }
 
+// Tiled INT8 layout (lsq_internal.h). One thread per output dword.
+__global__ void __launch_bounds__(256) retile_w8_kernel(const uint32_t* __restrict__ wq,
+                                                        uint32_t* __restrict__ tiled, int64_t N,
+                                                        int64_t K) {
+  const int64_t nkt = K / kTileK;
+  const int64_t nrt = (N + kTileN - 1) / kTileN;
+  const int64_t total = nrt * nkt * (kTileBytes8 / 4);
+  for (int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; t < total;
+       t += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t tile = t / (kTileBytes8 / 4);
+    const int w = static_cast<int>(t - tile * (kTileBytes8 / 4));
+    const int j = w >> 8, lane = (w >> 2) & 63, d = w & 3;
+    const int64_t rt = tile / nkt, kt = tile - rt * nkt;
+    const int64_t n = rt * kTileN + (lane & 15);
+    const int64_t col = kt * kTileK + (lane >> 4) * 32 + j * 16 + d * 4;
+    tiled[t] = n < N ? wq[(n * K + col) / 4] : 0u;
+  }
+}
+
+__global__ void __launch_bounds__(256) untile_w8_kernel(const uint32_t* __restrict__ tiled,
+                                                        uint32_t* __restrict__ wq, int64_t N,
+                                                        int64_t K) {
+  const int64_t nkt = K / kTileK;
+  const int64_t nrt = (N + kTileN - 1) / kTileN;
+  const int64_t total = nrt * nkt * (kTileBytes8 / 4);
+  for (int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; t < total;
+       t += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t tile = t / (kTileBytes8 / 4);
+    const int w = static_cast<int>(t - tile * (kTileBytes8 / 4));
+    const int j = w >> 8, lane = (w >> 2) & 63, d = w & 3;
+    const int64_t rt = tile / nkt, kt = tile - rt * nkt;
+    const int64_t n = rt * kTileN + (lane & 15);
+    if (n >= N) continue;
+    const int64_t col = kt * kTileK + (lane >> 4) * 32 + j * 16 + d * 4;
+    wq[(n * K + col) / 4] = tiled[t];
+  }
+}
+
 static inline int elementwise_grid(int64_t work) {
   int64_t blocks = (work + 255) / 256;
   if (blocks > 65536) blocks = 65536;
@@ -233,5 +271,36 @@ extern "C" int lsq_w4_untile(const uint8_t* tiled, uint8_t* weight_packed, int64
   const int64_t dwords = lsq_w4_tiled_bytes(N, K) / 4;
   untile_w4_kernel<<<elementwise_grid(dwords), 256, 0, static_cast<hipStream_t>(stream)>>>(
       reinterpret_cast<const uint32_t*>(tiled), weight_packed, N, K);
+  return static_cast<int>(hipGetLastError());
+}
+
+extern "C" int64_t lsq_w8_tiled_bytes(int64_t N, int64_t K) {
+  if (N <= 0 || K <= 0 || K % kTileK != 0) return 0;
+  return ((N + kTileN - 1) / kTileN) * (K / kTileK) * kTileBytes8;
+}
+
+extern "C" int lsq_w8_retile(const int8_t* weight_q, int8_t* tiled, int64_t N, int64_t K,
+                             void* stream) {
+  if (!weight_q || !tiled) return LSQ_E_NULL;
+  if (N <= 0 || K <= 0) return LSQ_E_SHAPE;
+  if (K % kTileK != 0) return LSQ_E_LAYOUT;
+  if ((reinterpret_cast<uintptr_t>(weight_q) & 3) || (reinterpret_cast<uintptr_t>(tiled) & 15))
+    return LSQ_E_ALIGN;
+  const int64_t dwords = lsq_w8_tiled_bytes(N, K) / 4;
+  retile_w8_kernel<<<elementwise_grid(dwords), 256, 0, static_cast<hipStream_t>(stream)>>>(
+      reinterpret_cast<const uint32_t*>(weight_q), reinterpret_cast<uint32_t*>(tiled), N, K);
+  return static_cast<int>(hipGetLastError());
+}
+
+extern "C" int lsq_w8_untile(const int8_t* tiled, int8_t* weight_q, int64_t N, int64_t K,
+                             void* stream) {
+  if (!weight_q || !tiled) return LSQ_E_NULL;
+  if (N <= 0 || K <= 0) return LSQ_E_SHAPE;
+  if (K % kTileK != 0) return LSQ_E_LAYOUT;
+  if ((reinterpret_cast<uintptr_t>(weight_q) & 3) || (reinterpret_cast<uintptr_t>(tiled) & 15))
+    return LSQ_E_ALIGN;
+  const int64_t dwords = lsq_w8_tiled_bytes(N, K) / 4;
+  untile_w8_kernel<<<elementwise_grid(dwords), 256, 0, static_cast<hipStream_t>(stream)>>>(
+      reinterpret_cast<const uint32_t*>(tiled), reinterpret_cast<uint32_t*>(weight_q), N, K);
   return static_cast<int>(hipGetLastError());
 }

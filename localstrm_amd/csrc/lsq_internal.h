@@ -20,4 +20,11 @@ constexpr int kTileBytes = kTileN * kTileK / 2;
 
 __host__ __device__ constexpr int tiled_nibble_k(int p) { return p < 4 ? 2 * p : 2 * (p - 4) + 1; }
 
+// Tiled INT8 decode layout: the same 16-row x 128-column tiles in (row-tile, k-tile)
+// order, kTileBytes8 contiguous bytes each, made of two 1 KB halves j = 0, 1. Byte
+// j * 1024 + 16 l + b of a tile is W[16 rt + (l & 15)][128 kt + 32 (l >> 4) + 16 j + b],
+// so each 64-lane wavefront load reads 1 KB contiguous and lane l ends up with the 32
+// consecutive columns [32 (l >> 4), 32 (l >> 4) + 32) of row l & 15 of the tile.
+constexpr int kTileBytes8 = kTileN * kTileK;
+
 }  // namespace lsq

@@ -25,6 +25,7 @@
 #include "lsq_common.h"
 #include "lsq_internal.h"
 #include "lsq_gemm.h"
+#include "lsq_decode.h"
 
 #include <cstdlib>
 #include <cstring>
@@ -75,8 +76,6 @@ __global__ void __launch_bounds__(256) linear_generic_kernel(
 }
 
 // ============================================================ decode kernel
-
-enum WeightKind : int { kW8 = 0, kW4Tiled = 1, kW4Canon = 2 };
 
 template <int DT> struct Mfma;
 
@@ -400,6 +399,13 @@ static int dispatch(bool w4, const void* x, int64_t ldx, const uint8_t* w, const
     const bool mfma_ok = K % kTileK == 0 && x_aligned16(x, ldx) &&
                          (reinterpret_cast<uintptr_t>(w) & 15) == 0 &&
                          (!grouped || group % kTileK == 0);
+    if (mfma_ok && M <= 16) {
+      LinearArgs a{x, ldx, tiled ? tiled : w, scale, scale_dt, bias, bias_dt, y, ldy,
+                   M, N, K, group, ng};
+      const int kind = w4 ? (tiled ? kW4Tiled : kW4Canon) : (tiled ? kW8Tiled : kW8);
+      const int rc = launch_decode<DT>(kind, a, s);
+      if (rc != LSQ_E_LAYOUT) return rc;
+    }
     if (mfma_ok && M <= 64) {
       if (!w4)
         return launch_decode<DT, kW8>(x, ldx, w, scale, scale_dt, group, ng, false, bias, bias_dt,
@@ -433,7 +439,7 @@ extern "C" const char* lsq_status_string(int status) {
     case LSQ_E_SHAPE: return "lsq: M, N or K out of range, or leading dimension smaller than the row";
     case LSQ_E_DTYPE: return "lsq: unsupported dtype code";
     case LSQ_E_GROUP: return "lsq: group_size must be >= 1";
-    case LSQ_E_LAYOUT: return "lsq: the tiled INT4 layout needs K % 128 == 0";
+    case LSQ_E_LAYOUT: return "lsq: the tiled weight layouts need K % 128 == 0";
     case LSQ_E_ALIGN: return "lsq: pointer or leading dimension not aligned as required";
     default: break;
   }
@@ -441,20 +447,24 @@ extern "C" const char* lsq_status_string(int status) {
   return "lsq: unknown status";
 }
 
-extern "C" int lsq_w8_linear(const void* x, int64_t ldx, const int8_t* weight_q, const void* scale,
-                             int scale_dtype, const void* bias, int bias_dtype, void* y, int64_t ldy,
-                             int dtype, int64_t M, int64_t N, int64_t K, void* stream) {
+extern "C" int lsq_w8_linear(const void* x, int64_t ldx, const int8_t* weight_q,
+                             const int8_t* tiled, const void* scale, int scale_dtype,
+                             const void* bias, int bias_dtype, void* y, int64_t ldy, int dtype,
+                             int64_t M, int64_t N, int64_t K, void* stream) {
   const int rc = check_common(x, ldx, weight_q, scale, y, ldy, dtype, bias_dtype, bias, M, N, K);
   if (rc != LSQ_OK) return rc;
   if (scale_dtype != LSQ_F32 && scale_dtype != LSQ_F16 && scale_dtype != LSQ_BF16) return LSQ_E_DTYPE;
+  if (tiled && (reinterpret_cast<uintptr_t>(tiled) & 15)) return LSQ_E_ALIGN;
+  if (tiled && K % kTileK != 0) return LSQ_E_LAYOUT;
   if (M == 0 || N == 0) return LSQ_OK;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const uint8_t* w = reinterpret_cast<const uint8_t*>(weight_q);
+  const uint8_t* t = reinterpret_cast<const uint8_t*>(tiled);
   const int64_t group = K > 0 ? K : 1;
   switch (dtype) {
-    case LSQ_F32: return dispatch<LSQ_F32>(false, x, ldx, w, nullptr, scale, scale_dtype, group, bias, bias_dtype, y, ldy, M, N, K, s);
-    case LSQ_F16: return dispatch<LSQ_F16>(false, x, ldx, w, nullptr, scale, scale_dtype, group, bias, bias_dtype, y, ldy, M, N, K, s);
-    default: return dispatch<LSQ_BF16>(false, x, ldx, w, nullptr, scale, scale_dtype, group, bias, bias_dtype, y, ldy, M, N, K, s);
+    case LSQ_F32: return dispatch<LSQ_F32>(false, x, ldx, w, t, scale, scale_dtype, group, bias, bias_dtype, y, ldy, M, N, K, s);
+    case LSQ_F16: return dispatch<LSQ_F16>(false, x, ldx, w, t, scale, scale_dtype, group, bias, bias_dtype, y, ldy, M, N, K, s);
+    default: return dispatch<LSQ_BF16>(false, x, ldx, w, t, scale, scale_dtype, group, bias, bias_dtype, y, ldy, M, N, K, s);
   }
 }
 

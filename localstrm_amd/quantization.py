@@ -15,10 +15,11 @@ Extensions beyond the reference (all opt-in, defaults reproduce the reference):
     reference's per-output-channel scale `[N, 1]`.
   * `from_quantized` to install pre-quantized weights (pattern of
     CachedQuantizedLinear.from_quantized, quantization.py:241-256).
-  * `weight_tiled`: a derived, non-persistent copy of `weight_packed` re-tiled on the GPU
-    for the decode kernels (16x128 tiles of 1 KB, one wavefront load each). It is rebuilt
-    whenever the module moves to a GPU or `weight_packed` changes; the canonical
-    `weight_packed` keeps the reference's nibble layout.
+  * `weight_tiled`: a derived, non-persistent copy of `weight_q` / `weight_packed`
+    re-tiled on the GPU for the decode kernels (16x128 tiles, each 1 KB wavefront load
+    contiguous in HBM). It is rebuilt whenever the module moves to a GPU or the canonical
+    buffer changes; `weight_q` / `weight_packed` keep the reference's layouts.
+    LSQ_WEIGHT_LAYOUT=canonical makes forward() read the canonical buffers instead.
 """
 
 from __future__ import annotations
@@ -49,7 +50,7 @@ def format_bytes(num_bytes: int) -> str:
 
 
 def _use_tiled_layout() -> bool:
-    return os.environ.get("LSQ_W4_LAYOUT", "tiled").lower() != "canonical"
+    return os.environ.get("LSQ_WEIGHT_LAYOUT", "tiled").lower() != "canonical"
 
 
 def _require_gpu(t: torch.Tensor, what: str) -> None:
@@ -106,6 +107,8 @@ class QuantizedLinear(nn.Module):
             self.register_buffer(
                 "scale", torch.zeros((out_features, 1), dtype=scale_dtype or torch.float32)
             )
+            self.register_buffer("weight_tiled", torch.zeros(0, dtype=torch.int8), persistent=False)
+            self._tiled_key = None
         elif self.quant_type == "int4":
             if group_size is not None and group_size < 1:
                 raise ValueError(f"group_size must be >= 1, got {group_size}")
@@ -233,50 +236,61 @@ class QuantizedLinear(nn.Module):
 
     # ------------------------------------------------------------------ tiled layout
 
+    def _canonical(self) -> torch.Tensor:
+        return self.weight_q if self.quant_type == "int8" else self.weight_packed
+
     def _tiled_wanted(self) -> bool:
         return (
-            self.quant_type == "int4"
-            and self.weight_packed.device.type == "cuda"
+            self.quant_type in ("int8", "int4")
+            and self._canonical().device.type == "cuda"
             and self.in_features % TILE_K == 0
             and self.in_features > 0
             and self.out_features > 0
         )
 
     def _refresh_tiled(self) -> None:
-        """(Re)build weight_tiled from weight_packed on the GPU; empty elsewhere."""
-        if self.quant_type != "int4":
+        """(Re)build weight_tiled from the canonical buffer on the GPU; empty elsewhere."""
+        if self.quant_type not in ("int8", "int4"):
             return
+        src = self._canonical()
+        tdt = torch.int8 if self.quant_type == "int8" else torch.uint8
         if not self._tiled_wanted():
-            if self.weight_tiled.numel() != 0 or self.weight_tiled.device != self.weight_packed.device:
-                self.weight_tiled = torch.zeros(0, dtype=torch.uint8, device=self.weight_packed.device)
+            if self.weight_tiled.numel() != 0 or self.weight_tiled.device != src.device:
+                self.weight_tiled = torch.zeros(0, dtype=tdt, device=src.device)
             self._tiled_key = None
             return
-        wp = self.weight_packed
-        if not wp.is_contiguous():
-            self.weight_packed = wp = wp.contiguous()
+        if not src.is_contiguous():
+            src = src.contiguous()
+            if self.quant_type == "int8":
+                self.weight_q = src
+            else:
+                self.weight_packed = src
         lib = _lib.load()
-        nbytes = lib.lsq_w4_tiled_bytes(self.out_features, self.in_features)
-        if self.weight_tiled.numel() != nbytes or self.weight_tiled.device != wp.device:
-            self.weight_tiled = torch.empty(nbytes, dtype=torch.uint8, device=wp.device)
-        with torch.cuda.device(wp.device):
+        w8 = self.quant_type == "int8"
+        nbytes = (lib.lsq_w8_tiled_bytes if w8 else lib.lsq_w4_tiled_bytes)(
+            self.out_features, self.in_features)
+        if self.weight_tiled.numel() != nbytes or self.weight_tiled.device != src.device:
+            self.weight_tiled = torch.empty(nbytes, dtype=tdt, device=src.device)
+        with torch.cuda.device(src.device):
             _lib.check(
-                lib.lsq_w4_retile(wp.data_ptr(), self.weight_tiled.data_ptr(), self.out_features,
-                                  self.in_features, _lib.stream_handle(wp.device)),
-                "lsq_w4_retile",
+                (lib.lsq_w8_retile if w8 else lib.lsq_w4_retile)(
+                    src.data_ptr(), self.weight_tiled.data_ptr(), self.out_features,
+                    self.in_features, _lib.stream_handle(src.device)),
+                "lsq_w8_retile" if w8 else "lsq_w4_retile",
             )
-        self._tiled_key = (wp.data_ptr(), wp._version, wp.device)
+        self._tiled_key = (src.data_ptr(), src._version, src.device)
 
     def _apply(self, fn, recurse=True):
         super()._apply(fn, recurse)
-        if self.quant_type == "int4":
+        if self.quant_type in ("int8", "int4"):
             self._refresh_tiled()
         return self
 
     def _tiled_for_forward(self) -> Optional[torch.Tensor]:
         if not self._tiled_wanted() or not _use_tiled_layout():
             return None
-        wp = self.weight_packed
-        if self._tiled_key != (wp.data_ptr(), wp._version, wp.device):
+        src = self._canonical()
+        if self._tiled_key != (src.data_ptr(), src._version, src.device):
             self._refresh_tiled()
         return self.weight_tiled
 
@@ -361,13 +375,13 @@ class QuantizedLinear(nn.Module):
         lib = _lib.load()
         ldx = x2.stride(0) if m > 1 else self.in_features
         stream = _lib.stream_handle(x.device)
+        tiled = self._tiled_for_forward()
         if self.quant_type == "int8":
-            rc = lib.lsq_w8_linear(x2.data_ptr(), ldx, src.data_ptr(), scale.data_ptr(),
-                                   _lib.dtype_code(scale.dtype), bias_ptr, bias_code,
-                                   y.data_ptr(), self.out_features, code, m, self.out_features,
-                                   self.in_features, stream)
+            rc = lib.lsq_w8_linear(x2.data_ptr(), ldx, src.data_ptr(), _lib.ptr(tiled),
+                                   scale.data_ptr(), _lib.dtype_code(scale.dtype), bias_ptr,
+                                   bias_code, y.data_ptr(), self.out_features, code, m,
+                                   self.out_features, self.in_features, stream)
         else:
-            tiled = self._tiled_for_forward()
             rc = lib.lsq_w4_linear(x2.data_ptr(), ldx, src.data_ptr(), _lib.ptr(tiled),
                                    scale.data_ptr(), _lib.dtype_code(scale.dtype),
                                    self._group_for_kernel(), bias_ptr, bias_code, y.data_ptr(),

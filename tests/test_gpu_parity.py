@@ -116,6 +116,30 @@ def test_full_size_dequant_bit_exact(dt):
     assert np.array_equal(got4.view(np.uint32), _oracle_deq("int4", p, s4, 3584, 128, dt).view(np.uint32))
 
 
+def test_retile_w8_round_trip():
+    _say("retile w8 round trip")
+    lib = _lib.load()
+    for n, k in [(16, 128), (17, 256), (18944, 3584), (100, 896)]:
+        w, _, _ = bench.make_int8(n, k, 1, seed=n)
+        w = w.to(DEV)
+        tiled = torch.empty(lib.lsq_w8_tiled_bytes(n, k), dtype=torch.int8, device=DEV)
+        back = torch.zeros_like(w)
+        st = _lib.stream_handle(DEV)
+        _lib.check(lib.lsq_w8_retile(w.data_ptr(), tiled.data_ptr(), n, k, st), "retile")
+        _lib.check(lib.lsq_w8_untile(tiled.data_ptr(), back.data_ptr(), n, k, st), "untile")
+        assert torch.equal(back, w)
+        # layout: byte j*1024 + 16*l + b of tile (rt, kt) = W[16 rt + l%16, 128 kt + 32 (l//16) + 16 j + b]
+        t = tiled.view(-1, k // 128, 2, 64, 16).cpu()
+        wc = w.cpu()
+        for rt, kt, j, l, b in [(0, 0, 0, 0, 0), (0, 0, 1, 63, 15), ((n - 1) // 16, k // 128 - 1, 1, 17, 3)]:
+            r = 16 * rt + l % 16
+            if r < n:
+                assert t[rt, kt, j, l, b] == wc[r, 128 * kt + 32 * (l // 16) + 16 * j + b]
+        if n % 16:
+            lanes = torch.arange(64) % 16
+            assert int(t[-1][:, :, lanes >= n % 16].abs().sum()) == 0
+
+
 def test_retile_round_trip():
     _say("retile round trip")
     lib = _lib.load()
@@ -160,8 +184,11 @@ def _check_layer(kind, n, k, m, group=128, dtype=torch.bfloat16, bias=False, see
 
 
 @pytest.mark.parametrize("m", [1, 8, 32, 64])
-def test_int8_decode_config_shape(m):
-    """INT8 per-channel decode at 18944x3584, M in {1, 8, 32, 64}; oracle on 512 rows."""
+@pytest.mark.parametrize("layout", ["tiled", "canonical"])
+def test_int8_decode_config_shape(m, layout, monkeypatch):
+    """INT8 per-channel decode at 18944x3584, M in {1, 8, 32, 64}, both weight layouts;
+    oracle on 512 rows."""
+    monkeypatch.setenv("LSQ_WEIGHT_LAYOUT", layout)
     rows = np.sort(np.random.default_rng(m).choice(18944, 512, replace=False))
     _check_layer("int8", 18944, 3584, m, rows=rows)
 
@@ -170,7 +197,7 @@ def test_int8_decode_config_shape(m):
 @pytest.mark.parametrize("layout", ["tiled", "canonical"])
 def test_int4_g128_decode_config_shape(m, layout, monkeypatch):
     """INT4 group-128 decode at 18944x3584, M in {1, 16, 64}, both weight layouts."""
-    monkeypatch.setenv("LSQ_W4_LAYOUT", layout)
+    monkeypatch.setenv("LSQ_WEIGHT_LAYOUT", layout)
     rows = np.sort(np.random.default_rng(m).choice(18944, 512, replace=False))
     _check_layer("int4", 18944, 3584, m, rows=rows)
 

@@ -228,7 +228,7 @@ def test_library_exports_every_declared_symbol():
 def test_library_rejects_bad_arguments_without_gpu():
     lib = _lib.load()
     # NULL pointers and bad shapes/dtypes are rejected before any HIP call
-    assert lib.lsq_w8_linear(None, 16, None, None, 0, None, 0, None, 16, 2, 1, 16, 16, None) == -1
+    assert lib.lsq_w8_linear(None, 16, None, None, None, 0, None, 0, None, 16, 2, 1, 16, 16, None) == -1
     assert lib.lsq_w4_linear(1 << 20, 8, 1 << 20, None, 1 << 20, 0, 128, None, 0, 1 << 20, 16, 2,
                              1, 16, 16, None) == -2  # ldx < K
     assert lib.lsq_w4_linear(1 << 20, 16, 1 << 20, None, 1 << 20, 0, 0, None, 0, 1 << 20, 16, 2,
@@ -239,10 +239,15 @@ def test_library_rejects_bad_arguments_without_gpu():
     # an empty batch (M = 0) may carry NULL x / y, as torch gives for zero-element tensors
     assert lib.lsq_w4_linear(None, 16, 1 << 20, None, 1 << 20, 0, 16, None, 0, None, 16, 2,
                              0, 16, 16, None) == 0
-    assert lib.lsq_w8_linear(None, 16, 1 << 20, 1 << 20, 0, None, 0, None, 16, 2, 0, 16, 16,
-                             None) == 0
-    assert lib.lsq_w8_linear(None, 16, 1 << 20, 1 << 20, 0, None, 0, 1 << 20, 16, 2, 1, 16, 16,
-                             None) == -1  # M > 0 needs x
+    assert lib.lsq_w8_linear(None, 16, 1 << 20, None, 1 << 20, 0, None, 0, None, 16, 2, 0, 16,
+                             16, None) == 0
+    assert lib.lsq_w8_linear(None, 16, 1 << 20, None, 1 << 20, 0, None, 0, 1 << 20, 16, 2, 1, 16,
+                             16, None) == -1  # M > 0 needs x
+    assert lib.lsq_w8_linear(1 << 20, 128, 1 << 20, (1 << 20) + 8, 1 << 20, 0, None, 0, 1 << 20,
+                             16, 2, 1, 16, 128, None) == -6  # tiled copy not 16-byte aligned
+    assert lib.lsq_w8_retile(1 << 20, 1 << 20, 16, 100, None) == -5
+    assert lib.lsq_w8_tiled_bytes(18944, 3584) == 18944 * 3584
+    assert lib.lsq_w8_tiled_bytes(17, 128) == 2 * 2048
     assert lib.lsq_w4_tiled_bytes(18944, 3584) == 18944 * 3584 // 2
     assert lib.lsq_w4_tiled_bytes(17, 128) == 2 * 1024  # rows padded to 16
     assert lib.lsq_w4_tiled_bytes(16, 100) == 0
