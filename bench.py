@@ -1,6 +1,7 @@
 """Benchmark of the weight-only quantized linear layer on one MI355X.
 
 python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-sweep] [--no-cpu]
+python bench.py --calibrate-copy   # one 64 MiB device-to-device copy, for PMC calibration
 
 Headline workload (one JSON line, `value`): INT8 per-output-channel decode GEMV at the
 Qwen2.5-7B MLP shape, W int8 [18944, 3584], x bf16 [1, 3584] -> y bf16 [1, 18944].
@@ -9,6 +10,10 @@ bytes) / time per step, with inputs resident in HBM. The timed region is a HIP g
 K back-to-back launches bracketed by events on the launch stream; successive launches
 cycle through enough distinct weight copies (> 256 MB) that every launch streams its
 weights from HBM rather than from the 256 MB Infinity Cache.
+
+`roofline.traffic` is the HBM bytes one launch of the headline kernel moves, as measured
+by rocprofv3 FETCH_SIZE + WRITE_SIZE (each scaled by what the counter reads for a 64 MiB
+copy, see --calibrate-copy) and recorded in profiles/decode_int8_m1_18944x3584.txt.
 
 `sweep` reports the other shapes of the same metric (INT8 M in {8,32,64}, INT4 group-128
 decode M in {1,16,64} at 18944x3584, INT4 group-128 prefill M in {256,2048,8192} at
@@ -125,6 +130,34 @@ def time_layers(layers, x, steps: int, warmup: int) -> float:
     return start.elapsed_time(stop) / steps
 
 
+PROFILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                       "decode_int8_m1_18944x3584.txt")
+
+
+def measured_traffic():
+    """HBM bytes per launch of the headline kernel from its committed rocprofv3 summary
+    (line 'traffic_bytes_per_launch: N'), or None."""
+    try:
+        with open(PROFILE) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(float(line.split(":", 1)[1]))
+    except (OSError, ValueError):
+        pass
+    return None
+
+
+def calibrate_copy(device) -> None:
+    """A plain device-to-device copy of 64 MiB, 5 times: run under rocprofv3 --pmc to get
+    what FETCH_SIZE / WRITE_SIZE read for 64 MiB moved."""
+    a = torch.empty(64 << 20, dtype=torch.uint8, device=device)
+    b = torch.empty_like(a)
+    for _ in range(5):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print(f"copied {a.numel()} bytes x 5", flush=True)
+
+
 def copies_for(nbytes: int) -> int:
     return max(2, min(32, -(-2 * MALL_BYTES // max(nbytes, 1)) + 1))
 
@@ -166,7 +199,7 @@ def cpu_baseline(n: int, k: int, m: int, budget_s: float = 15.0):
         for _ in range(2):
             torch_ref.forward_int8(x, w, s)
         t_end = time.perf_counter() + budget_s
-        while time.perf_counter() < t_end and len(times) < 50:
+        while time.perf_counter() < t_end and len(times) < 2000:
             t0 = time.perf_counter()
             torch_ref.forward_int8(x, w, s)
             times.append(time.perf_counter() - t0)
@@ -199,6 +232,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--calibrate-copy", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this layer's multi-GPU sharding is not built "
@@ -210,6 +244,9 @@ def main() -> int:
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
     device = torch.device("cuda:0")
     torch.cuda.set_device(device)
+    if args.calibrate_copy:
+        calibrate_copy(device)
+        return 0
 
     N, K, M = 18944, 3584, 1
     head = bench_decode("int8", N, K, M, args.steps, args.warmup, device)
@@ -242,7 +279,7 @@ def main() -> int:
         },
         "roofline": {
             "bound": "hbm", "achieved": round(head["GB_s"], 2), "peak": HBM_PEAK_GBS,
-            "unit": "GB/s", "frac": round(head["frac_hbm"], 4), "traffic": None,
+            "unit": "GB/s", "frac": round(head["frac_hbm"], 4), "traffic": measured_traffic(),
         },
         "cpu_baseline": cpu,
         "sweep": sweep,
