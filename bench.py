@@ -256,6 +256,9 @@ def main() -> int:
             sweep.append(bench_decode("int8", N, K, m, args.steps, args.warmup, device))
         for m in (1, 16, 64):
             sweep.append(bench_decode("int4", N, K, m, args.steps, args.warmup, device))
+        for m in (256, 2048, 8192):
+            sweep.append(bench_decode("int4", 14336, 4096, m, max(10, args.steps // 20),
+                                      max(2, args.warmup // 4), device))
     cpu = None if args.no_cpu else cpu_baseline(N, K, M)
 
     ms = head["us_per_call"] / 1e3

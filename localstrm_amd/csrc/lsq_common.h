@@ -100,4 +100,42 @@ __device__ __forceinline__ u32x4 load_u32x4(const void* p) {
   return *static_cast<const u32x4*>(p);
 }
 
+// ---------------------------------------------------------------- buffer loads
+// The fast kernels read global memory through buffer descriptors bounding a region the
+// workgroup owns; a load at an offset past the bound returns zero without touching
+// memory, so out-of-range rows and pipeline loads past the end need no clamping or
+// branches.
+using rsrc_t = __amdgpu_buffer_rsrc_t;
+constexpr int kRsrcWord3 = 0x00020000;  // gfx9-family descriptor word 3: raw 32-bit dwords
+constexpr uint32_t kOOB = 0x80000000u;  // past every descriptor's range
+constexpr int kNT = 2;                  // cache policy: non-temporal (weights, read once)
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, kRsrcWord3);
+}
+
+template <int AUX>
+__device__ __forceinline__ u32x4 bload16(rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, AUX);
+}
+
+__device__ __forceinline__ uint32_t bload4(rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+}
+
+// Workgroup barrier that orders LDS only: the compiler's __syncthreads() also waits for
+// every outstanding global load, which would drain the weight pipeline.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// fp32 value of element `half` (0 or 1) of a dword of 16-bit floats, or of an fp32 dword.
+__device__ __forceinline__ float dword_elem(uint32_t w, int half, int dt) {
+  if (dt == LSQ_F32) return __uint_as_float(w);
+  const uint32_t h = half ? (w >> 16) : (w & 0xFFFFu);
+  return dt == LSQ_BF16 ? __uint_as_float(h << 16) : f16_to_f32(static_cast<uint16_t>(h));
+}
+
 }  // namespace lsq

@@ -1,16 +1,18 @@
-// Prefill-shaped GEMM entry (M > 64) shared by the INT8 and INT4 paths.
+// Prefill-shaped GEMM (M > 16 tokens): declaration shared with the dispatcher in
+// lsq_linear.hip.
 #pragma once
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "lsq_decode.h"
+
 namespace lsq {
 
-// Returns LSQ_E_LAYOUT when the shape is outside what the GEMM kernels cover; the
-// caller then uses the generic kernel.
+// Launches the LDS-dequant MFMA GEMM when the shape fits it (fp16/bf16 activations,
+// K % 128 == 0, group % 128 == 0, tiled or canonical weights). Returns LSQ_E_LAYOUT
+// without launching anything when it does not fit.
 template <int DT>
-int launch_gemm(bool w4, const void* x, int64_t ldx, const uint8_t* w, const void* scale,
-                int scale_dt, int64_t group, int64_t ngroups, const void* bias, int bias_dt,
-                void* y, int64_t ldy, int64_t M, int64_t N, int64_t K, hipStream_t s);
+int launch_gemm(int kind, const LinearArgs& a, hipStream_t s);
 
 }  // namespace lsq

@@ -202,6 +202,37 @@ def test_int4_g128_decode_config_shape(m, layout, monkeypatch):
     _check_layer("int4", 18944, 3584, m, rows=rows)
 
 
+@pytest.mark.parametrize("m", [256, 2048])
+@pytest.mark.parametrize("layout", ["tiled", "canonical"])
+def test_int4_g128_prefill_config_shape(m, layout, monkeypatch):
+    """INT4 group-128 prefill GEMM at the Llama-3-8B MLP shape 14336x4096, M in {256, 2048};
+    oracle on 256 sampled output columns and (for M=2048) 256 sampled rows."""
+    monkeypatch.setenv("LSQ_WEIGHT_LAYOUT", layout)
+    n, k = 14336, 4096
+    p, s, x = bench.make_int4(n, k, m, 128, seed=m)
+    ql = _layer("int4", p, s, k, 128)
+    with torch.no_grad():
+        y = ql(x.to(DEV)).float().cpu().numpy()
+    rng = np.random.default_rng(m)
+    cols = np.sort(rng.choice(n, 256, replace=False))
+    rows = np.arange(m) if m <= 256 else np.sort(rng.choice(m, 256, replace=False))
+    wd = qo.dequant_int4(p[cols].numpy(), s[cols].float().numpy(), k, 128, "bf16")
+    ref = qo.linear_f64(x[rows].float().numpy(), wd, None, "bf16")
+    err = qo.rel_err(y[np.ix_(rows, cols)], ref)
+    _say(f"  int4 prefill M={m} {layout}: rel_err={err:.3e}")
+    assert err <= REL_TOL
+
+
+@pytest.mark.parametrize("kind", ["int8", "int4"])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_gemm_edges_bias_and_dtypes(kind, dtype):
+    """GEMM tiles with ragged M and N edges (M=300, N=272 = 256 + 16), bias, both dtypes,
+    per-channel INT8, group-128 INT4, and per-channel INT4."""
+    _check_layer(kind, 272, 512, 300, group=128, dtype=dtype, bias=True, seed=7)
+    if kind == "int4":
+        _check_layer("int4", 272, 512, 300, group=512, dtype=dtype, bias=True, seed=8)
+
+
 def test_int8_single_linear_config():
     """Qwen2.5-0.5B gate_proj: W int8 [4864, 896], fp32 scale, x fp32 and bf16 [1, 896]."""
     for dtype in (torch.float32, torch.bfloat16):
