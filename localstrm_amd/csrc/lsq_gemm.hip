@@ -6,17 +6,23 @@
 // weight tiles it needs straight into LDS and feeds bf16 / fp16 MFMA from there; the
 // dequantized weight never exists in HBM.
 //
-// Tiling. A workgroup computes a 256 x 256 tile of y with 4 waves in a 2 x 2 layout; each
-// wave owns 128 x 128 outputs as 4 x 4 blocks of v_mfma_f32_32x32x16_{bf16,f16} (fp32
-// accumulators, 256 registers, in AGPRs). K advances 64 columns per step:
-//   * the activation tile x[256, 64] is copied to LDS (row stride 72 elements = 144 B, so
-//     the MFMA operand reads ds_read_b128 of 32 consecutive rows hit disjoint banks);
-//   * the weight tile W[256, 64] is loaded packed (INT4: 8 KB, INT8: 16 KB), unpacked in
-//     registers and written to LDS as T: group-wise INT4 as round_T(q * round_T(s)), the
-//     reference's dequantized weight exactly; per-channel INT4 / INT8 as the exact integer
-//     q, with the row scale applied to the fp32 accumulator in the epilogue;
-//   * LDS is double-buffered: the global loads of step k+1 are issued before the MFMAs of
-//     step k and written to the other buffer after them, one barrier per step.
+// Tiling. A workgroup computes a 256 x 256 tile of y with 8 waves in a 2 x 4 layout (two
+// waves per SIMD, so one issues MFMAs while the other waits); each wave owns 128 x 64
+// outputs as 4 x 2 blocks of v_mfma_f32_32x32x16_{bf16,f16} (fp32 accumulators, 128
+// registers). K advances 64 columns per step:
+//   * the activation tile x[256, 64] goes from HBM / L2 straight into LDS with
+//     buffer_load ... lds (no registers, no VALU), one step ahead;
+//   * the weight tile W[256, 64] is loaded packed (INT4: 8 KB, INT8: 16 KB) two steps
+//     ahead, unpacked in registers and written to LDS as T: group-wise INT4 as
+//     round_T(q * round_T(s)), the reference's dequantized weight exactly; per-channel
+//     INT4 / INT8 as the exact integer q, with the row scale applied to the fp32
+//     accumulator in the epilogue;
+//   * both LDS tiles store row r's 16-byte column chunk c at position c ^ ((r >> 1) & 7):
+//     the LDS serves a 16-byte-per-lane access 16 lanes at a time across 64 banks, and
+//     with this swizzle 16 consecutive rows at one column chunk hit 16 disjoint 4-bank
+//     groups (MFMA operand reads, weight stores);
+//   * LDS is double-buffered, one barrier per step; MFMA operands are double-buffered in
+//     registers across the four 16-column sub-steps.
 // All global reads go through buffer descriptors bounding the workgroup's rows, so
 // partial tiles at the M / N edges read zeros without branches.
 
@@ -34,10 +40,10 @@ typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
-constexpr int BM = 256, BN = 256, BK = 64, NT = 256;
-constexpr int LDP = BK + 8;  // LDS row stride of both tiles, elements
-constexpr int kTileElems = BM * LDP;
-constexpr int kLdsBytes = 2 * 2 * kTileElems * 2;  // {x, w} x 2 buffers x bf16
+constexpr int BM = 256, BN = 256, BK = 64, NT = 512;
+constexpr int WTM = 128, WTN = 64;  // wave tile: 2 x 4 waves
+constexpr int FM = WTM / 32, FN = WTN / 32;  // 32x32 MFMA blocks per wave
+constexpr int kLdsBytes = 2 * 2 * BM * BK * 2;  // {x, w} x 2 buffers x 16-bit
 
 template <int DT> struct Mma32;
 
@@ -108,16 +114,15 @@ __device__ __forceinline__ u32x4 convert8_w8(uint32_t w0, uint32_t w1) {
   return r;
 }
 
-// Per-thread share of one weight tile W[256 rows, 64 columns] of a step:
-//   kW4Tiled : 2 rows x 32 columns (two 16-byte lane chunks of a 1 KB tile)
-//   kW4Canon : 1 row  x 64 columns (32 bytes of a row)
-//   kW8Tiled : 2 rows x 32 columns (four 16-byte lane chunks of a 2 KB tile)
-//   kW8      : 1 row  x 64 columns (64 bytes of a row)
+// Per-thread share of one weight tile W[256 rows, 64 columns] of a step: thread t takes
+// row t & 255, columns 32 (t >> 8) .. +32 (so 16 consecutive lanes store 16 consecutive
+// rows), as 16-byte loads: INT4 one (a lane chunk of the tiled layout / 16 bytes of the
+// canonical row), INT8 two (two 1 KB halves of the tiled layout / 32 bytes of the row).
 template <int KIND> struct WPlan;
-template <> struct WPlan<kW4Tiled> { static constexpr int kLoads = 2, kRows = 2; };
-template <> struct WPlan<kW4Canon> { static constexpr int kLoads = 2, kRows = 1; };
-template <> struct WPlan<kW8Tiled> { static constexpr int kLoads = 4, kRows = 2; };
-template <> struct WPlan<kW8> { static constexpr int kLoads = 4, kRows = 1; };
+template <> struct WPlan<kW4Tiled> { static constexpr int kLoads = 1, kRows = 1; };
+template <> struct WPlan<kW4Canon> { static constexpr int kLoads = 1, kRows = 1; };
+template <> struct WPlan<kW8Tiled> { static constexpr int kLoads = 2, kRows = 1; };
+template <> struct WPlan<kW8> { static constexpr int kLoads = 2, kRows = 1; };
 
 template <int DT, int KIND, bool GROUPED>
 __global__ void __launch_bounds__(NT) gemm_kernel(LinearArgs p) {
@@ -126,8 +131,6 @@ __global__ void __launch_bounds__(NT) gemm_kernel(LinearArgs p) {
   constexpr int WL = WPlan<KIND>::kLoads;
   constexpr int WR = WPlan<KIND>::kRows;
   extern __shared__ __align__(16) unsigned char smem[];
-  uint16_t* xs = reinterpret_cast<uint16_t*>(smem);  // [2][BM][LDP]
-  uint16_t* ws = xs + 2 * kTileElems;                 // [2][BN][LDP]
   using S = typename Act<DT>::storage;
 
   const int M = static_cast<int>(p.M), N = static_cast<int>(p.N), K = static_cast<int>(p.K);
@@ -145,7 +148,22 @@ __global__ void __launch_bounds__(NT) gemm_kernel(LinearArgs p) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wid & 1, wn = wid >> 1;
+  const int wm = wid & 1, wn = wid >> 1;  // wave tile rows wm * 128, columns wn * 64
+
+  // K rotation. Workgroups are dealt to the 8 XCDs round-robin and the ~32 resident on
+  // one XCD share activation rows; walking K in lockstep, every step's activation tile
+  // would be a fresh HBM miss all of them wait on. Each workgroup instead starts at a
+  // different step (spread over K by its slot on the XCD) and wraps around, so after the
+  // first two steps the tiles it needs are already in the XCD's L2. The order of the
+  // fp32 sums over K is fixed per workgroup, so results do not depend on timing.
+  const int rot = (((blockIdx.x >> 3) & 31) * nsteps) >> 5;
+  auto gstep = [&](int st) { const int g = st + rot; return g >= nsteps ? g - nsteps : g; };
+
+  // LDS: x tiles at [0, 2 * kTile), w tiles after; each tile is 256 rows of 8 chunks of
+  // 16 bytes, chunk c of row r stored at position c ^ ((r >> 1) & 7).
+  constexpr int kTile = BM * BK * 2;
+  auto xs_at = [&](int buf) { return smem + buf * kTile; };
+  auto ws_at = [&](int buf) { return smem + (2 + buf) * kTile; };
 
   // ---- descriptors
   const rsrc_t rx = make_rsrc(static_cast<const uint16_t*>(p.x) + static_cast<int64_t>(m0) * p.ldx,
@@ -166,143 +184,176 @@ __global__ void __launch_bounds__(NT) gemm_kernel(LinearArgs p) {
   const rsrc_t rw = make_rsrc(wbase, wbytes);
   const int es_s = p.scale_dt == LSQ_F32 ? 4 : 2;
   const int ngs = GROUPED ? ng : 1;
-  // (see lsq_decode.hip: the dword of the last 16-bit element may reach 2 bytes past the
-  // array; an aligned dword never crosses a page)
+  // (the dword of the last 16-bit element may reach 2 bytes past the array; an aligned
+  // dword never crosses a page)
   const rsrc_t rs = make_rsrc(static_cast<const uint8_t*>(p.scale) + static_cast<int64_t>(n0) * ngs * es_s,
                               static_cast<uint32_t>((rows_n * ngs * es_s + 3) & ~3));
 
-  // ---- per-thread load plan
-  // activations: chunk c = tid + NT u (u < 8) of the 256 x 64 tile, 8 chunks per row
-  uint32_t xoff[8];
+  // ---- activations: DMA straight into LDS. One wave instruction fills 8 rows (1 KB):
+  // lane l writes LDS row rb + (l >> 3), position l & 7, which must hold column chunk
+  // (l & 7) ^ (((rb + (l >> 3)) >> 1) & 7); rb is a multiple of 8, so that swizzle term
+  // is ((rb >> 1) & 4) | (l >> 4), i.e. one of two lane patterns.
+  uint32_t x_lane_off[2];
 #pragma unroll
-  for (int u = 0; u < 8; ++u) {
-    const int c = tid + NT * u;
-    xoff[u] = static_cast<uint32_t>(((c >> 3) * p.ldx + (c & 7) * 8) * 2);
-  }
-  // weights: row(s) and first column of this thread's share, and its byte offsets
-  int wrow0, wcol0;  // tile-local
+  for (int v = 0; v < 2; ++v)
+    x_lane_off[v] = static_cast<uint32_t>(
+        ((lane >> 3) * p.ldx + 8 * ((lane & 7) ^ ((v << 2) | (lane >> 4)))) * 2);
+  auto issue_x = [&](int st, int buf) {
+    unsigned char* dst = xs_at(buf);
+#pragma unroll
+    for (int b = 0; b < BM / 8 / (NT / 64); ++b) {  // 4 row blocks per wave
+      const int rb = (wid * (BM / 8 / (NT / 64)) + b) * 8;  // (rb >> 1) & 4 == (b & 1) * 4
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rx, (__attribute__((address_space(3))) void*)(dst + rb * BK * 2), 16,
+          x_lane_off[b & 1], static_cast<int>((rb * p.ldx + gstep(st) * BK) * 2), 0, 0);
+    }
+  };
+
+  // ---- weights: packed tile share of this thread, prefetched two steps ahead
+  const int wrow0 = tid & (BN - 1);  // tile-local row
+  const int wc = tid >> 8;           // which 32 of the step's 64 columns
   uint32_t woff[WL];
   if (TILED) {
-    const int rtl = tid >> 4, e0 = 2 * (tid & 15);
-    wrow0 = rtl * kTileN + (e0 & 15);
-    wcol0 = 32 * (e0 >> 4);
-    // step-independent part; the step adds (k tile) * tile bytes + half * lanes
+    // lane chunk (row & 15) + 16 wc of the half-tile; INT8 adds the 1 KB half j
     const int tb = W4 ? kTileBytes : kTileBytes8;
 #pragma unroll
-    for (int l = 0; l < WL; ++l) {
-      const int e = W4 ? l : (l & 1), j = W4 ? 0 : (l >> 1);
-      woff[l] = static_cast<uint32_t>(rtl * nkt * tb + j * (kTileBytes8 / 2) + (e0 + e) * 16);
-    }
+    for (int l = 0; l < WL; ++l)
+      woff[l] = static_cast<uint32_t>((wrow0 >> 4) * nkt * tb + l * (kTileBytes8 / 2) +
+                                      ((wrow0 & 15) + 16 * wc) * 16);
   } else {
-    wrow0 = tid;
-    wcol0 = 0;
     const int rb = W4 ? K / 2 : K;
 #pragma unroll
-    for (int l = 0; l < WL; ++l) woff[l] = static_cast<uint32_t>(tid * rb + l * 16);
+    for (int l = 0; l < WL; ++l)
+      woff[l] = static_cast<uint32_t>(wrow0 * rb + (W4 ? 16 : 32) * wc + l * 16);
   }
-
-  u32x4 xr[8];
-  u32x4 wr[WL];
-  uint32_t sr[WR];
-  auto prefetch = [&](int st) {
-    const uint32_t kx = static_cast<uint32_t>(st * BK * 2);
-#pragma unroll
-    for (int u = 0; u < 8; ++u) xr[u] = bload16<0>(rx, xoff[u] + kx);
+  struct WRegs {
+    u32x4 w[WL];
+    uint32_t s[WR];
+  };
+  auto issue_w = [&](int st, WRegs& r) {
+    const bool real = st < nsteps;
+    const int gs = gstep(min(st, nsteps - 1));
     uint32_t kw;
     if (TILED) {
       const int tb = W4 ? kTileBytes : kTileBytes8;
-      kw = static_cast<uint32_t>((st >> 1) * tb + (st & 1) * 32 * 16);  // k tile, half
+      kw = static_cast<uint32_t>((gs >> 1) * tb + (gs & 1) * 32 * 16);  // k tile, half
     } else {
-      kw = static_cast<uint32_t>(st * (W4 ? BK / 2 : BK));
+      kw = static_cast<uint32_t>(gs * (W4 ? BK / 2 : BK));
     }
 #pragma unroll
-    for (int l = 0; l < WL; ++l) wr[l] = bload16<kNT>(rw, woff[l] + kw);
+    for (int l = 0; l < WL; ++l) r.w[l] = bload16<kNT>(rw, real ? woff[l] + kw : kOOB);
     if (GROUPED) {
-      const int g = (st * BK) / group;
+      const int g = (gs * BK) / group;
 #pragma unroll
-      for (int r = 0; r < WR; ++r) {
-        const uint32_t eb = static_cast<uint32_t>(((wrow0 + r) * ng + g) * es_s);
-        sr[r] = bload4(rs, eb & ~3u) >> (es_s == 2 ? 8 * (eb & 2) : 0);
+      for (int rr = 0; rr < WR; ++rr)
+        r.s[rr] = bload4(rs, static_cast<uint32_t>(((wrow0 + rr) * ng + g) * es_s) & ~3u);
+    }
+  };
+  // The thread's share of a weight tile is 4 units of 8 columns (INT4: one dword, INT8: a
+  // pair of dwords). put_w_unit(r, sf, buf, u) dequantizes unit u into LDS; the main loop
+  // spreads the 4 units over the MFMA sub-steps so the VALU work overlaps the MFMAs.
+  // Group scales of this thread's rows for step st, round_T, as fp32 (1 per-channel).
+  auto w_scales = [&](const WRegs& r, int st, float (&sf)[WR]) {
+#pragma unroll
+    for (int rr = 0; rr < WR; ++rr) sf[rr] = 1.f;
+    if (GROUPED) {
+      const int g = (gstep(min(st, nsteps - 1)) * BK) / group;
+#pragma unroll
+      for (int rr = 0; rr < WR; ++rr) {
+        const uint32_t eb = static_cast<uint32_t>(((wrow0 + rr) * ng + g) * es_s);
+        sf[rr] = Act<DT>::round(dword_elem(r.s[rr], (eb >> 1) & 1, p.scale_dt));
       }
     }
   };
-
-  auto store = [&](int buf) {
-    uint16_t* xb = xs + buf * kTileElems;
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int c = tid + NT * u;
-      *reinterpret_cast<u32x4*>(xb + (c >> 3) * LDP + (c & 7) * 8) = xr[u];
-    }
-    uint16_t* wbp = ws + buf * kTileElems;
+  // unit u = columns 32 wc + 8u .. +7 of the thread's row (u = 0..3)
+  auto put_w_unit = [&](const WRegs& r, const float (&sf)[WR], int buf, int u) {
+    const int row = wrow0;
+    unsigned char* addr = ws_at(buf) + row * (BK * 2) + (((4 * wc + u) ^ ((row >> 1) & 7)) << 4);
     if (W4) {
-#pragma unroll
-      for (int r = 0; r < WR; ++r) {
-        float s = 1.f;
-        if (GROUPED) s = Act<DT>::round(dword_elem(sr[r], 0, p.scale_dt));
-        const float ms8 = -8.f * s;
-        // this row's dwords: tiled: lane chunk r (4 dwords, 32 columns); canonical: 8
-        // dwords (64 columns) over the two loads
-        constexpr int DW = TILED ? 4 : 8;
-#pragma unroll
-        for (int d = 0; d < DW; ++d) {
-          const uint32_t w = TILED ? wr[r][d] : wr[d >> 2][d & 3];
-          *reinterpret_cast<u32x4*>(wbp + (wrow0 + r) * LDP + wcol0 + 8 * d) =
-              dequant8_w4<DT, TILED>(w, s, ms8);
-        }
-      }
+      *reinterpret_cast<u32x4*>(addr) = dequant8_w4<DT, TILED>(r.w[0][u], sf[0], -8.f * sf[0]);
     } else {
-#pragma unroll
-      for (int r = 0; r < WR; ++r) {
-        // tiled: chunk (j, e=r) holds 16 columns wcol0 + 16 j; canonical: 64 columns
-        constexpr int C16 = TILED ? 2 : 4;  // 16-column chunks of this row
-#pragma unroll
-        for (int c16 = 0; c16 < C16; ++c16) {
-          const u32x4 v = TILED ? wr[2 * c16 + r] : wr[c16];
-          uint16_t* dst = wbp + (wrow0 + r) * LDP + wcol0 + 16 * c16;
-          *reinterpret_cast<u32x4*>(dst) = convert8_w8<DT>(v[0], v[1]);
-          *reinterpret_cast<u32x4*>(dst + 8) = convert8_w8<DT>(v[2], v[3]);
-        }
-      }
+      // 16 columns per load (tiled: the 1 KB half u >> 1; canonical: bytes 16 (u >> 1))
+      const u32x4 v = r.w[u >> 1];
+      *reinterpret_cast<u32x4*>(addr) = (u & 1) ? convert8_w8<DT>(v[2], v[3]) : convert8_w8<DT>(v[0], v[1]);
     }
   };
+  auto put_w = [&](const WRegs& r, int st, int buf) {
+    float sf[WR];
+    w_scales(r, st, sf);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) put_w_unit(r, sf, buf, u);
+  };
 
-  f32x16 acc[4][4];
+  // ---- MFMA operands: lane l reads row (l & 31) of each 32-row block, 8 columns at
+  // 16 kk + 8 (l >> 5); with the swizzle that is position (2 kk + (l >> 5)) ^ (((l & 31) >> 1) & 7).
+  f32x16 acc[FM][FN];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < FM; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < FN; ++j)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
-
-  const int arow = wm * 128 + (lane & 31);
-  const int brow = wn * 128 + (lane & 31);
-  const int kcol = 8 * (lane >> 5);
-
-  prefetch(0);
-  store(0);
-  lds_barrier();
-  for (int st = 0; st < nsteps; ++st) {
-    const int buf = st & 1;
-    if (st + 1 < nsteps) prefetch(st + 1);
-    const uint16_t* xb = xs + buf * kTileElems;
-    const uint16_t* wbp = ws + buf * kTileElems;
+  const int frow = lane & 31;
+  auto frag_off = [&](int kk) {
+    return frow * (BK * 2) + (((2 * kk + (lane >> 5)) ^ ((frow >> 1) & 7)) << 4);
+  };
+  // One step of MFMAs on LDS buffer `buf`; after each 16-column sub-step, side(kk) does
+  // a quarter of the next weight tile's dequantization.
+  auto compute = [&](int buf, auto&& side) {
+    const unsigned char* xb = xs_at(buf) + wm * WTM * (BK * 2);
+    const unsigned char* wbp = ws_at(buf) + wn * WTN * (BK * 2);
+    u32x4 a[2][FM], b[2][FN];
+    auto load = [&](int kk, u32x4 (&aa)[FM], u32x4 (&bb)[FN]) {
+      const int off = frag_off(kk);
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+        aa[i] = *reinterpret_cast<const u32x4*>(xb + 32 * i * (BK * 2) + off);
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+        bb[j] = *reinterpret_cast<const u32x4*>(wbp + 32 * j * (BK * 2) + off);
+    };
+    load(0, a[0], b[0]);
 #pragma unroll
     for (int kk = 0; kk < BK / 16; ++kk) {
-      u32x4 a[4], b[4];
+      if (kk + 1 < BK / 16) load(kk + 1, a[(kk + 1) & 1], b[(kk + 1) & 1]);
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        a[i] = *reinterpret_cast<const u32x4*>(xb + (arow + 32 * i) * LDP + kk * 16 + kcol);
+      for (int i = 0; i < FM; ++i)
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-        b[j] = *reinterpret_cast<const u32x4*>(wbp + (brow + 32 * j) * LDP + kk * 16 + kcol);
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = Mma32<DT>::mma(a[i], b[j], acc[i][j]);
+        for (int j = 0; j < FN; ++j) acc[i][j] = Mma32<DT>::mma(a[kk & 1][i], b[kk & 1][j], acc[i][j]);
+      side(kk);
     }
-    if (st + 1 < nsteps) store(buf ^ 1);
+  };
+
+  // ---- pipeline: x one step ahead (LDS DMA), w two steps ahead (registers). The step
+  // count K / 64 is even (K % 128 == 0), so the loop runs whole pairs of steps and every
+  // load is unconditional: past the last step the w loads are out of range and the x DMA
+  // lands in a buffer nobody reads again. Before each barrier only the x DMA must have
+  // landed: the w loads issued after it (for three steps ahead) stay in flight.
+  constexpr int kWLoads = WL + (GROUPED ? WR : 0);
+  constexpr int kWaitX = (kWLoads & 15) | (7 << 4) | ((kWLoads >> 4) << 14);  // vmcnt(kWLoads), lgkmcnt(0)
+  WRegs wr0, wr1;
+  issue_x(0, 0);
+  issue_w(0, wr0);
+  issue_w(1, wr1);
+  put_w(wr0, 0, 0);
+  issue_w(2, wr0);
+  __builtin_amdgcn_s_waitcnt(kWaitX);
+  lds_barrier();
+  auto step = [&](int st, WRegs& next) {  // next holds step st + 1; refilled with st + 3
+    const int buf = st & 1;
+    issue_x(st + 1, buf ^ 1);
+    float sf[WR];
+    w_scales(next, st + 1, sf);
+    compute(buf, [&](int kk) {
+      put_w_unit(next, sf, buf ^ 1, kk);
+    });
+    issue_w(st + 3, next);
+    __builtin_amdgcn_s_waitcnt(kWaitX);
     lds_barrier();
+  };
+  for (int st = 0; st < nsteps; st += 2) {
+    step(st, wr1);
+    step(st + 1, wr0);
   }
 
   // ---- epilogue: per-channel scale, bias, one rounding to T
@@ -311,10 +362,10 @@ __global__ void __launch_bounds__(NT) gemm_kernel(LinearArgs p) {
   const rsrc_t rb = make_rsrc(p.bias ? static_cast<const uint8_t*>(p.bias) + static_cast<int64_t>(n0) * es_b
                                      : static_cast<const uint8_t*>(p.scale),
                               p.bias ? static_cast<uint32_t>((rows_n * es_b + 3) & ~3) : 0u);
-  float scn[4], bsn[4];
+  float scn[FN], bsn[FN];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int nl = wn * 128 + 32 * j + (lane & 31);  // tile-local column
+  for (int j = 0; j < FN; ++j) {
+    const int nl = wn * WTN + 32 * j + (lane & 31);  // tile-local column
     if (GROUPED) {
       scn[j] = 1.f;
     } else {
@@ -325,13 +376,13 @@ __global__ void __launch_bounds__(NT) gemm_kernel(LinearArgs p) {
     bsn[j] = p.bias ? Act<DT>::round(dword_elem(bload4(rb, ebb & ~3u), (ebb >> 1) & 1, p.bias_dt)) : 0.f;
   }
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < FM; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int n = n0 + wn * 128 + 32 * j + (lane & 31);
+    for (int j = 0; j < FN; ++j) {
+      const int n = n0 + wn * WTN + 32 * j + (lane & 31);
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
-        const int m = m0 + wm * 128 + 32 * i + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+        const int m = m0 + wm * WTM + 32 * i + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
         if (m < M && n < N)
           y[static_cast<int64_t>(m) * p.ldy + n] = Act<DT>::from_f32(fmaf(acc[i][j][v], scn[j], bsn[j]));
       }
