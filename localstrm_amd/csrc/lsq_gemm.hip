@@ -68,34 +68,33 @@ template <> struct Mma32<LSQ_F16> {
   }
 };
 
-// Byte b of a dword as an unsigned value, as fp32 (v_cvt_f32_ubyte{0..3}).
-__device__ __forceinline__ float ub(uint32_t w, int b) {
-  return static_cast<float>((w >> (8 * b)) & 0xFFu);
-}
-
 // 8 nibbles of one dword -> 8 values of T for 8 consecutive columns, in column order:
-// value = round_T((u - 8) * s) computed as fma(u, s, -8 s), exact before the rounding
-// (q has 4 significant bits, s 8 or 11). TILED: nibble p holds column tiled_nibble_k(p);
-// canonical: nibble p holds column p.
+// value = round_T((u - 8) * s). The AND-OR (w >> 4p) & 0x000F000F | 0x64006400 turns
+// nibbles p and p + 4 into the fp16 pair (1024 + u_p, 1024 + u_{p+4}); v_fma_mix_f32 then
+// computes (1024 + u) * s - 1032 * s in fp32, which is exact ((1024 + u) has 11
+// significant bits, s at most 11, 1032 = 2^10 + 2^3), and one v_cvt_pk rounds to T.
+// TILED: nibble p holds column tiled_nibble_k(p), so pair p is columns (2p, 2p + 1);
+// canonical: nibble p holds column p, so pair p is columns (p, p + 4). `mask` and
+// `magic` are the two constants, kept in VGPRs (VOP3 takes no literal).
 template <int DT, bool TILED>
-__device__ __forceinline__ u32x4 dequant8_w4(uint32_t w, float s, float ms8) {
-  const uint32_t lo = w & 0x0F0F0F0Fu;         // nibbles 0, 2, 4, 6
-  const uint32_t hi = (w >> 4) & 0x0F0F0F0Fu;  // nibbles 1, 3, 5, 7
-  float c[8];
-  if (TILED) {  // lo bytes -> columns 0, 4, 1, 5; hi bytes -> columns 2, 6, 3, 7
-    c[0] = ub(lo, 0); c[4] = ub(lo, 1); c[1] = ub(lo, 2); c[5] = ub(lo, 3);
-    c[2] = ub(hi, 0); c[6] = ub(hi, 1); c[3] = ub(hi, 2); c[7] = ub(hi, 3);
-  } else {      // byte b holds columns 2b (low nibble) and 2b + 1 (high nibble)
+__device__ __forceinline__ u32x4 dequant8_w4(uint32_t w, float s, float c, uint32_t mask, uint32_t magic) {
+  float v[8];
 #pragma unroll
-    for (int b = 0; b < 4; ++b) {
-      c[2 * b] = ub(lo, b);
-      c[2 * b + 1] = ub(hi, b);
+  for (int p = 0; p < 4; ++p) {
+    const uint32_t pair = ((w >> (4 * p)) & mask) | magic;
+    const float lo = __builtin_fmaf(static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(pair))), s, c);
+    const float hi = __builtin_fmaf(static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(pair >> 16))), s, c);
+    if (TILED) {
+      v[2 * p] = lo;
+      v[2 * p + 1] = hi;
+    } else {
+      v[p] = lo;
+      v[p + 4] = hi;
     }
   }
   u32x4 r;
 #pragma unroll
-  for (int j = 0; j < 4; ++j)
-    r[j] = Mma32<DT>::pack2(fmaf(c[2 * j], s, ms8), fmaf(c[2 * j + 1], s, ms8));
+  for (int j = 0; j < 4; ++j) r[j] = Mma32<DT>::pack2(v[2 * j], v[2 * j + 1]);
   return r;
 }
 
@@ -149,6 +148,9 @@ __global__ void __launch_bounds__(NT) gemm_kernel(LinearArgs p) {
   const int lane = tid & 63;
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wid & 1, wn = wid >> 1;  // wave tile rows wm * 128, columns wn * 64
+  uint32_t nib_mask, nib_magic;
+  asm volatile("v_mov_b32 %0, 0x000f000f" : "=v"(nib_mask));
+  asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(nib_magic));
 
   // K rotation. Workgroups are dealt to the 8 XCDs round-robin and the ~32 resident on
   // one XCD share activation rows; walking K in lockstep, every step's activation tile
@@ -270,7 +272,7 @@ __global__ void __launch_bounds__(NT) gemm_kernel(LinearArgs p) {
     const int row = wrow0;
     unsigned char* addr = ws_at(buf) + row * (BK * 2) + (((4 * wc + u) ^ ((row >> 1) & 7)) << 4);
     if (W4) {
-      *reinterpret_cast<u32x4*>(addr) = dequant8_w4<DT, TILED>(r.w[0][u], sf[0], -8.f * sf[0]);
+      *reinterpret_cast<u32x4*>(addr) = dequant8_w4<DT, TILED>(r.w[0][u], sf[0], -1032.f * sf[0], nib_mask, nib_magic);
     } else {
       // 16 columns per load (tiled: the 1 KB half u >> 1; canonical: bytes 16 (u >> 1))
       const u32x4 v = r.w[u >> 1];
