@@ -36,4 +36,9 @@ struct LinearArgs {
 template <int DT>
 int launch_decode(int kind, const LinearArgs& a, hipStream_t s);
 
+// Batched decode, 16 < M <= 64 tokens (activations streamed through LDS in chunks).
+// Same contract as launch_decode.
+template <int DT>
+int launch_decode_mb(int kind, const LinearArgs& a, hipStream_t s);
+
 }  // namespace lsq

@@ -1,0 +1,350 @@
+// Decode-shaped weight-only GEMM for small batches, 16 < M <= 64 tokens (gfx950).
+//
+// GPU form of QuantizedLinear.forward (src/kernels/quantization.py:129-141) for batched
+// decode steps. Same weight stream and in-register unpack as the M <= 16 kernel
+// (lsq_decode.hip): each wave owns one 16-row tile of W and all of K, streams its
+// tiles once from HBM through a ring of kD k-tile steps in registers, and turns them into
+// the B operands of v_mfma_f32_16x16x32. What changes is the activation side: 17..64
+// tokens of a 3584..4096-column layer no longer fit in LDS at once, so the workgroup
+// streams x through LDS in chunks of kCT k tiles, double-buffered, with one barrier
+// per chunk. Every token block of 16 (MB of them) reuses each unpacked weight operand,
+// so the unpack cost per weight is shared by up to 64 tokens.
+//
+// Chunk pipeline (chunk c lives in LDS buffer c & 1). At the start of chunk c all
+// waves pass one barrier (chunk c is visible, chunk c - 1 is finished); the workgroup
+// then writes chunk c + 1, already in registers, into the other buffer with its
+// per-(k tile, token) activation sums, issues the global loads of chunk c + 2, and
+// computes chunk c. The activation loads of a chunk are issued a whole chunk before
+// they are needed, and the weight loads issued after them stay in flight across the
+// wait.
+//
+// Numerics as in lsq_decode.hip: weight products are exact in the fp32 accumulators; the
+// INT4 nibble bias (and the magic exponent) is removed per 128-column tile with the
+// activation sums, group scales are applied per tile in fp32, per-channel scales and
+// the bias at the end, then one rounding to T.
+
+#include "lsq_mfma16.h"
+
+#include <atomic>
+#include <cstdlib>
+
+namespace lsq {
+namespace {
+
+constexpr int kCT = 2;  // k tiles per activation chunk
+constexpr int kD = 8;   // weight ring depth in k tiles; a multiple of 2 * kCT
+
+// LDS layout shared by kernel and host: two activation chunk buffers (mp rows of
+// kCT * 128 columns, row stride ldxs elements), their per-(k tile, token) sums, the
+// workgroup's scales and bias as fp32 rounded to the activation type.
+struct MbLds {
+  int64_t xs, xsum, ss, sb, total;
+  int ldxs;
+};
+
+__host__ __device__ inline MbLds mb_lds(int mp, int rows, int64_t ngs) {
+  MbLds l;
+  l.ldxs = kCT * kTileK + 8;  // +8: rows r and r + 1 start 4 banks apart
+  l.xs = 0;
+  l.xsum = align16(int64_t(2) * mp * l.ldxs * 2);
+  l.ss = l.xsum + int64_t(2) * kCT * mp * 4;
+  l.sb = l.ss + align16(rows * ngs * 4);
+  l.total = l.sb + align16(rows * 4);
+  return l;
+}
+
+template <int DT, int KIND, int MB, int RG, bool GROUPED>
+__global__ void __launch_bounds__(64 * RG) decode_mb_kernel(LinearArgs p) {
+  constexpr int NT = 64 * RG;
+  constexpr bool W4 = KIND == kW4Tiled || KIND == kW4Canon;
+  constexpr bool TILED = KIND == kW4Tiled || KIND == kW8Tiled;
+  constexpr int LPT = W4 ? 1 : 2;  // 16-byte weight loads per lane per k tile
+  constexpr int kTileB = W4 ? kTileBytes : kTileBytes8;
+  constexpr int kStride = TILED ? kTileB : (W4 ? kTileK / 2 : kTileK);
+  constexpr int kHalf = KIND == kW8Tiled ? kTileBytes8 / 2 : 64;
+  constexpr int MP = 16 * MB;                 // token rows held per chunk (zero padded)
+  constexpr int ROWS = RG * kTileN;
+  constexpr int PIECES = kCT * kTileK / 8;    // 16-byte pieces per chunk row
+  constexpr int XL = MP * PIECES / NT;        // activation loads per thread per chunk
+  static_assert(MP * PIECES % NT == 0, "chunk pieces must split evenly over the threads");
+  static_assert(kD % (2 * kCT) == 0, "the ring block must hold whole pairs of chunks");
+  extern __shared__ __align__(16) unsigned char smem[];
+  using S = typename Act<DT>::storage;
+
+  const int M = static_cast<int>(p.M), N = static_cast<int>(p.N), K = static_cast<int>(p.K);
+  const int nkt = K / kTileK;
+  const int nrt = (N + kTileN - 1) / kTileN;
+  const int ng = static_cast<int>(p.ngroups);
+  const int ngs = GROUPED ? ng : 1;
+  const int gtiles = static_cast<int>(p.group / kTileK);
+  const int nchunks = (nkt + kCT - 1) / kCT;
+
+  const MbLds L = mb_lds(MP, ROWS, ngs);
+  const int ldxs = L.ldxs;
+  uint16_t* xs = reinterpret_cast<uint16_t*>(smem + L.xs);
+  float* xsum = reinterpret_cast<float*>(smem + L.xsum);
+  float* ss = reinterpret_cast<float*>(smem + L.ss);
+  float* sb = reinterpret_cast<float*>(smem + L.sb);
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);  // row tile within the workgroup
+  const int r = lane & 15;
+  const int q = lane >> 4;
+  const int rt_wg = blockIdx.x * RG;
+  const int row0 = rt_wg * kTileN;
+  const int rows_valid = min(ROWS, N - row0);
+
+  // ---- descriptors over what this workgroup reads
+  const int es_s = p.scale_dt == LSQ_F32 ? 4 : 2;
+  const int es_b = p.bias_dt == LSQ_F32 ? 4 : 2;
+  const rsrc_t rx = make_rsrc(p.x, static_cast<uint32_t>(((M - 1) * p.ldx + K) * 2));
+  const uint8_t* wbase;
+  uint32_t wbytes;
+  if (TILED) {
+    wbase = p.w + static_cast<int64_t>(rt_wg) * nkt * kTileB;
+    wbytes = static_cast<uint32_t>(min(RG, nrt - rt_wg) * nkt * kTileB);
+  } else {
+    const int row_bytes = W4 ? K / 2 : K;
+    wbase = p.w + static_cast<int64_t>(row0) * row_bytes;
+    wbytes = static_cast<uint32_t>(rows_valid * row_bytes);
+  }
+  const rsrc_t rw = make_rsrc(wbase, wbytes);
+  const int nsc = rows_valid * ngs;
+  // (the dword holding the last 16-bit element may reach 2 bytes past the array; an
+  // aligned dword never crosses a page)
+  const rsrc_t rs = make_rsrc(static_cast<const uint8_t*>(p.scale) + static_cast<int64_t>(row0) * ngs * es_s,
+                              static_cast<uint32_t>((nsc * es_s + 3) & ~3));
+  const rsrc_t rb = make_rsrc(p.bias ? static_cast<const uint8_t*>(p.bias) + static_cast<int64_t>(row0) * es_b
+                                     : static_cast<const uint8_t*>(p.scale),
+                              p.bias ? static_cast<uint32_t>((rows_valid * es_b + 3) & ~3) : 0u);
+
+  // ---- scales and bias of the workgroup's rows -> LDS, as round_T fp32
+  for (int t = tid; t < nsc; t += NT) {
+    const uint32_t eb = static_cast<uint32_t>(t * es_s);
+    ss[t] = Act<DT>::round(dword_elem(bload4(rs, eb & ~3u), (eb >> 1) & 1, p.scale_dt));
+  }
+  if (p.bias) {
+    for (int t = tid; t < rows_valid; t += NT) {
+      const uint32_t eb = static_cast<uint32_t>(t * es_b);
+      sb[t] = Act<DT>::round(dword_elem(bload4(rb, eb & ~3u), (eb >> 1) & 1, p.bias_dt));
+    }
+  }
+
+  // ---- activation chunks: piece i of chunk c is token i / PIECES, columns
+  // c * kCT * 128 + 8 (i % PIECES) .. +7; tokens >= M and columns >= K read as zeros.
+  u32x4 xr[XL];
+  auto load_x = [&](int c) {
+#pragma unroll
+    for (int u = 0; u < XL; ++u) {
+      const int i = u * NT + tid;
+      const int m = i / PIECES;
+      const int k = c * (kCT * kTileK) + (i - m * PIECES) * 8;
+      xr[u] = bload16<0>(rx, (m < M && k < K && c < nchunks)
+                                  ? static_cast<uint32_t>((m * p.ldx + k) * 2) : kOOB);
+    }
+  };
+  auto put_x = [&](int b) {
+    uint16_t* xb = xs + b * MP * ldxs;
+    float* xsb = xsum + b * kCT * MP;
+#pragma unroll
+    for (int u = 0; u < XL; ++u) {
+      const int i = u * NT + tid;
+      const int m = i / PIECES;
+      const int pc = i - m * PIECES;
+      *reinterpret_cast<u32x4*>(xb + m * ldxs + pc * 8) = KIND == kW4Canon ? permute_canon(xr[u]) : xr[u];
+      if (W4) {
+        float sum = 0.f;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sum += Mma<DT>::lo(xr[u][e]) + Mma<DT>::hi(xr[u][e]);
+        // the 16 pieces of one (token, k tile) sit in 16 consecutive lanes
+        sum += __shfl_xor(sum, 1, 64);
+        sum += __shfl_xor(sum, 2, 64);
+        sum += __shfl_xor(sum, 4, 64);
+        sum += __shfl_xor(sum, 8, 64);
+        if ((lane & 15) == 0) xsb[(pc / 16) * MP + m] = sum;
+      }
+    }
+  };
+
+  // ---- weight ring: kD k-tile steps per wave; refills past the end are out-of-range
+  // loads (no memory traffic), so every load is unconditional.
+  u32x4 wbuf[kD][LPT];
+  auto issue = [&](u32x4 (&wv)[LPT], int st) {
+    const bool real = st < nkt;
+    const uint32_t off = TILED ? static_cast<uint32_t>((wid * nkt + st) * kTileB + lane * 16)
+                               : static_cast<uint32_t>((wid * kTileN + r) * (W4 ? K / 2 : K) +
+                                                       st * kStride + q * 16);
+    wv[0] = bload16<kNT>(rw, real ? off : kOOB);
+    if (LPT == 2) wv[LPT - 1] = bload16<kNT>(rw, real ? off + kHalf : kOOB);
+  };
+
+  load_x(0);
+  put_x(0);
+  load_x(1);
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int s = 0; s < kD; ++s) issue(wbuf[s], s);
+
+  f32x4 acc[MB];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) acc[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  uint32_t nib_mask, magic;  // INT4 unpack constants in registers (VOP3 takes no literal)
+  asm volatile("v_mov_b32 %0, 0x000f000f" : "=v"(nib_mask));
+  asm volatile("v_mov_b32 %0, %1" : "=v"(magic) : "i"(Mma<DT>::kMagic));
+  const float* srow = ss + (wid * kTileN + r) * ngs;
+
+  const int nblocks = (nkt + kD - 1) / kD;
+  for (int b = 0; b < nblocks; ++b) {
+#pragma unroll
+    for (int s = 0; s < kD; ++s) {
+      const int st = b * kD + s;
+      if (s % kCT == 0) {
+        const int c = st / kCT;
+        if (c < nchunks) {  // uniform
+          lds_barrier();    // chunk c visible to all waves; chunk c - 1 finished by all
+          if (c + 1 < nchunks) {
+            put_x((c + 1) & 1);
+            load_x(c + 2);
+          }
+        }
+      }
+      if (st < nkt) {  // uniform
+        const int kBuf = (s / kCT) & 1;  // (b * kD + s) / kCT has the parity of s / kCT
+        const uint16_t* xb = xs + kBuf * MP * ldxs + (s % kCT) * kTileK;
+        const float* xsb = xsum + kBuf * kCT * MP + (s % kCT) * MP;
+        u32x4 bb[4];
+#pragma unroll
+        for (int d = 0; d < 4; ++d)
+          bb[d] = W4 ? unpack_w4(wbuf[s][0][d], nib_mask, magic)
+                     : convert_w8<DT>(wbuf[s][d >> 1][2 * (d & 1)], wbuf[s][d >> 1][2 * (d & 1) + 1]);
+        float sc = 1.f;
+        if (GROUPED) sc = srow[gtiles == 1 ? st : st / gtiles];
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) {
+          u32x4 a[4];
+#pragma unroll
+          for (int d = 0; d < 4; ++d)
+            a[d] = *reinterpret_cast<const u32x4*>(xb + (16 * mb + r) * ldxs + a_col<KIND>(q, d));
+          if (W4) {
+            f32x4 dacc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int d = 0; d < 4; ++d) dacc = Mma<DT>::mma(a[d], bb[d], dacc);
+            const f32x4 xo = *reinterpret_cast<const f32x4*>(xsb + 16 * mb + 4 * q);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const float v = fmaf(-Mma<DT>::kOff4, xo[e], dacc[e]);
+              acc[mb][e] = GROUPED ? fmaf(sc, v, acc[mb][e]) : acc[mb][e] + v;
+            }
+          } else {
+#pragma unroll
+            for (int d = 0; d < 4; ++d) acc[mb] = Mma<DT>::mma(a[d], bb[d], acc[mb]);
+          }
+        }
+      }
+      issue(wbuf[s], st + kD);
+    }
+  }
+
+  // ---- epilogue: per-channel scale, bias, one rounding to T
+  S* y = static_cast<S*>(p.y);
+  const int rl = wid * kTileN + r;
+  const int n = row0 + rl;
+  if (n < N) {
+    const float sc = GROUPED ? 1.f : ss[rl];
+    const float bias = p.bias ? sb[rl] : 0.f;
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int m = 16 * mb + 4 * q + e;
+        if (m < M) {
+          float v = acc[mb][e];
+          if (!GROUPED) v *= sc;
+          y[static_cast<int64_t>(m) * p.ldy + n] = Act<DT>::from_f32(v + bias);
+        }
+      }
+  }
+}
+
+// ------------------------------------------------------------------ launch
+
+int mb_max_lds() {
+  static int v = -1;
+  if (v < 0) {
+    int dev = 0, x = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&x, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess)
+      x = 64 * 1024;
+    v = x;
+  }
+  return v;
+}
+
+// Waves per workgroup: 8 (128 rows share one pass over x) when that still leaves enough
+// workgroups, else 4. LSQ_DECODE_MB_RG=4|8 overrides (tuning sweeps); read once.
+int pick_rg(int64_t N) {
+  static int env = -1;
+  if (env < 0) {
+    const char* e = std::getenv("LSQ_DECODE_MB_RG");
+    env = e ? std::atoi(e) : 0;
+  }
+  if (env == 4 || env == 8) return env;
+  const int64_t nrt = (N + kTileN - 1) / kTileN;
+  return nrt >= 8 * 128 ? 8 : 4;
+}
+
+template <int DT, int KIND, int MB, int RG, bool GROUPED>
+int launch_one(const LinearArgs& a, hipStream_t s) {
+  const MbLds L = mb_lds(16 * MB, RG * kTileN, GROUPED ? a.ngroups : 1);
+  if (L.total > mb_max_lds()) return LSQ_E_LAYOUT;
+  auto kern = decode_mb_kernel<DT, KIND, MB, RG, GROUPED>;
+  if (L.total > 64 * 1024) {
+    static std::atomic<int> attr_set{0};
+    if (!attr_set.load(std::memory_order_acquire)) {
+      const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, mb_max_lds());
+      if (e != hipSuccess) return static_cast<int>(e);
+      attr_set.store(1, std::memory_order_release);
+    }
+  }
+  const int64_t nrt = (a.N + kTileN - 1) / kTileN;
+  const dim3 grid(static_cast<unsigned>((nrt + RG - 1) / RG));
+  kern<<<grid, dim3(64 * RG), static_cast<size_t>(L.total), s>>>(a);
+  return static_cast<int>(hipGetLastError());
+}
+
+template <int DT, int KIND, bool GROUPED>
+int launch_kind(const LinearArgs& a, hipStream_t s) {
+  const int rg = pick_rg(a.N);
+  if (a.M <= 32) return rg == 8 ? launch_one<DT, KIND, 2, 8, GROUPED>(a, s) : launch_one<DT, KIND, 2, 4, GROUPED>(a, s);
+  return rg == 8 ? launch_one<DT, KIND, 4, 8, GROUPED>(a, s) : launch_one<DT, KIND, 4, 4, GROUPED>(a, s);
+}
+
+}  // namespace
+
+template <int DT>
+int launch_decode_mb(int kind, const LinearArgs& a, hipStream_t s) {
+  if (a.M < 1 || a.M > 64 || a.K % kTileK != 0 || a.K < kTileK) return LSQ_E_LAYOUT;
+  const bool grouped = kind != kW8 && kind != kW8Tiled && a.group < a.K;
+  if (grouped && a.group % kTileK != 0) return LSQ_E_LAYOUT;
+  auto aligned4 = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 3) == 0; };
+  if (!aligned4(a.scale) || (a.bias && !aligned4(a.bias))) return LSQ_E_LAYOUT;
+  // 32-bit descriptor ranges: activations, and the weight rows of one workgroup
+  if (((a.M - 1) * a.ldx + a.K) * 2 >= (int64_t(1) << 31)) return LSQ_E_LAYOUT;
+  if (int64_t(128) * a.K >= (int64_t(1) << 31)) return LSQ_E_LAYOUT;
+  switch (kind) {
+    case kW8: return launch_kind<DT, kW8, false>(a, s);
+    case kW8Tiled: return launch_kind<DT, kW8Tiled, false>(a, s);
+    case kW4Tiled:
+      return grouped ? launch_kind<DT, kW4Tiled, true>(a, s) : launch_kind<DT, kW4Tiled, false>(a, s);
+    case kW4Canon:
+      return grouped ? launch_kind<DT, kW4Canon, true>(a, s) : launch_kind<DT, kW4Canon, false>(a, s);
+    default: return LSQ_E_LAYOUT;
+  }
+}
+
+template int launch_decode_mb<LSQ_BF16>(int, const LinearArgs&, hipStream_t);
+template int launch_decode_mb<LSQ_F16>(int, const LinearArgs&, hipStream_t);
+
+}  // namespace lsq

@@ -113,7 +113,10 @@ static int dispatch(bool w4, const void* x, int64_t ldx, const uint8_t* w, const
       LinearArgs a{x, ldx, tiled ? tiled : w, scale, scale_dt, bias, bias_dt, y, ldy,
                    M, N, K, group, ng};
       const int kind = w4 ? (tiled ? kW4Tiled : kW4Canon) : (tiled ? kW8Tiled : kW8);
-      const int rc = M <= 16 ? launch_decode<DT>(kind, a, s) : launch_gemm<DT>(kind, a, s);
+      int rc = LSQ_E_LAYOUT;
+      if (M <= 16) rc = launch_decode<DT>(kind, a, s);
+      else if (M <= 64) rc = launch_decode_mb<DT>(kind, a, s);
+      if (rc == LSQ_E_LAYOUT && M > 16) rc = launch_gemm<DT>(kind, a, s);
       if (rc != LSQ_E_LAYOUT) return rc;
     }
   }

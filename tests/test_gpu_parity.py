@@ -268,6 +268,30 @@ def test_odd_shapes(kind, n, k, group):
         _check_layer(kind, n, k, 5, group=g, dtype=dtype, seed=n + k)
 
 
+@pytest.mark.parametrize("layout", ["tiled", "canonical"])
+@pytest.mark.parametrize("kind,group", [("int8", None), ("int4", 128), ("int4", 896)])
+def test_batched_decode_edges(layout, kind, group, monkeypatch):
+    """Batched decode (17..64 tokens): a partial last workgroup (N = 272 = 17 row tiles),
+    an odd number of k tiles (K = 896, so the last activation chunk is half empty), a
+    single k tile (K = 128), bias, both activation types, group-128 and per-channel INT4."""
+    monkeypatch.setenv("LSQ_WEIGHT_LAYOUT", layout)
+    g = group if group is not None else 128
+    for m in (17, 40, 64):
+        for dtype in (torch.bfloat16, torch.float16):
+            _check_layer(kind, 272, 896, m, group=g, dtype=dtype, bias=True, seed=m)
+    _check_layer(kind, 80, 128, 33, group=128, bias=True, seed=3)
+
+
+def test_batched_decode_strided_x():
+    p, s, _ = bench.make_int4(256, 512, 40)
+    ql = _layer("int4", p, s, 512, 128)
+    wide = torch.randn(40, 640, dtype=torch.bfloat16, device=DEV)
+    with torch.no_grad():
+        y1 = ql(wide[:, :512])
+        y2 = ql(wide[:, :512].contiguous())
+    assert torch.equal(y1, y2)
+
+
 def test_fp16_decode_paths():
     for kind in ("int8", "int4"):
         for m in (1, 16, 40):
