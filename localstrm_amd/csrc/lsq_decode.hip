@@ -299,38 +299,50 @@ __global__ void __launch_bounds__(64 * RG * KS) decode_kernel(LinearArgs p) {
 #pragma unroll
     for (int s = 0; s < D; ++s) {
       const int st = b * D + s;
-      if (st < nsteps) {  // uniform; dead steps of the last block only refill below
-        const int kt = k_lo + st;
-        u32x4 a[4];
+      // Order within a step: LDS reads (independent of the weights, so they overlap the
+      // wait for this step's weights), unpack, refill of the ring slot just freed, then
+      // the MFMAs and the scale math, so that the next load leaves before the MFMA chain.
+      const bool live = st < nsteps;  // uniform; dead steps of the last block only refill
+      const int kt = k_lo + st;
+      u32x4 a[4];
+      f32x4 xo = f32x4{0.f, 0.f, 0.f, 0.f};
+      float scg[RT];
+      u32x4 bb[RT][4];
+      if (live) {
 #pragma unroll
         for (int d = 0; d < 4; ++d)
           a[d] = *reinterpret_cast<const u32x4*>(xrow + kt * kTileK + a_col<KIND>(q, d));
-        f32x4 xo = f32x4{0.f, 0.f, 0.f, 0.f};
-        if (W4 && GROUPED) xo = *reinterpret_cast<const f32x4*>(xsum + kt * 16 + 4 * q);
+        if (W4 && GROUPED) {
+          xo = *reinterpret_cast<const f32x4*>(xsum + kt * 16 + 4 * q);
+          const int g = gtiles == 1 ? kt : kt / gtiles;
 #pragma unroll
-        for (int i = 0; i < RT; ++i) {
-          u32x4 bb[4];
+          for (int i = 0; i < RT; ++i) scg[i] = ss[((rtl + i) * kTileN + r) * ngs + g];
+        }
+#pragma unroll
+        for (int i = 0; i < RT; ++i)
 #pragma unroll
           for (int d = 0; d < 4; ++d)
-            bb[d] = W4 ? unpack_w4(wbuf[s][i][0][d], nib_mask, magic)
-                       : convert_w8<DT>(wbuf[s][i][d >> 1][2 * (d & 1)],
-                                        wbuf[s][i][d >> 1][2 * (d & 1) + 1]);
+            bb[i][d] = W4 ? unpack_w4(wbuf[s][i][0][d], nib_mask, magic)
+                          : convert_w8<DT>(wbuf[s][i][d >> 1][2 * (d & 1)],
+                                           wbuf[s][i][d >> 1][2 * (d & 1) + 1]);
+      }
+      issue(wbuf[s], st + D);
+      if (live) {
+#pragma unroll
+        for (int i = 0; i < RT; ++i) {
           if (W4 && GROUPED) {
             f32x4 dacc = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int d = 0; d < 4; ++d) dacc = Mma<DT>::mma(a[d], bb[d], dacc);
-            const int g = gtiles == 1 ? kt : kt / gtiles;
-            const float sc = ss[((rtl + i) * kTileN + r) * ngs + g];
+            for (int d = 0; d < 4; ++d) dacc = Mma<DT>::mma(a[d], bb[i][d], dacc);
 #pragma unroll
             for (int e = 0; e < 4; ++e)
-              acc[i][e] = fmaf(sc, fmaf(-Mma<DT>::kOff4, xo[e], dacc[e]), acc[i][e]);
+              acc[i][e] = fmaf(scg[i], fmaf(-Mma<DT>::kOff4, xo[e], dacc[e]), acc[i][e]);
           } else {
 #pragma unroll
-            for (int d = 0; d < 4; ++d) acc[i] = Mma<DT>::mma(a[d], bb[d], acc[i]);
+            for (int d = 0; d < 4; ++d) acc[i] = Mma<DT>::mma(a[d], bb[i][d], acc[i]);
           }
         }
       }
-      issue(wbuf[s], st + D);
     }
   }
 

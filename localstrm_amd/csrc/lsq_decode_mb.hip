@@ -209,40 +209,56 @@ __global__ void __launch_bounds__(64 * RG) decode_mb_kernel(LinearArgs p) {
           }
         }
       }
-      if (st < nkt) {  // uniform
-        const int kBuf = (s / kCT) & 1;  // (b * kD + s) / kCT has the parity of s / kCT
-        const uint16_t* xb = xs + kBuf * MP * ldxs + (s % kCT) * kTileK;
-        const float* xsb = xsum + kBuf * kCT * MP + (s % kCT) * MP;
-        u32x4 bb[4];
+      // Per k tile: LDS reads first (they overlap the wait for the weights), unpack,
+      // refill of the ring slot just freed, then MB interleaved MFMA chains.
+      const bool live = st < nkt;  // uniform
+      const int kBuf = (s / kCT) & 1;  // (b * kD + s) / kCT has the parity of s / kCT
+      const uint16_t* xb = xs + kBuf * MP * ldxs + (s % kCT) * kTileK;
+      const float* xsb = xsum + kBuf * kCT * MP + (s % kCT) * MP;
+      u32x4 a[MB][4];
+      f32x4 xo[MB];
+      float sc = 1.f;
+      u32x4 bb[4];
+      if (live) {
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+          for (int d = 0; d < 4; ++d)
+            a[mb][d] = *reinterpret_cast<const u32x4*>(xb + (16 * mb + r) * ldxs + a_col<KIND>(q, d));
+        if (W4) {
+#pragma unroll
+          for (int mb = 0; mb < MB; ++mb) xo[mb] = *reinterpret_cast<const f32x4*>(xsb + 16 * mb + 4 * q);
+        }
+        if (GROUPED) sc = srow[gtiles == 1 ? st : st / gtiles];
 #pragma unroll
         for (int d = 0; d < 4; ++d)
           bb[d] = W4 ? unpack_w4(wbuf[s][0][d], nib_mask, magic)
                      : convert_w8<DT>(wbuf[s][d >> 1][2 * (d & 1)], wbuf[s][d >> 1][2 * (d & 1) + 1]);
-        float sc = 1.f;
-        if (GROUPED) sc = srow[gtiles == 1 ? st : st / gtiles];
-#pragma unroll
-        for (int mb = 0; mb < MB; ++mb) {
-          u32x4 a[4];
-#pragma unroll
-          for (int d = 0; d < 4; ++d)
-            a[d] = *reinterpret_cast<const u32x4*>(xb + (16 * mb + r) * ldxs + a_col<KIND>(q, d));
-          if (W4) {
-            f32x4 dacc = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int d = 0; d < 4; ++d) dacc = Mma<DT>::mma(a[d], bb[d], dacc);
-            const f32x4 xo = *reinterpret_cast<const f32x4*>(xsb + 16 * mb + 4 * q);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              const float v = fmaf(-Mma<DT>::kOff4, xo[e], dacc[e]);
-              acc[mb][e] = GROUPED ? fmaf(sc, v, acc[mb][e]) : acc[mb][e] + v;
-            }
-          } else {
-#pragma unroll
-            for (int d = 0; d < 4; ++d) acc[mb] = Mma<DT>::mma(a[d], bb[d], acc[mb]);
-          }
-        }
       }
       issue(wbuf[s], st + kD);
+      if (live) {
+        if (W4) {
+          f32x4 dacc[MB];
+#pragma unroll
+          for (int mb = 0; mb < MB; ++mb) dacc[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int d = 0; d < 4; ++d)
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb) dacc[mb] = Mma<DT>::mma(a[mb][d], bb[d], dacc[mb]);
+#pragma unroll
+          for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const float v = fmaf(-Mma<DT>::kOff4, xo[mb][e], dacc[mb][e]);
+              acc[mb][e] = GROUPED ? fmaf(sc, v, acc[mb][e]) : acc[mb][e] + v;
+            }
+        } else {
+#pragma unroll
+          for (int d = 0; d < 4; ++d)
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb) acc[mb] = Mma<DT>::mma(a[mb][d], bb[d], acc[mb]);
+        }
+      }
     }
   }
 
