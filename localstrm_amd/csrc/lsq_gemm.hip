@@ -31,6 +31,7 @@
 #include "lsq_gemm.h"
 
 #include <atomic>
+#include <cstdlib>
 
 namespace lsq {
 namespace {
@@ -391,8 +392,258 @@ __global__ void __launch_bounds__(NT) gemm_kernel(LinearArgs p) {
     }
 }
 
+// ---------------------------------------------------------------------------------------
+// Register-weight variant. A workgroup of 4 waves computes a 128 x 256 tile; two such
+// workgroups share a CU (one wave of each per SIMD), each with its own barrier, so one
+// workgroup's barrier and LDS latency bubbles are filled by the other's MFMAs. Wave w
+// owns columns [64 w, 64 w + 64) for all 128 rows (4 x 2 blocks of 32 x 32). Only the
+// activations go through LDS (two 16 KB stages, DMA one step ahead); each wave loads its
+// own 64 weight rows straight into registers in MFMA operand order (three steps in
+// flight) and dequantizes them right before use, so weight tiles never touch LDS.
+// K order inside a step: lane l at 16-column sub-step kk multiplies columns
+// 32 (l >> 5) + 8 kk .. +7 (the same permutation on both operands), which makes each
+// lane's weights one contiguous 32-column chunk per step.
+constexpr int RBM = 128, RBN = 256, RNT = 256;
+constexpr int RFM = RBM / 32, RFN = 2;
+constexpr int kRLdsBytes = 2 * RBM * BK * 2;
+
+template <int DT, int KIND, bool GROUPED>
+__global__ void __launch_bounds__(RNT, 2) gemm_rw_kernel(LinearArgs p) {
+  constexpr bool W4 = KIND == kW4Tiled || KIND == kW4Canon;
+  constexpr bool TILED = KIND == kW4Tiled || KIND == kW8Tiled;
+  constexpr int WLB = W4 ? 1 : 2;  // 16-byte loads per lane per 32-row block per step
+  extern __shared__ __align__(16) unsigned char smem[];
+  using S = typename Act<DT>::storage;
+
+  const int M = static_cast<int>(p.M), N = static_cast<int>(p.N), K = static_cast<int>(p.K);
+  const int nsteps = K / BK;
+  const int nkt = K / kTileK;
+  const int ng = static_cast<int>(p.ngroups);
+  const int group = static_cast<int>(p.group);
+  const int mtiles = (M + RBM - 1) / RBM;
+  const int mt = blockIdx.x % mtiles;  // M fastest: consecutive workgroups share W tiles
+  const int nt = blockIdx.x / mtiles;
+  const int m0 = mt * RBM, n0 = nt * RBN;
+  const int rows_m = min(RBM, M - m0);
+  const int rows_n = min(RBN, N - n0);
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int h = lane >> 5;  // which 32-column half of the step this lane multiplies
+  uint32_t nib_mask, nib_magic;
+  asm volatile("v_mov_b32 %0, 0x000f000f" : "=v"(nib_mask));
+  asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(nib_magic));
+
+  // K rotation per workgroup (see gemm_kernel): spreads first-touch misses over K.
+  const int rot = (((blockIdx.x >> 3) & 31) * nsteps) >> 5;
+  auto gstep = [&](int st) { const int g = st + rot; return g >= nsteps ? g - nsteps : g; };
+
+  // ---- descriptors
+  const rsrc_t rx = make_rsrc(static_cast<const uint16_t*>(p.x) + static_cast<int64_t>(m0) * p.ldx,
+                              static_cast<uint32_t>(((rows_m - 1) * p.ldx + K) * 2));
+  const int tb = W4 ? kTileBytes : kTileBytes8;
+  const uint8_t* wbase;
+  uint32_t wbytes;
+  if (TILED) {
+    const int rt0 = n0 / kTileN;
+    const int nrt = (N + kTileN - 1) / kTileN;
+    wbase = p.w + static_cast<int64_t>(rt0) * nkt * tb;
+    wbytes = static_cast<uint32_t>(min(RBN / kTileN, nrt - rt0) * nkt * tb);
+  } else {
+    const int rb = W4 ? K / 2 : K;
+    wbase = p.w + static_cast<int64_t>(n0) * rb;
+    wbytes = static_cast<uint32_t>(rows_n * rb);
+  }
+  const rsrc_t rw = make_rsrc(wbase, wbytes);
+  const int es_s = p.scale_dt == LSQ_F32 ? 4 : 2;
+  const int ngs = GROUPED ? ng : 1;
+  const rsrc_t rs = make_rsrc(static_cast<const uint8_t*>(p.scale) + static_cast<int64_t>(n0) * ngs * es_s,
+                              static_cast<uint32_t>((rows_n * ngs * es_s + 3) & ~3));
+
+  // ---- activations: two LDS stages of 128 rows x 64 columns, chunk c of row r at
+  // position c ^ ((r >> 1) & 7); DMA as in gemm_kernel (4 x 1 KB per wave per step).
+  constexpr int kStage = RBM * BK * 2;
+  uint32_t x_lane_off[2];
+#pragma unroll
+  for (int v = 0; v < 2; ++v)
+    x_lane_off[v] = static_cast<uint32_t>(
+        ((lane >> 3) * p.ldx + 8 * ((lane & 7) ^ ((v << 2) | (lane >> 4)))) * 2);
+  auto issue_x = [&](int st, int buf) {
+    unsigned char* dst = smem + buf * kStage;
+#pragma unroll
+    for (int b = 0; b < RBM / 8 / (RNT / 64); ++b) {
+      const int rb = (wid * (RBM / 8 / (RNT / 64)) + b) * 8;  // (rb >> 1) & 4 == (b & 1) * 4
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rx, (__attribute__((address_space(3))) void*)(dst + rb * BK * 2), 16,
+          x_lane_off[b & 1], static_cast<int>((rb * p.ldx + gstep(st) * BK) * 2), 0, 0);
+    }
+  };
+
+  // ---- weights: lane's row of block j is tile-local row lr[j]; per step it reads the
+  // 32-column chunk h of the step (INT8: two 16-byte loads).
+  uint32_t woff[RFN];
+  int lr[RFN];
+#pragma unroll
+  for (int j = 0; j < RFN; ++j) {
+    lr[j] = 64 * wid + 32 * j + (lane & 31);
+    woff[j] = TILED ? static_cast<uint32_t>((lr[j] >> 4) * nkt * tb + ((lr[j] & 15) + 16 * h) * 16)
+                    : static_cast<uint32_t>(lr[j] * (W4 ? K / 2 : K) + (W4 ? 16 : 32) * h);
+  }
+  struct WSet {
+    u32x4 w[RFN][WLB];
+    uint32_t s[RFN];
+  };
+  auto issue_w = [&](int st, WSet& r) {
+    const bool real = st < nsteps;
+    const int gs = gstep(min(st, nsteps - 1));
+    const uint32_t kw = TILED ? static_cast<uint32_t>((gs >> 1) * tb + (gs & 1) * 512)
+                              : static_cast<uint32_t>(gs * (W4 ? BK / 2 : BK));
+#pragma unroll
+    for (int j = 0; j < RFN; ++j)
+#pragma unroll
+      for (int l = 0; l < WLB; ++l)
+        r.w[j][l] = bload16<kNT>(rw, real ? woff[j] + kw + l * (TILED ? kTileBytes8 / 2 : 16) : kOOB);
+    if (GROUPED) {
+      const int g = (gs * BK) / group;
+#pragma unroll
+      for (int j = 0; j < RFN; ++j)
+        r.s[j] = bload4(rs, static_cast<uint32_t>((lr[j] * ng + g) * es_s) & ~3u);
+    }
+  };
+
+  // ---- MFMA fragments
+  f32x16 acc[RFM][RFN];
+#pragma unroll
+  for (int i = 0; i < RFM; ++i)
+#pragma unroll
+    for (int j = 0; j < RFN; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+  const int frow = lane & 31;
+  auto frag_off = [&](int kk) { return frow * (BK * 2) + (((4 * h + kk) ^ ((frow >> 1) & 7)) << 4); };
+
+  auto step = [&](int st, const WSet& cur, WSet& nxt2) {
+    const int buf = st & 1;
+    const unsigned char* xb = smem + buf * kStage;
+    u32x4 a[2][RFM];
+    auto load_a = [&](int kk, u32x4 (&aa)[RFM]) {
+      const int off = frag_off(kk);
+#pragma unroll
+      for (int i = 0; i < RFM; ++i) aa[i] = *reinterpret_cast<const u32x4*>(xb + 32 * i * (BK * 2) + off);
+    };
+    load_a(0, a[0]);
+    issue_x(st + 1, buf ^ 1);
+    issue_w(st + 2, nxt2);
+    float sf[RFN], cf[RFN];
+#pragma unroll
+    for (int j = 0; j < RFN; ++j) {
+      sf[j] = 1.f;
+      if (GROUPED) {
+        const int g = (gstep(min(st, nsteps - 1)) * BK) / group;
+        const uint32_t eb = static_cast<uint32_t>((lr[j] * ng + g) * es_s);
+        sf[j] = Act<DT>::round(dword_elem(cur.s[j], (eb >> 1) & 1, p.scale_dt));
+      }
+      cf[j] = -1032.f * sf[j];
+    }
+    // B operands one sub-step ahead: the dequantization of sub-step kk + 1 is independent
+    // of the MFMAs of sub-step kk, so the two interleave.
+    u32x4 b[2][RFN];
+    auto dequant = [&](int kk, u32x4 (&bb)[RFN]) {
+#pragma unroll
+      for (int j = 0; j < RFN; ++j)
+        bb[j] = W4 ? dequant8_w4<DT, TILED>(cur.w[j][0][kk], sf[j], cf[j], nib_mask, nib_magic)
+                   : convert8_w8<DT>(cur.w[j][kk >> 1][2 * (kk & 1)], cur.w[j][kk >> 1][2 * (kk & 1) + 1]);
+    };
+    dequant(0, b[0]);
+#pragma unroll
+    for (int kk = 0; kk < BK / 16; ++kk) {
+      if (kk + 1 < BK / 16) {
+        load_a(kk + 1, a[(kk + 1) & 1]);
+        dequant(kk + 1, b[(kk + 1) & 1]);
+      }
+#pragma unroll
+      for (int i = 0; i < RFM; ++i)
+#pragma unroll
+        for (int j = 0; j < RFN; ++j) acc[i][j] = Mma32<DT>::mma(a[kk & 1][i], b[kk & 1][j], acc[i][j]);
+    }
+    // Before the barrier only this step's activation DMA must have landed: the weight
+    // loads issued after it (for two steps ahead) stay in flight.
+    constexpr int kAfter = RFN * WLB + (GROUPED ? RFN : 0);
+    __builtin_amdgcn_s_waitcnt((kAfter & 15) | (7 << 4) | ((kAfter >> 4) << 14));
+    lds_barrier();
+  };
+
+  WSet r0, r1, r2;
+  issue_x(0, 0);
+  issue_w(0, r0);
+  issue_w(1, r1);
+  {
+    constexpr int kAfter = 2 * (RFN * WLB + (GROUPED ? RFN : 0));
+    __builtin_amdgcn_s_waitcnt((kAfter & 15) | (7 << 4) | ((kAfter >> 4) << 14));
+  }
+  lds_barrier();
+  int st = 0;
+  for (; st + 3 <= nsteps; st += 3) {
+    step(st, r0, r2);
+    step(st + 1, r1, r0);
+    step(st + 2, r2, r1);
+  }
+  if (st < nsteps) step(st, r0, r2);
+  if (st + 1 < nsteps) step(st + 1, r1, r0);
+
+  // ---- epilogue: per-channel scale, bias, one rounding to T
+  S* y = static_cast<S*>(p.y);
+  const int es_b = p.bias_dt == LSQ_F32 ? 4 : 2;
+  const rsrc_t rb = make_rsrc(p.bias ? static_cast<const uint8_t*>(p.bias) + static_cast<int64_t>(n0) * es_b
+                                     : static_cast<const uint8_t*>(p.scale),
+                              p.bias ? static_cast<uint32_t>((rows_n * es_b + 3) & ~3) : 0u);
+  float scn[RFN], bsn[RFN];
+#pragma unroll
+  for (int j = 0; j < RFN; ++j) {
+    if (GROUPED) {
+      scn[j] = 1.f;
+    } else {
+      const uint32_t eb = static_cast<uint32_t>(lr[j] * es_s);
+      scn[j] = Act<DT>::round(dword_elem(bload4(rs, eb & ~3u), (eb >> 1) & 1, p.scale_dt));
+    }
+    const uint32_t ebb = static_cast<uint32_t>(lr[j] * es_b);
+    bsn[j] = p.bias ? Act<DT>::round(dword_elem(bload4(rb, ebb & ~3u), (ebb >> 1) & 1, p.bias_dt)) : 0.f;
+  }
+#pragma unroll
+  for (int i = 0; i < RFM; ++i)
+#pragma unroll
+    for (int j = 0; j < RFN; ++j) {
+      const int n = n0 + lr[j];
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int m = m0 + 32 * i + 8 * (v >> 2) + 4 * h + (v & 3);
+        if (m < M && n < N)
+          y[static_cast<int64_t>(m) * p.ldy + n] = Act<DT>::from_f32(fmaf(acc[i][j][v], scn[j], bsn[j]));
+      }
+    }
+}
+
+template <int DT, int KIND, bool GROUPED>
+int launch_rw(const LinearArgs& a, hipStream_t s) {
+  const int64_t tiles = ((a.M + RBM - 1) / RBM) * ((a.N + RBN - 1) / RBN);
+  gemm_rw_kernel<DT, KIND, GROUPED><<<dim3(static_cast<unsigned>(tiles)), dim3(RNT), kRLdsBytes, s>>>(a);
+  return static_cast<int>(hipGetLastError());
+}
+
+// Which prefill kernel: the register-weight one up to 768 tokens (it launches twice as
+// many workgroups, which decides small M), the LDS-weight one above (fewer dequantized
+// weights per output). LSQ_GEMM=reg|lds forces one (tests, tuning).
+bool use_rw(int64_t M) {
+  const char* e = std::getenv("LSQ_GEMM");
+  if (e && e[0] == 'r') return true;
+  if (e && e[0] == 'l') return false;
+  return M <= 768;
+}
+
 template <int DT, int KIND, bool GROUPED>
 int launch_kind(const LinearArgs& a, hipStream_t s) {
+  if (use_rw(a.M)) return launch_rw<DT, KIND, GROUPED>(a, s);
   auto kern = gemm_kernel<DT, KIND, GROUPED>;
   static std::atomic<int> attr_set{0};
   if (!attr_set.load(std::memory_order_acquire)) {

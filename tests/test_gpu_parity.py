@@ -223,11 +223,14 @@ def test_int4_g128_prefill_config_shape(m, layout, monkeypatch):
     assert err <= REL_TOL
 
 
+@pytest.mark.parametrize("variant", ["reg", "lds"])
 @pytest.mark.parametrize("kind", ["int8", "int4"])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-def test_gemm_edges_bias_and_dtypes(kind, dtype):
-    """GEMM tiles with ragged M and N edges (M=300, N=272 = 256 + 16), bias, both dtypes,
-    per-channel INT8, group-128 INT4, and per-channel INT4."""
+def test_gemm_edges_bias_and_dtypes(kind, dtype, variant, monkeypatch):
+    """Both prefill kernels (register weights, LDS weights) on ragged M and N edges
+    (M=300, N=272 = 256 + 16), bias, both dtypes, per-channel INT8, group-128 INT4, and
+    per-channel INT4."""
+    monkeypatch.setenv("LSQ_GEMM", variant)
     _check_layer(kind, 272, 512, 300, group=128, dtype=dtype, bias=True, seed=7)
     if kind == "int4":
         _check_layer("int4", 272, 512, 300, group=512, dtype=dtype, bias=True, seed=8)
