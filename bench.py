@@ -2,6 +2,7 @@
 
 python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-sweep] [--no-cpu]
 python bench.py --calibrate-copy   # one 64 MiB device-to-device copy, for PMC calibration
+python bench.py --case int4,14336,4096,2048 --steps 20   # one layer shape only
 
 Headline workload (one JSON line, `value`): INT8 per-output-channel decode GEMV at the
 Qwen2.5-7B MLP shape, W int8 [18944, 3584], x bf16 [1, 3584] -> y bf16 [1, 18944].
@@ -17,8 +18,10 @@ copy, see --calibrate-copy) and recorded in profiles/decode_int8_m1_18944x3584.t
 
 `sweep` reports the other shapes of the same metric (INT8 M in {8,32,64}, INT4 group-128
 decode M in {1,16,64} at 18944x3584, INT4 group-128 prefill M in {256,2048,8192} at
-14336x4096 in TFLOP/s); `cpu_baseline` times the reference's CPU path (dequantize, then
-F.linear, on the host cores) on the headline shape.
+14336x4096 in TFLOP/s, the single INT8 layer 4864x896 at M=1, and one batch-32 decode step
+through the 168 INT4 projections of a Qwen2.5-0.5B-architecture stack); `cpu_baseline`
+times the reference's CPU path (dequantize, then F.linear, on the host cores) on the
+headline shape.
 """
 
 from __future__ import annotations
@@ -184,6 +187,77 @@ def bench_decode(kind: str, n: int, k: int, m: int, steps: int, warmup: int, dev
     }
 
 
+# Qwen2.5-0.5B attention and MLP projections (name, out_features N, in_features K, bias):
+# modeling_qwen2.py q/k/v carry a bias, o/gate/up/down do not.
+QWEN05_LINEARS = [("q", 896, 896, True), ("k", 128, 896, True), ("v", 128, 896, True),
+                  ("o", 896, 896, False), ("gate", 4864, 896, False), ("up", 4864, 896, False),
+                  ("down", 896, 4864, False)]
+
+
+def stack_bytes(m: int, group: int = 128) -> int:
+    """Algorithmic bytes of one decode step through the 7 projections of one layer."""
+    tot = 0
+    for _, n, k, bias in QWEN05_LINEARS:
+        tot += decode_bytes("int4", n, k, m, group) + (2 * n if bias else 0)
+    return tot
+
+
+def bench_stack(steps: int, warmup: int, device, m: int = 32, n_layers: int = 24, group: int = 128):
+    """One decode step of a random-init Qwen2.5-0.5B-architecture stack: the 168 INT4
+    group-128 forwards (24 layers x q, k, v, o, gate, up, down) in layer order, batch m,
+    bf16 activations. Every layer holds its own copy of the weights, and steps alternate
+    between enough copies of the whole stack to exceed the 256 MB Infinity Cache."""
+    from localstrm_amd import QuantizedLinear
+
+    protos = []
+    for _, n, k, bias in QWEN05_LINEARS:
+        p, s, _ = make_int4(n, k, 1, group, seed=n * 7 + k)
+        b = torch.randn(n, generator=_gen(n + k)).to(torch.bfloat16) if bias else None
+        protos.append((p.to(device), s.to(device), None if b is None else b.to(device), k))
+    per_step = n_layers * stack_bytes(m, group)
+    copies = max(2, -(-2 * MALL_BYTES // per_step))
+    stacks = [[QuantizedLinear.from_quantized(p.clone(), s, bias=b, quant_type="int4", in_features=k,
+                                              group_size=group)
+               for _ in range(n_layers) for (p, s, b, k) in protos] for _ in range(copies)]
+    xs = {k: torch.randn(m, k, generator=_gen(k)).to(torch.bfloat16).to(device) for k in (896, 4864)}
+
+    stream = torch.cuda.Stream()
+    with torch.no_grad():
+        def run(i):
+            for lin in stacks[i % copies]:
+                lin(xs[lin.in_features])
+        for i in range(max(warmup, 1)):
+            run(i)
+        torch.cuda.synchronize()
+        stream.wait_stream(torch.cuda.current_stream())
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(stream):
+            with torch.cuda.graph(graph, stream=stream):
+                for i in range(steps):
+                    run(i)
+        graph.replay()
+        torch.cuda.synchronize()
+        start = torch.cuda.Event(enable_timing=True)
+        stop = torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(stream):
+            start.record(stream)
+            graph.replay()
+            stop.record(stream)
+        stop.synchronize()
+        del graph
+    ms = start.elapsed_time(stop) / steps
+    del stacks
+    torch.cuda.empty_cache()
+    flops = 2.0 * m * n_layers * sum(n * k for _, n, k, _ in QWEN05_LINEARS)
+    return {
+        "kind": "int4 stack", "M": m, "layers": n_layers, "forwards": n_layers * len(QWEN05_LINEARS),
+        "group": group, "us_per_call": ms * 1e3, "GB_s": per_step / (ms * 1e-3) / 1e9,
+        "TFLOP_s": flops / (ms * 1e-3) / 1e12, "bytes": per_step, "stack_copies": copies,
+        "frac_hbm": per_step / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+        "frac_mfma": flops / (ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TF,
+    }
+
+
 # ----------------------------------------------------------------------------- CPU baseline
 
 
@@ -233,6 +307,11 @@ def main() -> int:
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true")
+    ap.add_argument("--case", default=None,
+                    help="kind,N,K,M (e.g. int4,14336,4096,2048), or 'stack' for the batch-32 "
+                         "decode step through the Qwen2.5-0.5B-architecture stack: time only "
+                         "that case and print its line (used for the rocprofv3 summaries in "
+                         "profiles/)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this layer's multi-GPU sharding is not built "
@@ -248,6 +327,15 @@ def main() -> int:
         calibrate_copy(device)
         return 0
 
+    if args.case == "stack":
+        print(json.dumps(bench_stack(max(2, args.steps), args.warmup, device)), flush=True)
+        return 0
+    if args.case:
+        kind, n, k, m = args.case.split(",")
+        r = bench_decode(kind, int(n), int(k), int(m), args.steps, args.warmup, device)
+        print(json.dumps(r), flush=True)
+        return 0
+
     N, K, M = 18944, 3584, 1
     head = bench_decode("int8", N, K, M, args.steps, args.warmup, device)
     sweep = []
@@ -259,6 +347,8 @@ def main() -> int:
         for m in (256, 2048, 8192):
             sweep.append(bench_decode("int4", 14336, 4096, m, max(10, args.steps // 20),
                                       max(2, args.warmup // 4), device))
+        sweep.append(bench_decode("int8", 4864, 896, 1, args.steps, args.warmup, device))
+        sweep.append(bench_stack(max(5, args.steps // 20), 2, device))
     cpu = None if args.no_cpu else cpu_baseline(N, K, M)
 
     ms = head["us_per_call"] / 1e3

@@ -30,7 +30,7 @@ struct LinearArgs {
   int64_t ngroups;
 };
 
-// Launches the LDS-staged decode kernel when the shape fits it (M <= 16, K % 128 == 0,
+// Launches the LDS-staged decode kernel when the shape fits it (M <= 64, K % 128 == 0,
 // group % 128 == 0, activations small enough to stage in LDS). Returns LSQ_E_LAYOUT
 // without launching anything when it does not fit.
 template <int DT>

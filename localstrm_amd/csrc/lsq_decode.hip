@@ -1,4 +1,4 @@
-// Decode-shaped weight-only GEMV, M <= 16 tokens (gfx950).
+// Decode-shaped weight-only GEMV, M <= 64 tokens with all activations in LDS (gfx950).
 //
 // GPU form of QuantizedLinear.forward (src/kernels/quantization.py:129-141) for the
 // decode step, where the reference dequantizes the whole [N, K] weight and calls
@@ -13,14 +13,17 @@
 // K slices. Partial sums of the KS slices are added through LDS at the end, in slice
 // order, so results do not depend on timing.
 //
+// Tokens: MB blocks of 16 token rows (MB = 1, 2, 4 for up to 16, 32, 64 tokens); every
+// unpacked weight operand feeds MB MFMAs. The launcher uses this kernel whenever the
+// activations fit in LDS (e.g. 64 tokens up to K ~ 1100, 32 up to ~2300, 16 up to ~4600).
+//
 // Prologue. Before the first MFMA each workgroup stages, once, the activations
 // x[0:M, 0:K] into LDS (row stride K + 8 elements, already in the column order the
-// weight unpack produces, plus one all-zero row) and per (128-column tile, token) sums of
-// x, used to remove the INT4 nibble bias. The per-channel scale and bias of each lane's
-// rows are loaded into registers and decoded only in the epilogue. The first D weight
-// steps are issued before the activation staging completes, so their HBM latency
-// overlaps it; after the prologue only the weight stream (and, for grouped INT4, the
-// group scales riding with it) uses the in-order vmcnt counter.
+// weight unpack produces, plus one all-zero row), per (128-column tile, token) sums of
+// x, used to remove the INT4 nibble bias, and the workgroup's scales and bias as fp32
+// (rounded to the activation type). The first D weight steps are issued before the
+// staging completes, so their HBM latency overlaps it; after the prologue only the
+// weight stream uses the in-order vmcnt counter.
 //
 // Main loop. Each lane streams 16 bytes (INT4: 32 weights) or 2 x 16 bytes (INT8: 32
 // weights) per (row tile, k tile) with non-temporal loads, D steps ahead of use, and
@@ -54,7 +57,7 @@ namespace lsq {
 namespace {
 
 constexpr int kXB = 8;  // activation chunks (16 B) per thread per batch, large-M staging
-constexpr int kSB = 4;  // scale dwords in flight per thread while staging
+constexpr int kSB = 8;  // scale dwords in flight per thread while staging
 
 // LDS layout, shared by kernel and host: staged activations (M rows + one zero row),
 // per-(k tile, token) activation sums, per-token totals, the workgroup's scales and bias
@@ -64,13 +67,13 @@ struct DecodeLds {
 };
 
 __host__ __device__ inline DecodeLds decode_lds(int64_t M, int64_t K, int rows, int64_t ngs,
-                                                int red_floats) {
+                                                int red_floats, int mp) {
   DecodeLds l;
   const int64_t nkt = K / kTileK;
   l.xs = 0;
   l.xsum = align16((M + 1) * (K + 8) * 2);
-  l.xtot = l.xsum + nkt * 16 * 4;
-  l.ss = l.xtot + 16 * 4;
+  l.xtot = l.xsum + nkt * mp * 4;
+  l.ss = l.xtot + mp * 4;
   l.sb = l.ss + align16(rows * ngs * 4);
   l.red = l.sb + align16(rows * 4);
   l.total = l.red + static_cast<int64_t>(red_floats) * 4;
@@ -94,8 +97,9 @@ __device__ __forceinline__ void put_floats(const uint32_t (&v)[kSB], int t0, int
   }
 }
 
-template <int DT, int KIND, int RT, int RG, int KS, int D, bool GROUPED>
+template <int DT, int KIND, int RT, int RG, int KS, int D, bool GROUPED, int MB>
 __global__ void __launch_bounds__(64 * RG * KS) decode_kernel(LinearArgs p) {
+  constexpr int MP = 16 * MB;  // token rows covered: MB blocks of 16
   constexpr int NT = 64 * RG * KS;
   constexpr bool W4 = KIND == kW4Tiled || KIND == kW4Canon;
   constexpr bool TILED = KIND == kW4Tiled || KIND == kW8Tiled;
@@ -105,7 +109,7 @@ __global__ void __launch_bounds__(64 * RG * KS) decode_kernel(LinearArgs p) {
   constexpr int kStride = TILED ? kTileB : (W4 ? kTileK / 2 : kTileK);
   constexpr int kHalf = KIND == kW8Tiled ? kTileBytes8 / 2 : 64;
   constexpr int ROWS = RG * RT * kTileN;
-  constexpr int RED = KS > 1 ? (KS - 1) * RG * RT * 4 * 64 : 0;
+  constexpr int RED = KS > 1 ? (KS - 1) * RG * RT * MB * 4 * 64 : 0;
   extern __shared__ __align__(16) unsigned char smem[];
   using S = typename Act<DT>::storage;
 
@@ -117,7 +121,7 @@ __global__ void __launch_bounds__(64 * RG * KS) decode_kernel(LinearArgs p) {
   const int gtiles = static_cast<int>(p.group / kTileK);
   const int ldxs = K + 8;
 
-  const DecodeLds L = decode_lds(M, K, ROWS, ngs, RED);
+  const DecodeLds L = decode_lds(M, K, ROWS, ngs, RED, MP);
   uint16_t* xs = reinterpret_cast<uint16_t*>(smem + L.xs);
   float* xsum = reinterpret_cast<float*>(smem + L.xsum);
   float* xtot = reinterpret_cast<float*>(smem + L.xtot);
@@ -175,20 +179,22 @@ __global__ void __launch_bounds__(64 * RG * KS) decode_kernel(LinearArgs p) {
     const int m = c / K8;
     return c < nchunks ? static_cast<uint32_t>((m * p.ldx + (c - m * K8) * 8) * 2) : kOOB;
   };
-  // First batch: XS chunks per thread, 2048 chunks per workgroup (M * K / 8 <= 2048 covers
-  // M <= 4 at K = 4096); larger inputs take the staging path before the weight stream.
-  constexpr int XS = NT >= 2048 ? 1 : 2048 / NT;
+  // First batch: XS chunks per thread, all issued at once (one memory round trip):
+  // 8192 chunks per 512-thread workgroup covers 16 tokens at K = 4096, 32 at 2048, 64 at
+  // 1024. Larger inputs take a second, batched pass after the weight stream is issued.
+  constexpr int XS = NT >= 8192 ? 1 : (NT >= 512 ? 8192 / NT : 16);
   u32x4 xv[XS];
 #pragma unroll
-  for (int u = 0; u < XS; ++u) xv[u] = bload16<0>(rx, x_off(u * NT + tid));
+  for (int u = 0; u < XS; ++u)
+    if (u * NT < nchunks) xv[u] = bload16<0>(rx, x_off(u * NT + tid));  // uniform skip
   uint32_t sv[kSB];
 #pragma unroll
   for (int u = 0; u < kSB; ++u) {
     const int t = u * NT + tid;
-    sv[u] = bload4(rs, t < nsd ? t * 4 : kOOB);
+    if (u * NT < nsd) sv[u] = bload4(rs, t < nsd ? t * 4 : kOOB);  // uniform skip
   }
   const uint32_t bv = bload4(rb, tid < nbd ? tid * 4 : kOOB);  // ROWS * 4 bytes <= 4 * NT
-  // ---- activations -> LDS (in the unpack's column order) and per-(tile, token) sums
+  // ---- activations -> LDS, in the unpack's column order
   auto put_x = [&](const auto& v, int c0, auto nb) {
 #pragma unroll
     for (int u = 0; u < decltype(nb)::value; ++u) {
@@ -196,25 +202,13 @@ __global__ void __launch_bounds__(64 * RG * KS) decode_kernel(LinearArgs p) {
       const int c = c0 + u * NT + tid;
       const int m = c / K8;
       const int c8 = c - m * K8;
-      float sum = 0.f;
-      if (c < nchunks) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) sum += Mma<DT>::lo(v[u][e]) + Mma<DT>::hi(v[u][e]);
-        *reinterpret_cast<u32x4*>(xs + m * ldxs + c8 * 8) =
-            KIND == kW4Canon ? permute_canon(v[u]) : v[u];
-      }
-      // 16 consecutive lanes hold the 16 chunks of one (token, k tile); all valid or none.
-      sum += __shfl_xor(sum, 1, 64);
-      sum += __shfl_xor(sum, 2, 64);
-      sum += __shfl_xor(sum, 4, 64);
-      sum += __shfl_xor(sum, 8, 64);
-      if (W4 && c < nchunks && (lane & 15) == 0) xsum[(c8 / 16) * 16 + m] = sum;
+      if (c < nchunks)
+        *reinterpret_cast<u32x4*>(xs + m * ldxs + c8 * 8) = KIND == kW4Canon ? permute_canon(v[u]) : v[u];
     }
   };
-  // Staging of what the prologue loaded. A workgroup with more activations or scales
-  // than one batch of loads (many tokens, or many scale groups) stages everything before
-  // issuing any weight load; the common case stages after, so that code between the
-  // weight issue and the main loop is straight-line and the compiler waits precisely.
+  // Staging of what the prologue loaded, done after the first weight steps are issued:
+  // these loads were issued before the weights, so waiting for them leaves the weight
+  // loads in flight.
   auto stage_first = [&]() {
     put_x(xv, 0, std::integral_constant<int, XS>());
     put_floats<DT, NT>(sv, 0, tid, p.scale_dt, nsc, ss);
@@ -227,24 +221,6 @@ __global__ void __launch_bounds__(64 * RG * KS) decode_kernel(LinearArgs p) {
       }
     }
   };
-  const bool big = nchunks > NT * XS || nsd > NT * kSB;  // uniform
-  if (big) {
-    stage_first();
-    for (int c0 = NT * XS; c0 < nchunks; c0 += NT * kXB) {
-      u32x4 xb[kXB];
-#pragma unroll
-      for (int u = 0; u < kXB; ++u) xb[u] = bload16<0>(rx, x_off(c0 + u * NT + tid));
-      put_x(xb, c0, std::integral_constant<int, kXB>());
-    }
-    for (int t0 = NT * kSB; t0 < nsd; t0 += NT * kSB) {
-#pragma unroll
-      for (int u = 0; u < kSB; ++u) {
-        const int t = t0 + u * NT + tid;
-        sv[u] = bload4(rs, t < nsd ? t * 4 : kOOB);
-      }
-      put_floats<DT, NT>(sv, t0, tid, p.scale_dt, nsc, ss);
-    }
-  }
   // Keep the scheduler from moving any of the loads above below the weight stream:
   // their consumers then wait only for them, not for the weights.
   __builtin_amdgcn_sched_barrier(0);
@@ -269,25 +245,67 @@ __global__ void __launch_bounds__(64 * RG * KS) decode_kernel(LinearArgs p) {
 #pragma unroll
   for (int s = 0; s < D; ++s) issue(wbuf[s], s);
 
-  if (!big) stage_first();
+  stage_first();
+  // Activations or scales beyond the first batch (many tokens, or many scale groups) are
+  // loaded and staged now, while the first D weight steps are in flight (the loop's waits
+  // also cover the weights, which are needed next anyway).
+  const bool big = nchunks > NT * XS || nsd > NT * kSB;  // uniform
+  if (big) {
+    for (int c0 = NT * XS; c0 < nchunks; c0 += NT * kXB) {
+      u32x4 xb[kXB];
+#pragma unroll
+      for (int u = 0; u < kXB; ++u) xb[u] = bload16<0>(rx, x_off(c0 + u * NT + tid));
+      put_x(xb, c0, std::integral_constant<int, kXB>());
+    }
+    for (int t0 = NT * kSB; t0 < nsd; t0 += NT * kSB) {
+#pragma unroll
+      for (int u = 0; u < kSB; ++u) {
+        const int t = t0 + u * NT + tid;
+        sv[u] = bload4(rs, t < nsd ? t * 4 : kOOB);
+      }
+      put_floats<DT, NT>(sv, t0, tid, p.scale_dt, nsc, ss);
+    }
+  }
   for (int c = tid; c < K8; c += NT)  // row M: zeros, read by lanes of token rows >= M
     *reinterpret_cast<u32x4*>(xs + M * ldxs + c * 8) = u32x4{0u, 0u, 0u, 0u};
   lds_barrier();
+  if (W4) {
+    // Per-(k tile, token) activation sums for the INT4 bias correction, as MFMAs of the
+    // staged activations with a ones operand (exact products, fp32 sums), one (k tile,
+    // token block) pair per wave at a time: lane (r, q) gets the sums of tokens
+    // 16 mb + 4 q + e in every column r.
+    const u32x4 ones = u32x4{Mma<DT>::kOne2, Mma<DT>::kOne2, Mma<DT>::kOne2, Mma<DT>::kOne2};
+    for (int pi = wid; pi < nkt * MB; pi += RG * KS) {  // uniform per wave
+      const int kt = pi / MB;
+      const int mb = pi - kt * MB;
+      const uint16_t* xr = xs + min(16 * mb + r, M) * ldxs + kt * kTileK;
+      f32x4 sum = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int d = 0; d < 4; ++d)
+        sum = Mma<DT>::mma(*reinterpret_cast<const u32x4*>(xr + a_col<KIND>(q, d)), ones, sum);
+      if (r == 0) *reinterpret_cast<f32x4*>(xsum + kt * MP + 16 * mb + 4 * q) = sum;
+    }
+    lds_barrier();
+  }
   if (W4 && !GROUPED) {
-    if (tid < 16) {
+    if (tid < MP) {
       float t = 0.f;
       if (tid < M)
-        for (int kt = 0; kt < nkt; ++kt) t += xsum[kt * 16 + tid];
+        for (int kt = 0; kt < nkt; ++kt) t += xsum[kt * MP + tid];
       xtot[tid] = t;
     }
     lds_barrier();
   }
 
   // ---- main loop
-  f32x4 acc[RT];
+  f32x4 acc[RT][MB];
 #pragma unroll
-  for (int i = 0; i < RT; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-  const uint16_t* xrow = xs + min(r, M) * ldxs;  // token rows >= M read the zero row
+  for (int i = 0; i < RT; ++i)
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) acc[i][mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const uint16_t* xrow[MB];  // token rows >= M read the zero row
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) xrow[mb] = xs + min(16 * mb + r, M) * ldxs;
   // Constants of the INT4 unpack in registers, so it selects v_and_or_b32 (VOP3 has no
   // literal operands on gfx9).
   uint32_t nib_mask, magic;
@@ -304,16 +322,20 @@ __global__ void __launch_bounds__(64 * RG * KS) decode_kernel(LinearArgs p) {
       // the MFMAs and the scale math, so that the next load leaves before the MFMA chain.
       const bool live = st < nsteps;  // uniform; dead steps of the last block only refill
       const int kt = k_lo + st;
-      u32x4 a[4];
-      f32x4 xo = f32x4{0.f, 0.f, 0.f, 0.f};
+      u32x4 a[MB][4];
+      f32x4 xo[MB];
       float scg[RT];
       u32x4 bb[RT][4];
       if (live) {
 #pragma unroll
-        for (int d = 0; d < 4; ++d)
-          a[d] = *reinterpret_cast<const u32x4*>(xrow + kt * kTileK + a_col<KIND>(q, d));
+        for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+          for (int d = 0; d < 4; ++d)
+            a[mb][d] = *reinterpret_cast<const u32x4*>(xrow[mb] + kt * kTileK + a_col<KIND>(q, d));
         if (W4 && GROUPED) {
-          xo = *reinterpret_cast<const f32x4*>(xsum + kt * 16 + 4 * q);
+#pragma unroll
+          for (int mb = 0; mb < MB; ++mb)
+            xo[mb] = *reinterpret_cast<const f32x4*>(xsum + kt * MP + 16 * mb + 4 * q);
           const int g = gtiles == 1 ? kt : kt / gtiles;
 #pragma unroll
           for (int i = 0; i < RT; ++i) scg[i] = ss[((rtl + i) * kTileN + r) * ngs + g];
@@ -331,15 +353,23 @@ __global__ void __launch_bounds__(64 * RG * KS) decode_kernel(LinearArgs p) {
 #pragma unroll
         for (int i = 0; i < RT; ++i) {
           if (W4 && GROUPED) {
-            f32x4 dacc = f32x4{0.f, 0.f, 0.f, 0.f};
+            f32x4 dacc[MB];
 #pragma unroll
-            for (int d = 0; d < 4; ++d) dacc = Mma<DT>::mma(a[d], bb[i][d], dacc);
+            for (int mb = 0; mb < MB; ++mb) dacc[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int e = 0; e < 4; ++e)
-              acc[i][e] = fmaf(scg[i], fmaf(-Mma<DT>::kOff4, xo[e], dacc[e]), acc[i][e]);
+            for (int d = 0; d < 4; ++d)
+#pragma unroll
+              for (int mb = 0; mb < MB; ++mb) dacc[mb] = Mma<DT>::mma(a[mb][d], bb[i][d], dacc[mb]);
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+              for (int e = 0; e < 4; ++e)
+                acc[i][mb][e] = fmaf(scg[i], fmaf(-Mma<DT>::kOff4, xo[mb][e], dacc[mb][e]), acc[i][mb][e]);
           } else {
 #pragma unroll
-            for (int d = 0; d < 4; ++d) acc[i] = Mma<DT>::mma(a[d], bb[i][d], acc[i]);
+            for (int d = 0; d < 4; ++d)
+#pragma unroll
+              for (int mb = 0; mb < MB; ++mb) acc[i][mb] = Mma<DT>::mma(a[mb][d], bb[i][d], acc[i][mb]);
           }
         }
       }
@@ -352,8 +382,10 @@ __global__ void __launch_bounds__(64 * RG * KS) decode_kernel(LinearArgs p) {
 #pragma unroll
       for (int i = 0; i < RT; ++i)
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-          red[((((ks - 1) * RG + rg) * RT + i) * 4 + e) * 64 + lane] = acc[i][e];
+        for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            red[(((((ks - 1) * RG + rg) * RT + i) * MB + mb) * 4 + e) * 64 + lane] = acc[i][mb][e];
     }
     lds_barrier();
     if (ks > 0) return;
@@ -362,8 +394,10 @@ __global__ void __launch_bounds__(64 * RG * KS) decode_kernel(LinearArgs p) {
 #pragma unroll
       for (int i = 0; i < RT; ++i)
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-          acc[i][e] += red[(((kk * RG + rg) * RT + i) * 4 + e) * 64 + lane];
+        for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            acc[i][mb][e] += red[((((kk * RG + rg) * RT + i) * MB + mb) * 4 + e) * 64 + lane];
   }
 
   S* y = static_cast<S*>(p.y);
@@ -374,15 +408,17 @@ __global__ void __launch_bounds__(64 * RG * KS) decode_kernel(LinearArgs p) {
     const float sc = GROUPED ? 1.f : ss[rl];
     const float bias = p.bias ? sb[rl] : 0.f;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int m = 4 * q + e;
-      if (m < M && n < N) {
-        float v = acc[i][e];
-        if (W4 && !GROUPED) v = fmaf(-Mma<DT>::kOff4, xtot[m], v);
-        if (!GROUPED) v *= sc;
-        y[static_cast<int64_t>(m) * p.ldy + n] = Act<DT>::from_f32(v + bias);
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int m = 16 * mb + 4 * q + e;
+        if (m < M && n < N) {
+          float v = acc[i][mb][e];
+          if (W4 && !GROUPED) v = fmaf(-Mma<DT>::kOff4, xtot[m], v);
+          if (!GROUPED) v *= sc;
+          y[static_cast<int64_t>(m) * p.ldy + n] = Act<DT>::from_f32(v + bias);
+        }
       }
-    }
   }
 }
 
@@ -448,13 +484,13 @@ Cfg pick_cfg(int kind, int64_t M, int64_t N, int64_t K) {
   return Cfg{1, 1, 8, 4};
 }
 
-template <int DT, int KIND, int RT, int RG, int KS, int D, bool GROUPED>
+template <int DT, int KIND, int RT, int RG, int KS, int D, bool GROUPED, int MB>
 int launch_one(const LinearArgs& a, hipStream_t s) {
-  constexpr int RED = KS > 1 ? (KS - 1) * RG * RT * 4 * 64 : 0;
+  constexpr int RED = KS > 1 ? (KS - 1) * RG * RT * MB * 4 * 64 : 0;
   const bool grouped = a.group < a.K;
-  const DecodeLds L = decode_lds(a.M, a.K, RG * RT * kTileN, grouped ? a.ngroups : 1, RED);
+  const DecodeLds L = decode_lds(a.M, a.K, RG * RT * kTileN, grouped ? a.ngroups : 1, RED, 16 * MB);
   if (L.total > max_lds_bytes()) return LSQ_E_LAYOUT;
-  auto kern = decode_kernel<DT, KIND, RT, RG, KS, D, GROUPED>;
+  auto kern = decode_kernel<DT, KIND, RT, RG, KS, D, GROUPED, MB>;
   if (L.total > 64 * 1024) {
     static std::atomic<int> attr_set{0};
     if (!attr_set.load(std::memory_order_acquire)) {
@@ -474,19 +510,33 @@ int launch_one(const LinearArgs& a, hipStream_t s) {
 template <int DT, int KIND, bool GROUPED>
 int launch_kind(const LinearArgs& a, hipStream_t s) {
   const Cfg c = pick_cfg(KIND, a.M, a.N, a.K);
+  if (a.M > 16) {
+    // 17..64 tokens in 2 or 4 blocks of 16; only the configurations pick_cfg returns
+#define LSQ_TRY_MB(RT_, RG_, KS_, D_)                                                   \
+    if (c.rt == RT_ && c.rg == RG_ && c.ks == KS_ && c.d == D_)                          \
+      return a.M <= 32 ? launch_one<DT, KIND, RT_, RG_, KS_, D_, GROUPED, 2>(a, s)       \
+                       : launch_one<DT, KIND, RT_, RG_, KS_, D_, GROUPED, 4>(a, s);
+    LSQ_TRY_MB(1, 8, 1, 4)
+    LSQ_TRY_MB(1, 4, 2, 8)
+    LSQ_TRY_MB(1, 2, 4, 4)
+    LSQ_TRY_MB(1, 1, 8, 4)
+#undef LSQ_TRY_MB
+    return a.M <= 32 ? launch_one<DT, KIND, 1, 8, 1, 4, GROUPED, 2>(a, s)
+                     : launch_one<DT, KIND, 1, 8, 1, 4, GROUPED, 4>(a, s);
+  }
 #define LSQ_TRY(RT_, RG_, KS_, D_)                                        \
   if (c.rt == RT_ && c.rg == RG_ && c.ks == KS_ && c.d == D_)             \
-    return launch_one<DT, KIND, RT_, RG_, KS_, D_, GROUPED>(a, s);
+    return launch_one<DT, KIND, RT_, RG_, KS_, D_, GROUPED, 1>(a, s);
   LSQ_DECODE_CONFIGS(LSQ_TRY)
 #undef LSQ_TRY
-  return launch_one<DT, KIND, 1, 8, 1, 4, GROUPED>(a, s);
+  return launch_one<DT, KIND, 1, 8, 1, 4, GROUPED, 1>(a, s);
 }
 
 }  // namespace
 
 template <int DT>
 int launch_decode(int kind, const LinearArgs& a, hipStream_t s) {
-  if (a.M < 1 || a.M > 16 || a.K % kTileK != 0 || a.K < kTileK) return LSQ_E_LAYOUT;
+  if (a.M < 1 || a.M > 64 || a.K % kTileK != 0 || a.K < kTileK) return LSQ_E_LAYOUT;
   const bool grouped = kind != kW8 && a.group < a.K;
   if (grouped && a.group % kTileK != 0) return LSQ_E_LAYOUT;
   // Buffer descriptors: 4-byte aligned scale / bias bases, 32-bit byte ranges.

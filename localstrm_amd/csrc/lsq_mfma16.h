@@ -19,6 +19,7 @@ template <int DT> struct Mma;
 
 template <> struct Mma<LSQ_BF16> {
   static constexpr uint32_t kMagic = 0x43004300u;  // bf16 pair (128, 128)
+  static constexpr uint32_t kOne2 = 0x3F803F80u;   // bf16 pair (1, 1)
   static constexpr float kOff4 = 136.f;            // 128 + the nibble bias 8
   static __device__ __forceinline__ f32x4 mma(u32x4 a, u32x4 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
@@ -33,6 +34,7 @@ template <> struct Mma<LSQ_BF16> {
 
 template <> struct Mma<LSQ_F16> {
   static constexpr uint32_t kMagic = 0x64006400u;  // fp16 pair (1024, 1024)
+  static constexpr uint32_t kOne2 = 0x3C003C00u;   // fp16 pair (1, 1)
   static constexpr float kOff4 = 1032.f;           // 1024 + the nibble bias 8
   static __device__ __forceinline__ f32x4 mma(u32x4 a, u32x4 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),

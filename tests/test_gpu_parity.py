@@ -285,6 +285,16 @@ def test_batched_decode_edges(layout, kind, group, monkeypatch):
     _check_layer(kind, 80, 128, 33, group=128, bias=True, seed=3)
 
 
+@pytest.mark.parametrize("kind,group", [("int8", None), ("int4", 128), ("int4", 4864)])
+def test_chunked_decode_large_k(kind, group):
+    """17..64 tokens with activations too large for LDS (K = 4864, the Qwen2.5-0.5B down
+    projection): the chunked decode kernel, partial last workgroup, bias, both dtypes."""
+    g = group if group is not None else 128
+    for m in (17, 48):
+        for dtype in (torch.bfloat16, torch.float16):
+            _check_layer(kind, 272, 4864, m, group=g, dtype=dtype, bias=True, seed=m + 1)
+
+
 def test_batched_decode_strided_x():
     p, s, _ = bench.make_int4(256, 512, 40)
     ql = _layer("int4", p, s, 512, 128)
