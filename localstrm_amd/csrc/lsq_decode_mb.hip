@@ -13,10 +13,10 @@
 // Chunk pipeline (chunk c lives in LDS buffer c & 1). At the start of chunk c all
 // waves pass one barrier (chunk c is visible, chunk c - 1 is finished); the workgroup
 // then writes chunk c + 1, already in registers, into the other buffer with its
-// per-(k tile, token) activation sums, issues the global loads of chunk c + 2, and
-// computes chunk c. The activation loads of a chunk are issued a whole chunk before
-// they are needed, and the weight loads issued after them stay in flight across the
-// wait.
+// per-(k tile, token) activation sums (16-lane DPP reductions), issues the global loads
+// of a later chunk into the register set just freed, and computes chunk c. The
+// activation loads of a chunk are issued one (INT8) or two (INT4) chunks before they are
+// needed, and the weight loads issued after them stay in flight across the wait.
 //
 // Numerics as in lsq_decode.hip: weight products are exact in the fp32 accumulators; the
 // INT4 nibble bias (and the magic exponent) is removed per 128-column tile with the
@@ -133,18 +133,31 @@ __global__ void __launch_bounds__(64 * RG) decode_mb_kernel(LinearArgs p) {
 
   // ---- activation chunks: piece i of chunk c is token i / PIECES, columns
   // c * kCT * 128 + 8 (i % PIECES) .. +7; tokens >= M and columns >= K read as zeros.
-  u32x4 xr[XL];
-  auto load_x = [&](int c) {
+  // XSETS register sets: chunk c + 1 is written to LDS at the start of chunk c from the
+  // set its loads went into XSETS chunks earlier, so each chunk's loads have XSETS chunk
+  // periods to land (INT4 takes two; INT8, whose weight ring holds twice the registers,
+  // one).
+  constexpr int XSETS = W4 ? 2 : 1;
+  u32x4 xr[XSETS][XL];
+  auto load_x = [&](int c, int set) {
 #pragma unroll
     for (int u = 0; u < XL; ++u) {
       const int i = u * NT + tid;
       const int m = i / PIECES;
       const int k = c * (kCT * kTileK) + (i - m * PIECES) * 8;
-      xr[u] = bload16<0>(rx, (m < M && k < K && c < nchunks)
-                                  ? static_cast<uint32_t>((m * p.ldx + k) * 2) : kOOB);
+      xr[set][u] = bload16<0>(rx, (m < M && k < K && c < nchunks)
+                                       ? static_cast<uint32_t>((m * p.ldx + k) * 2) : kOOB);
     }
   };
-  auto put_x = [&](int b) {
+  // Sum of a float over each row of 16 lanes, in every lane of the row (DPP, no LDS).
+  auto row16_sum = [](float v) {
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false));
+    return v;
+  };
+  auto put_x = [&](int b, int set) {
     uint16_t* xb = xs + b * MP * ldxs;
     float* xsb = xsum + b * kCT * MP;
 #pragma unroll
@@ -152,16 +165,14 @@ __global__ void __launch_bounds__(64 * RG) decode_mb_kernel(LinearArgs p) {
       const int i = u * NT + tid;
       const int m = i / PIECES;
       const int pc = i - m * PIECES;
-      *reinterpret_cast<u32x4*>(xb + m * ldxs + pc * 8) = KIND == kW4Canon ? permute_canon(xr[u]) : xr[u];
+      const u32x4 v = xr[set][u];
+      *reinterpret_cast<u32x4*>(xb + m * ldxs + pc * 8) = KIND == kW4Canon ? permute_canon(v) : v;
       if (W4) {
         float sum = 0.f;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) sum += Mma<DT>::lo(xr[u][e]) + Mma<DT>::hi(xr[u][e]);
-        // the 16 pieces of one (token, k tile) sit in 16 consecutive lanes
-        sum += __shfl_xor(sum, 1, 64);
-        sum += __shfl_xor(sum, 2, 64);
-        sum += __shfl_xor(sum, 4, 64);
-        sum += __shfl_xor(sum, 8, 64);
+        for (int e = 0; e < 4; ++e) sum += Mma<DT>::lo(v[e]) + Mma<DT>::hi(v[e]);
+        // the 16 pieces of one (token, k tile) sit in one 16-lane row
+        sum = row16_sum(sum);
         if ((lane & 15) == 0) xsb[(pc / 16) * MP + m] = sum;
       }
     }
@@ -179,9 +190,10 @@ __global__ void __launch_bounds__(64 * RG) decode_mb_kernel(LinearArgs p) {
     if (LPT == 2) wv[LPT - 1] = bload16<kNT>(rw, real ? off + kHalf : kOOB);
   };
 
-  load_x(0);
-  put_x(0);
-  load_x(1);
+  load_x(0, 0);
+  put_x(0, 0);
+#pragma unroll
+  for (int c = 1; c <= XSETS; ++c) load_x(c, c % XSETS);
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int s = 0; s < kD; ++s) issue(wbuf[s], s);
@@ -204,8 +216,10 @@ __global__ void __launch_bounds__(64 * RG) decode_mb_kernel(LinearArgs p) {
         if (c < nchunks) {  // uniform
           lds_barrier();    // chunk c visible to all waves; chunk c - 1 finished by all
           if (c + 1 < nchunks) {
-            put_x((c + 1) & 1);
-            load_x(c + 2);
+            // (b * kD + s) / kCT = 4 b + s / kCT and 4 is a multiple of XSETS, so the set
+            // is static
+            put_x((c + 1) & 1, (s / kCT + 1) % XSETS);
+            load_x(c + 1 + XSETS, (s / kCT + 1) % XSETS);
           }
         }
       }
