@@ -194,7 +194,15 @@ __global__ void __launch_bounds__(64 * RG * KS) decode_kernel(LinearArgs p) {
     if (u * NT < nsd) sv[u] = bload4(rs, t < nsd ? t * 4 : kOOB);  // uniform skip
   }
   const uint32_t bv = bload4(rb, tid < nbd ? tid * 4 : kOOB);  // ROWS * 4 bytes <= 4 * NT
-  // ---- activations -> LDS, in the unpack's column order
+  // ---- activations -> LDS (in the unpack's column order) and per-(k tile, token) sums
+  // Sum of a float over each row of 16 lanes, in every lane of the row (DPP, no LDS).
+  auto row16_sum = [](float v) {
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false));
+    return v;
+  };
   auto put_x = [&](const auto& v, int c0, auto nb) {
 #pragma unroll
     for (int u = 0; u < decltype(nb)::value; ++u) {
@@ -202,8 +210,19 @@ __global__ void __launch_bounds__(64 * RG * KS) decode_kernel(LinearArgs p) {
       const int c = c0 + u * NT + tid;
       const int m = c / K8;
       const int c8 = c - m * K8;
-      if (c < nchunks)
+      float sum = 0.f;
+      if (c < nchunks) {
         *reinterpret_cast<u32x4*>(xs + m * ldxs + c8 * 8) = KIND == kW4Canon ? permute_canon(v[u]) : v[u];
+        if (W4) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) sum += Mma<DT>::lo(v[u][e]) + Mma<DT>::hi(v[u][e]);
+        }
+      }
+      if (W4) {
+        // 16 consecutive lanes hold the 16 chunks of one (token, k tile); all valid or none
+        sum = row16_sum(sum);
+        if (c < nchunks && (lane & 15) == 0) xsum[(c8 / 16) * MP + m] = sum;
+      }
     }
   };
   // Staging of what the prologue loaded, done after the first weight steps are issued:
@@ -269,24 +288,6 @@ __global__ void __launch_bounds__(64 * RG * KS) decode_kernel(LinearArgs p) {
   for (int c = tid; c < K8; c += NT)  // row M: zeros, read by lanes of token rows >= M
     *reinterpret_cast<u32x4*>(xs + M * ldxs + c * 8) = u32x4{0u, 0u, 0u, 0u};
   lds_barrier();
-  if (W4) {
-    // Per-(k tile, token) activation sums for the INT4 bias correction, as MFMAs of the
-    // staged activations with a ones operand (exact products, fp32 sums), one (k tile,
-    // token block) pair per wave at a time: lane (r, q) gets the sums of tokens
-    // 16 mb + 4 q + e in every column r.
-    const u32x4 ones = u32x4{Mma<DT>::kOne2, Mma<DT>::kOne2, Mma<DT>::kOne2, Mma<DT>::kOne2};
-    for (int pi = wid; pi < nkt * MB; pi += RG * KS) {  // uniform per wave
-      const int kt = pi / MB;
-      const int mb = pi - kt * MB;
-      const uint16_t* xr = xs + min(16 * mb + r, M) * ldxs + kt * kTileK;
-      f32x4 sum = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int d = 0; d < 4; ++d)
-        sum = Mma<DT>::mma(*reinterpret_cast<const u32x4*>(xr + a_col<KIND>(q, d)), ones, sum);
-      if (r == 0) *reinterpret_cast<f32x4*>(xsum + kt * MP + 16 * mb + 4 * q) = sum;
-    }
-    lds_barrier();
-  }
   if (W4 && !GROUPED) {
     if (tid < MP) {
       float t = 0.f;
