@@ -202,12 +202,14 @@ def stack_bytes(m: int, group: int = 128) -> int:
     return tot
 
 
-def bench_stack(steps: int, warmup: int, device, m: int = 32, n_layers: int = 24, group: int = 128):
+def bench_stack(steps: int, warmup: int, device, m: int = 32, n_layers: int = 24, group: int = 128,
+                fused: bool = False):
     """One decode step of a random-init Qwen2.5-0.5B-architecture stack: the 168 INT4
     group-128 forwards (24 layers x q, k, v, o, gate, up, down) in layer order, batch m,
     bf16 activations. Every layer holds its own copy of the weights, and steps alternate
-    between enough copies of the whole stack to exceed the 256 MB Infinity Cache."""
-    from localstrm_amd import QuantizedLinear
+    between enough copies of the whole stack to exceed the 256 MB Infinity Cache.
+    fused=True runs q/k/v and gate/up as one launch each (fuse_linears): 96 launches."""
+    from localstrm_amd import QuantizedLinear, fuse_linears
 
     protos = []
     for _, n, k, bias in QWEN05_LINEARS:
@@ -216,9 +218,14 @@ def bench_stack(steps: int, warmup: int, device, m: int = 32, n_layers: int = 24
         protos.append((p.to(device), s.to(device), None if b is None else b.to(device), k))
     per_step = n_layers * stack_bytes(m, group)
     copies = max(2, -(-2 * MALL_BYTES // per_step))
-    stacks = [[QuantizedLinear.from_quantized(p.clone(), s, bias=b, quant_type="int4", in_features=k,
-                                              group_size=group)
-               for _ in range(n_layers) for (p, s, b, k) in protos] for _ in range(copies)]
+    def one_layer():
+        lins = [QuantizedLinear.from_quantized(p.clone(), s, bias=b, quant_type="int4", in_features=k,
+                                               group_size=group) for (p, s, b, k) in protos]
+        if not fused:
+            return lins
+        return [fuse_linears(lins[0:3]), lins[3], fuse_linears(lins[4:6]), lins[6]]
+
+    stacks = [[lin for _ in range(n_layers) for lin in one_layer()] for _ in range(copies)]
     xs = {k: torch.randn(m, k, generator=_gen(k)).to(torch.bfloat16).to(device) for k in (896, 4864)}
 
     stream = torch.cuda.Stream()
@@ -250,7 +257,8 @@ def bench_stack(steps: int, warmup: int, device, m: int = 32, n_layers: int = 24
     torch.cuda.empty_cache()
     flops = 2.0 * m * n_layers * sum(n * k for _, n, k, _ in QWEN05_LINEARS)
     return {
-        "kind": "int4 stack", "M": m, "layers": n_layers, "forwards": n_layers * len(QWEN05_LINEARS),
+        "kind": "int4 stack" + (" fused" if fused else ""), "M": m, "layers": n_layers,
+        "forwards": n_layers * len(QWEN05_LINEARS), "launches": n_layers * (4 if fused else 7),
         "group": group, "us_per_call": ms * 1e3, "GB_s": per_step / (ms * 1e-3) / 1e9,
         "TFLOP_s": flops / (ms * 1e-3) / 1e12, "bytes": per_step, "stack_copies": copies,
         "frac_hbm": per_step / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
@@ -327,8 +335,9 @@ def main() -> int:
         calibrate_copy(device)
         return 0
 
-    if args.case == "stack":
-        print(json.dumps(bench_stack(max(2, args.steps), args.warmup, device)), flush=True)
+    if args.case in ("stack", "stack-fused"):
+        print(json.dumps(bench_stack(max(2, args.steps), args.warmup, device,
+                                     fused=args.case == "stack-fused")), flush=True)
         return 0
     if args.case:
         kind, n, k, m = args.case.split(",")
@@ -349,6 +358,7 @@ def main() -> int:
                                       max(2, args.warmup // 4), device))
         sweep.append(bench_decode("int8", 4864, 896, 1, args.steps, args.warmup, device))
         sweep.append(bench_stack(max(5, args.steps // 20), 2, device))
+        sweep.append(bench_stack(max(5, args.steps // 20), 2, device, fused=True))
     cpu = None if args.no_cpu else cpu_baseline(N, K, M)
 
     ms = head["us_per_call"] / 1e3

@@ -6,18 +6,22 @@ gfx950 HIP kernels of liblsq.so (built by `python -m localstrm_amd.build`).
 
 from .quantization import (  # noqa: F401
     VALID_MODES,
+    FusedQuantizedLinear,
     QuantizedLinear,
     apply_optional_quantization,
     format_bytes,
+    fuse_linears,
     load_and_quantize_model,
     pack_int4,
 )
 
 __all__ = [
     "VALID_MODES",
+    "FusedQuantizedLinear",
     "QuantizedLinear",
     "apply_optional_quantization",
     "format_bytes",
+    "fuse_linears",
     "load_and_quantize_model",
     "pack_int4",
 ]

@@ -26,7 +26,7 @@ from __future__ import annotations
 
 import logging
 import os
-from typing import Any, Optional, Tuple, Union
+from typing import Any, List, Optional, Tuple, Union
 
 import torch
 import torch.nn as nn
@@ -421,6 +421,73 @@ class QuantizedLinear(nn.Module):
         g = f", group_size={self.group_size}" if self.group_size else ""
         return (f"in_features={self.in_features}, out_features={self.out_features}, "
                 f"bias={self.bias is not None}, quant_type={self.quant_type}{g}")
+
+
+class FusedQuantizedLinear(nn.Module):
+    """Several quantized layers that read the same input, run as one launch.
+
+    The concatenated-N form of a decoder layer's q/k/v projections and of its gate/up
+    projections (modeling_qwen2.py:46-48 and :206-208 call them one after the other on
+    the same hidden state). The layers' weights, scales and biases are concatenated along
+    the output dimension into one QuantizedLinear (`fused`); forward runs it once and
+    returns one output per layer, as views of the single output (last dimension split
+    into `splits`). Every output element is computed exactly as its own layer would
+    compute it; only the launch count changes.
+    """
+
+    def __init__(self, fused: QuantizedLinear, splits: List[int]):
+        super().__init__()
+        self.fused = fused
+        self.splits = [int(v) for v in splits]
+        self.in_features = fused.in_features
+        self.out_features = fused.out_features
+
+    def forward(self, x: torch.Tensor) -> Tuple[torch.Tensor, ...]:
+        return tuple(torch.split(self.fused(x), self.splits, dim=-1))
+
+    def memory_footprint_bytes(self) -> int:
+        return self.fused.memory_footprint_bytes()
+
+    def extra_repr(self) -> str:
+        return f"splits={self.splits}"
+
+
+def fuse_linears(layers: List[QuantizedLinear]) -> FusedQuantizedLinear:
+    """Fuse quantized layers with the same input into one launch (see
+    FusedQuantizedLinear). All layers must share quant_type (int8 / int4), in_features,
+    group size, scale dtype and device; a layer without bias contributes zeros when
+    others have one."""
+    if not layers:
+        raise ValueError("fuse_linears needs at least one layer")
+    first = layers[0]
+    qt = first.quant_type
+    if qt not in ("int8", "int4"):
+        raise ValueError(f"fuse_linears supports int8 / int4 layers, got '{qt}'")
+    for l in layers[1:]:
+        if l.quant_type != qt:
+            raise ValueError(f"fuse_linears: quant_type {l.quant_type} differs from {qt}")
+        if l.in_features != first.in_features:
+            raise ValueError(f"fuse_linears: in_features {l.in_features} differs from {first.in_features}")
+        if l.group_size != first.group_size:
+            raise ValueError(f"fuse_linears: group_size {l.group_size} differs from {first.group_size}")
+        if l.scale.dtype != first.scale.dtype:
+            raise ValueError(f"fuse_linears: scale dtype {l.scale.dtype} differs from {first.scale.dtype}")
+        if l._canonical().device != first._canonical().device:
+            raise ValueError("fuse_linears: layers are on different devices")
+    weight = torch.cat([l._canonical() for l in layers], dim=0)
+    scale = torch.cat([l.scale for l in layers], dim=0)
+    bias = None
+    if any(l.bias is not None for l in layers):
+        bdt = next(l.bias.dtype for l in layers if l.bias is not None)
+        bias = torch.cat([
+            l.bias.detach().to(bdt) if l.bias is not None
+            else torch.zeros(l.out_features, dtype=bdt, device=weight.device)
+            for l in layers
+        ])
+    fused = QuantizedLinear.from_quantized(weight, scale, bias, quant_type=qt,
+                                           in_features=first.in_features,
+                                           group_size=first.group_size)
+    return FusedQuantizedLinear(fused, [l.out_features for l in layers])
 
 
 # ---------------------------------------------------------------------------- helpers

@@ -424,3 +424,35 @@ def test_graph_capture_replays_match_eager():
             torch.cuda.synchronize()
             assert torch.equal(out, ref)
             _ = ql(x)  # eager work between replays
+
+
+@pytest.mark.parametrize("kind", ["int8", "int4"])
+def test_fused_linears_match_separate_layers(kind):
+    """fuse_linears (q/k/v-shaped: 896, 128, 128 rows with bias; and gate/up-shaped: two
+    4864-row layers without bias) against the layers run one by one and the oracle."""
+    from localstrm_amd import fuse_linears
+
+    for shapes, bias in (([896, 128, 128], True), ([4864, 4864], False)):
+        layers, wds = [], []
+        for i, n in enumerate(shapes):
+            if kind == "int8":
+                w, s, _ = bench.make_int8(n, 896, 1, seed=10 + i)
+            else:
+                w, s, _ = bench.make_int4(n, 896, 1, 128, seed=10 + i)
+            b = torch.randn(n, generator=torch.Generator().manual_seed(20 + i)) if bias else None
+            layers.append(_layer(kind, w, s, 896, 128, b))
+            wds.append((_oracle_deq(kind, w, s, 896, 128, "bf16"), None if b is None else b.numpy()))
+        fused = fuse_linears(layers)
+        for m in (1, 32, 300):
+            x = torch.randn(m, 896, generator=torch.Generator().manual_seed(m)).to(torch.bfloat16)
+            with torch.no_grad():
+                outs = fused(x.to(DEV))
+                sep = [l(x.to(DEV)) for l in layers]
+            assert len(outs) == len(shapes)
+            for o, s_, (wd, bd), n in zip(outs, sep, wds, shapes):
+                assert o.shape == (m, n) and o.dtype == torch.bfloat16
+                ref = qo.linear_f64(x.float().numpy(), wd, bd, "bf16")
+                err = qo.rel_err(o.float().cpu().numpy(), ref)
+                assert err <= REL_TOL
+                assert qo.rel_err(o.float().cpu().numpy(), s_.float().cpu().numpy()) <= REL_TOL
+            _say(f"  fused {kind} {shapes} M={m}: ok")

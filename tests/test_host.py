@@ -255,3 +255,29 @@ def test_library_rejects_bad_arguments_without_gpu():
         assert lib.lsq_status_string(code).startswith(b"lsq:")
     with pytest.raises(_lib.LsqError, match="group_size"):
         _lib.check(-4, "probe")
+
+
+def test_fuse_linears_concatenates_and_validates():
+    """fuse_linears builds one layer whose rows are the layers' rows in order (CPU side:
+    construction only, no kernel call)."""
+    import torch.nn as nn
+    from localstrm_amd import QuantizedLinear, fuse_linears
+
+    torch.manual_seed(0)
+    q = QuantizedLinear.from_float(nn.Linear(256, 64, bias=True), "int4", group_size=128)
+    k = QuantizedLinear.from_float(nn.Linear(256, 16, bias=True), "int4", group_size=128)
+    o = QuantizedLinear.from_float(nn.Linear(256, 32, bias=False), "int4", group_size=128)
+    f = fuse_linears([q, k, o])
+    assert f.splits == [64, 16, 32] and f.out_features == 112 and f.in_features == 256
+    assert torch.equal(f.fused.weight_packed, torch.cat([q.weight_packed, k.weight_packed, o.weight_packed]))
+    assert torch.equal(f.fused.scale, torch.cat([q.scale, k.scale, o.scale]))
+    assert torch.equal(f.fused.bias.detach(), torch.cat([q.bias.detach(), k.bias.detach(), torch.zeros(32)]))
+    w8 = [QuantizedLinear.from_float(nn.Linear(64, n), "int8") for n in (8, 24)]
+    f8 = fuse_linears(w8)
+    assert torch.equal(f8.fused.weight_q, torch.cat([w.weight_q for w in w8]))
+    with pytest.raises(ValueError):
+        fuse_linears([q, QuantizedLinear.from_float(nn.Linear(128, 8), "int4", group_size=64)])
+    with pytest.raises(ValueError):
+        fuse_linears([q, w8[0]])
+    with pytest.raises(ValueError):
+        fuse_linears([])
