@@ -1,14 +1,15 @@
 // Decode-shaped weight-only GEMM for small batches, 16 < M <= 64 tokens (gfx950).
 //
 // GPU form of QuantizedLinear.forward (src/kernels/quantization.py:129-141) for batched
-// decode steps. Same weight stream and in-register unpack as the M <= 16 kernel
-// (lsq_decode.hip): each wave owns one 16-row tile of W and all of K, streams its
-// tiles once from HBM through a ring of kD k-tile steps in registers, and turns them into
-// the B operands of v_mfma_f32_16x16x32. What changes is the activation side: 17..64
-// tokens of a 3584..4096-column layer no longer fit in LDS at once, so the workgroup
-// streams x through LDS in chunks of kCT k tiles, double-buffered, with one barrier
-// per chunk. Every token block of 16 (MB of them) reuses each unpacked weight operand,
-// so the unpack cost per weight is shared by up to 64 tokens.
+// decode steps. Same weight stream and in-register unpack as lsq_decode.hip: each wave
+// owns one 16-row tile of W and one of KS K slices, streams its tiles once from HBM
+// through a ring of kD k-tile steps in registers, and turns them into the B operands of
+// v_mfma_f32_16x16x32. What changes is the activation side: 17..64 tokens of a layer
+// with large K no longer fit in LDS at once, so the workgroup streams x through LDS in
+// chunks of kCT k tiles per slice, double-buffered, with one barrier per chunk. Every
+// token block of 16 (MB of them) reuses each unpacked weight operand, so the unpack cost
+// per weight is shared by up to 64 tokens. Small-N layers split K into KS slices so that
+// more waves stream; the slices' partial sums are added through LDS in slice order.
 //
 // Chunk pipeline (chunk c lives in LDS buffer c & 1). At the start of chunk c all
 // waves pass one barrier (chunk c is visible, chunk c - 1 is finished); the workgroup
@@ -34,28 +35,30 @@ namespace {
 constexpr int kCT = 2;  // k tiles per activation chunk
 constexpr int kD = 8;   // weight ring depth in k tiles; a multiple of 2 * kCT
 
-// LDS layout shared by kernel and host: two activation chunk buffers (mp rows of
-// kCT * 128 columns, row stride ldxs elements), their per-(k tile, token) sums, the
-// workgroup's scales and bias as fp32 rounded to the activation type.
+// LDS layout shared by kernel and host: per K slice, two activation chunk buffers (mp rows
+// of kCT * 128 columns, row stride ldxs elements) and their per-(k tile, token) sums; the
+// workgroup's scales and bias as fp32 rounded to the activation type; the cross-slice
+// partial sums.
 struct MbLds {
-  int64_t xs, xsum, ss, sb, total;
+  int64_t xs, xsum, ss, sb, red, total;
   int ldxs;
 };
 
-__host__ __device__ inline MbLds mb_lds(int mp, int rows, int64_t ngs) {
+__host__ __device__ inline MbLds mb_lds(int mp, int rows, int64_t ngs, int ks, int red_floats) {
   MbLds l;
   l.ldxs = kCT * kTileK + 8;  // +8: rows r and r + 1 start 4 banks apart
   l.xs = 0;
-  l.xsum = align16(int64_t(2) * mp * l.ldxs * 2);
-  l.ss = l.xsum + int64_t(2) * kCT * mp * 4;
+  l.xsum = align16(int64_t(ks) * 2 * mp * l.ldxs * 2);
+  l.ss = l.xsum + int64_t(ks) * 2 * kCT * mp * 4;
   l.sb = l.ss + align16(rows * ngs * 4);
-  l.total = l.sb + align16(rows * 4);
+  l.red = l.sb + align16(rows * 4);
+  l.total = l.red + int64_t(red_floats) * 4;
   return l;
 }
 
-template <int DT, int KIND, int MB, int RG, bool GROUPED>
-__global__ void __launch_bounds__(64 * RG) decode_mb_kernel(LinearArgs p) {
-  constexpr int NT = 64 * RG;
+template <int DT, int KIND, int MB, int RG, int KS, bool GROUPED>
+__global__ void __launch_bounds__(64 * RG * KS) decode_mb_kernel(LinearArgs p) {
+  constexpr int NT = 64 * RG * KS;
   constexpr bool W4 = KIND == kW4Tiled || KIND == kW4Canon;
   constexpr bool TILED = KIND == kW4Tiled || KIND == kW8Tiled;
   constexpr int LPT = W4 ? 1 : 2;  // 16-byte weight loads per lane per k tile
@@ -65,8 +68,10 @@ __global__ void __launch_bounds__(64 * RG) decode_mb_kernel(LinearArgs p) {
   constexpr int MP = 16 * MB;                 // token rows held per chunk (zero padded)
   constexpr int ROWS = RG * kTileN;
   constexpr int PIECES = kCT * kTileK / 8;    // 16-byte pieces per chunk row
-  constexpr int XL = MP * PIECES / NT;        // activation loads per thread per chunk
-  static_assert(MP * PIECES % NT == 0, "chunk pieces must split evenly over the threads");
+  constexpr int SP = MP * PIECES;             // pieces per slice per chunk
+  constexpr int XL = KS * SP / NT;            // activation loads per thread per chunk
+  constexpr int RED = KS > 1 ? (KS - 1) * RG * MB * 4 * 64 : 0;
+  static_assert(KS * SP % NT == 0, "chunk pieces must split evenly over the threads");
   static_assert(kD % (2 * kCT) == 0, "the ring block must hold whole pairs of chunks");
   extern __shared__ __align__(16) unsigned char smem[];
   using S = typename Act<DT>::storage;
@@ -77,23 +82,33 @@ __global__ void __launch_bounds__(64 * RG) decode_mb_kernel(LinearArgs p) {
   const int ng = static_cast<int>(p.ngroups);
   const int ngs = GROUPED ? ng : 1;
   const int gtiles = static_cast<int>(p.group / kTileK);
-  const int nchunks = (nkt + kCT - 1) / kCT;
+  // K slices: slice s owns k tiles [s * nkt / KS, (s + 1) * nkt / KS); every slice runs
+  // the same number of chunks (that of the longest one), so all waves meet at the same
+  // barriers.
+  auto kt_lo = [&](int sl) { return sl * nkt / KS; };
+  const int ntmax = (nkt + KS - 1) / KS;
+  const int nchunks = (ntmax + kCT - 1) / kCT;
 
-  const MbLds L = mb_lds(MP, ROWS, ngs);
+  const MbLds L = mb_lds(MP, ROWS, ngs, KS, RED);
   const int ldxs = L.ldxs;
   uint16_t* xs = reinterpret_cast<uint16_t*>(smem + L.xs);
   float* xsum = reinterpret_cast<float*>(smem + L.xsum);
   float* ss = reinterpret_cast<float*>(smem + L.ss);
   float* sb = reinterpret_cast<float*>(smem + L.sb);
+  float* red = reinterpret_cast<float*>(smem + L.red);
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);  // row tile within the workgroup
+  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int rg = wid % RG;  // row tile within the workgroup
+  const int ks = wid / RG;  // K slice
   const int r = lane & 15;
   const int q = lane >> 4;
   const int rt_wg = blockIdx.x * RG;
   const int row0 = rt_wg * kTileN;
   const int rows_valid = min(ROWS, N - row0);
+  const int my_lo = kt_lo(ks);
+  const int my_nt = kt_lo(ks + 1) - my_lo;
 
   // ---- descriptors over what this workgroup reads
   const int es_s = p.scale_dt == LSQ_F32 ? 4 : 2;
@@ -131,8 +146,9 @@ __global__ void __launch_bounds__(64 * RG) decode_mb_kernel(LinearArgs p) {
     }
   }
 
-  // ---- activation chunks: piece i of chunk c is token i / PIECES, columns
-  // c * kCT * 128 + 8 (i % PIECES) .. +7; tokens >= M and columns >= K read as zeros.
+  // ---- activation chunks: piece i of chunk c is slice i / SP, token (i % SP) / PIECES,
+  // columns of that slice's chunk c: 8 (i % PIECES) .. +7; tokens >= M and columns past
+  // the slice read as zeros.
   // XSETS register sets: chunk c + 1 is written to LDS at the start of chunk c from the
   // set its loads went into XSETS chunks earlier, so each chunk's loads have XSETS chunk
   // periods to land (INT4 takes two; INT8, whose weight ring holds twice the registers,
@@ -143,9 +159,11 @@ __global__ void __launch_bounds__(64 * RG) decode_mb_kernel(LinearArgs p) {
 #pragma unroll
     for (int u = 0; u < XL; ++u) {
       const int i = u * NT + tid;
-      const int m = i / PIECES;
-      const int k = c * (kCT * kTileK) + (i - m * PIECES) * 8;
-      xr[set][u] = bload16<0>(rx, (m < M && k < K && c < nchunks)
+      const int sl = i / SP;
+      const int j = i - sl * SP;
+      const int m = j / PIECES;
+      const int k = (kt_lo(sl) + c * kCT) * kTileK + (j - m * PIECES) * 8;
+      xr[set][u] = bload16<0>(rx, (m < M && k < kt_lo(sl + 1) * kTileK && c < nchunks)
                                        ? static_cast<uint32_t>((m * p.ldx + k) * 2) : kOOB);
     }
   };
@@ -158,34 +176,36 @@ __global__ void __launch_bounds__(64 * RG) decode_mb_kernel(LinearArgs p) {
     return v;
   };
   auto put_x = [&](int b, int set) {
-    uint16_t* xb = xs + b * MP * ldxs;
-    float* xsb = xsum + b * kCT * MP;
 #pragma unroll
     for (int u = 0; u < XL; ++u) {
       const int i = u * NT + tid;
-      const int m = i / PIECES;
-      const int pc = i - m * PIECES;
+      const int sl = i / SP;
+      const int j = i - sl * SP;
+      const int m = j / PIECES;
+      const int pc = j - m * PIECES;
       const u32x4 v = xr[set][u];
-      *reinterpret_cast<u32x4*>(xb + m * ldxs + pc * 8) = KIND == kW4Canon ? permute_canon(v) : v;
+      uint16_t* xb = xs + ((sl * 2 + b) * MP + m) * ldxs;
+      *reinterpret_cast<u32x4*>(xb + pc * 8) = KIND == kW4Canon ? permute_canon(v) : v;
       if (W4) {
         float sum = 0.f;
 #pragma unroll
         for (int e = 0; e < 4; ++e) sum += Mma<DT>::lo(v[e]) + Mma<DT>::hi(v[e]);
-        // the 16 pieces of one (token, k tile) sit in one 16-lane row
+        // the 16 pieces of one (slice, token, k tile) sit in one 16-lane row
         sum = row16_sum(sum);
-        if ((lane & 15) == 0) xsb[(pc / 16) * MP + m] = sum;
+        if ((lane & 15) == 0) xsum[((sl * 2 + b) * kCT + pc / 16) * MP + m] = sum;
       }
     }
   };
 
-  // ---- weight ring: kD k-tile steps per wave; refills past the end are out-of-range
-  // loads (no memory traffic), so every load is unconditional.
+  // ---- weight ring: kD k-tile steps per wave over its slice; refills past the end are
+  // out-of-range loads (no memory traffic), so every load is unconditional.
   u32x4 wbuf[kD][LPT];
   auto issue = [&](u32x4 (&wv)[LPT], int st) {
-    const bool real = st < nkt;
-    const uint32_t off = TILED ? static_cast<uint32_t>((wid * nkt + st) * kTileB + lane * 16)
-                               : static_cast<uint32_t>((wid * kTileN + r) * (W4 ? K / 2 : K) +
-                                                       st * kStride + q * 16);
+    const int kt = my_lo + st;
+    const bool real = st < my_nt;
+    const uint32_t off = TILED ? static_cast<uint32_t>((rg * nkt + kt) * kTileB + lane * 16)
+                               : static_cast<uint32_t>((rg * kTileN + r) * (W4 ? K / 2 : K) +
+                                                       kt * kStride + q * 16);
     wv[0] = bload16<kNT>(rw, real ? off : kOOB);
     if (LPT == 2) wv[LPT - 1] = bload16<kNT>(rw, real ? off + kHalf : kOOB);
   };
@@ -204,9 +224,9 @@ __global__ void __launch_bounds__(64 * RG) decode_mb_kernel(LinearArgs p) {
   uint32_t nib_mask, magic;  // INT4 unpack constants in registers (VOP3 takes no literal)
   asm volatile("v_mov_b32 %0, 0x000f000f" : "=v"(nib_mask));
   asm volatile("v_mov_b32 %0, %1" : "=v"(magic) : "i"(Mma<DT>::kMagic));
-  const float* srow = ss + (wid * kTileN + r) * ngs;
+  const float* srow = ss + (rg * kTileN + r) * ngs;
 
-  const int nblocks = (nkt + kD - 1) / kD;
+  const int nblocks = (nchunks * kCT + kD - 1) / kD;
   for (int b = 0; b < nblocks; ++b) {
 #pragma unroll
     for (int s = 0; s < kD; ++s) {
@@ -225,10 +245,10 @@ __global__ void __launch_bounds__(64 * RG) decode_mb_kernel(LinearArgs p) {
       }
       // Per k tile: LDS reads first (they overlap the wait for the weights), unpack,
       // refill of the ring slot just freed, then MB interleaved MFMA chains.
-      const bool live = st < nkt;  // uniform
+      const bool live = st < my_nt;  // uniform
       const int kBuf = (s / kCT) & 1;  // (b * kD + s) / kCT has the parity of s / kCT
-      const uint16_t* xb = xs + kBuf * MP * ldxs + (s % kCT) * kTileK;
-      const float* xsb = xsum + kBuf * kCT * MP + (s % kCT) * MP;
+      const uint16_t* xb = xs + (ks * 2 + kBuf) * MP * ldxs + (s % kCT) * kTileK;
+      const float* xsb = xsum + ((ks * 2 + kBuf) * kCT + (s % kCT)) * MP;
       u32x4 a[MB][4];
       f32x4 xo[MB];
       float sc = 1.f;
@@ -243,7 +263,10 @@ __global__ void __launch_bounds__(64 * RG) decode_mb_kernel(LinearArgs p) {
 #pragma unroll
           for (int mb = 0; mb < MB; ++mb) xo[mb] = *reinterpret_cast<const f32x4*>(xsb + 16 * mb + 4 * q);
         }
-        if (GROUPED) sc = srow[gtiles == 1 ? st : st / gtiles];
+        if (GROUPED) {
+          const int kt = my_lo + st;
+          sc = srow[gtiles == 1 ? kt : kt / gtiles];
+        }
 #pragma unroll
         for (int d = 0; d < 4; ++d)
           bb[d] = W4 ? unpack_w4(wbuf[s][0][d], nib_mask, magic)
@@ -276,9 +299,29 @@ __global__ void __launch_bounds__(64 * RG) decode_mb_kernel(LinearArgs p) {
     }
   }
 
-  // ---- epilogue: per-channel scale, bias, one rounding to T
+  // ---- cross-slice reduction (fixed slice order), epilogue
+  if (KS > 1) {
+    if (ks > 0) {
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          red[((((ks - 1) * RG + rg) * MB + mb) * 4 + e) * 64 + lane] = acc[mb][e];
+    }
+    lds_barrier();
+    if (ks > 0) return;
+#pragma unroll
+    for (int kk = 0; kk < KS - 1; ++kk)
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          acc[mb][e] += red[(((kk * RG + rg) * MB + mb) * 4 + e) * 64 + lane];
+  }
+
+  // per-channel scale, bias, one rounding to T
   S* y = static_cast<S*>(p.y);
-  const int rl = wid * kTileN + r;
+  const int rl = rg * kTileN + r;
   const int n = row0 + rl;
   if (n < N) {
     const float sc = GROUPED ? 1.f : ss[rl];
@@ -311,24 +354,33 @@ int mb_max_lds() {
   return v;
 }
 
-// Waves per workgroup: 8 (128 rows share one pass over x) when that still leaves enough
-// workgroups, else 4. LSQ_DECODE_MB_RG=4|8 overrides (tuning sweeps); read once.
-int pick_rg(int64_t N) {
+// Workgroup shape (row tiles RG x K slices KS): 8 row tiles when that still leaves
+// enough workgroups (one pass over x serves 128 rows), 4 for mid-size N; small N (fewer
+// than 256 row tiles) splits K so that more waves stream the weights (4 slices of 2 row
+// tiles for 32 tokens, 2 for 64, within LDS). LSQ_DECODE_MB_RG=4|8 forces RG (tuning).
+struct MbCfg {
+  int rg, ks;
+};
+
+MbCfg pick_mb(int64_t N, int mb) {
   static int env = -1;
   if (env < 0) {
     const char* e = std::getenv("LSQ_DECODE_MB_RG");
     env = e ? std::atoi(e) : 0;
   }
-  if (env == 4 || env == 8) return env;
+  if (env == 4 || env == 8) return MbCfg{env, 1};
   const int64_t nrt = (N + kTileN - 1) / kTileN;
-  return nrt >= 8 * 128 ? 8 : 4;
+  if (nrt >= 8 * 128) return MbCfg{8, 1};
+  if (nrt >= 256) return MbCfg{4, 1};
+  return MbCfg{2, mb == 2 ? 4 : 2};
 }
 
-template <int DT, int KIND, int MB, int RG, bool GROUPED>
+template <int DT, int KIND, int MB, int RG, int KS, bool GROUPED>
 int launch_one(const LinearArgs& a, hipStream_t s) {
-  const MbLds L = mb_lds(16 * MB, RG * kTileN, GROUPED ? a.ngroups : 1);
+  constexpr int RED = KS > 1 ? (KS - 1) * RG * MB * 4 * 64 : 0;
+  const MbLds L = mb_lds(16 * MB, RG * kTileN, GROUPED ? a.ngroups : 1, KS, RED);
   if (L.total > mb_max_lds()) return LSQ_E_LAYOUT;
-  auto kern = decode_mb_kernel<DT, KIND, MB, RG, GROUPED>;
+  auto kern = decode_mb_kernel<DT, KIND, MB, RG, KS, GROUPED>;
   if (L.total > 64 * 1024) {
     static std::atomic<int> attr_set{0};
     if (!attr_set.load(std::memory_order_acquire)) {
@@ -340,15 +392,20 @@ int launch_one(const LinearArgs& a, hipStream_t s) {
   }
   const int64_t nrt = (a.N + kTileN - 1) / kTileN;
   const dim3 grid(static_cast<unsigned>((nrt + RG - 1) / RG));
-  kern<<<grid, dim3(64 * RG), static_cast<size_t>(L.total), s>>>(a);
+  kern<<<grid, dim3(64 * RG * KS), static_cast<size_t>(L.total), s>>>(a);
   return static_cast<int>(hipGetLastError());
 }
 
 template <int DT, int KIND, bool GROUPED>
 int launch_kind(const LinearArgs& a, hipStream_t s) {
-  const int rg = pick_rg(a.N);
-  if (a.M <= 32) return rg == 8 ? launch_one<DT, KIND, 2, 8, GROUPED>(a, s) : launch_one<DT, KIND, 2, 4, GROUPED>(a, s);
-  return rg == 8 ? launch_one<DT, KIND, 4, 8, GROUPED>(a, s) : launch_one<DT, KIND, 4, 4, GROUPED>(a, s);
+  if (a.M <= 32) {
+    const MbCfg c = pick_mb(a.N, 2);
+    if (c.ks == 4) return launch_one<DT, KIND, 2, 2, 4, GROUPED>(a, s);
+    return c.rg == 8 ? launch_one<DT, KIND, 2, 8, 1, GROUPED>(a, s) : launch_one<DT, KIND, 2, 4, 1, GROUPED>(a, s);
+  }
+  const MbCfg c = pick_mb(a.N, 4);
+  if (c.ks == 2) return launch_one<DT, KIND, 4, 2, 2, GROUPED>(a, s);
+  return c.rg == 8 ? launch_one<DT, KIND, 4, 8, 1, GROUPED>(a, s) : launch_one<DT, KIND, 4, 4, 1, GROUPED>(a, s);
 }
 
 }  // namespace
