@@ -118,6 +118,45 @@ int lsq_w4_linear(const void* x, int64_t ldx, const uint8_t* weight_packed,
                   int64_t group_size, const void* bias, int bias_dtype, void* y, int64_t ldy,
                   int dtype, int64_t M, int64_t N, int64_t K, void* stream);
 
+/* ---- W8A8: Int8GEMMLinear (the MLP layers of the reference's 'hybrid_int8' mode) ----
+ * Weights: weight_q_t int8 [K, N] (N contiguous) and scale_w_t [N] (fp32 in the
+ * reference, any dtype code after a module cast), as Int8GEMMLinear stores them
+ * (src/kernels/quantization.py:309-319, from_float :326-353). Activations are quantized per token:
+ *   scale_x[m] = clamp(round_T(max_k |x[m,k]| * fp32(1/127)), min = round_T(1e-8))
+ *   x_q[m,k]   = clamp(rint(fp32(x[m,k]) / scale_x[m]), -128, 127)     (NaN -> 0)
+ * (quantization.py:411-414; torch evaluates the division by the Python scalar 127 on the
+ * GPU as a product with the fp32 reciprocal) and the output is
+ *   y[m,n] = round_T( fp32(sum_k x_q[m,k] * w[k,n]) * (scale_x[m] * scale_w[n]) + fp32(bias[n]) )
+ * with every product and sum one fp32 rounding (quantization.py:425-447): bit-exact. */
+
+/* Bytes of the W8A8 tiled weight layout: the tiled INT8 layout of the [N, K] weight with
+ * K padded to a multiple of 128 by zero columns. No reference counterpart. */
+int64_t lsq_w8a8_tiled_bytes(int64_t N, int64_t K);
+
+/* Re-tile weight_q_t [K, N] (the layout torch._int_mm consumes, quantization.py:309-313)
+ * into the W8A8 tiled layout. No reference counterpart; weight_q_t is left untouched. */
+int lsq_w8a8_retile(const int8_t* weight_q_t, int8_t* tiled, int64_t N, int64_t K, void* stream);
+
+/* Inverse of lsq_w8a8_retile (for round-trip checks). */
+int lsq_w8a8_untile(const int8_t* tiled, int8_t* weight_q_t, int64_t N, int64_t K, void* stream);
+
+/* Per-token activation quantization of x [M, K] (dtype `dtype`, row stride ldx elements)
+ * into x_q [M, ldq] int8 and scale_x [M] fp32. Replaces quantization.py:411-414. Columns
+ * K .. min(ldq, round_up(K, 128)) - 1 of x_q are set to 0. */
+int lsq_act_quant_i8(const void* x, int64_t ldx, int dtype, int64_t M, int64_t K, int8_t* x_q,
+                     int64_t ldq, float* scale_x, void* stream);
+
+/* y [M, N] (dtype `dtype`, row stride ldy) = W8A8 linear of x [M, K] (same dtype, row
+ * stride ldx). Replaces Int8GEMMLinear.forward's native path, quantization.py:404-447
+ * (activation quantization, torch._int_mm, rescale, bias, cast). `tiled` is the output of
+ * lsq_w8a8_retile; bias is NULL or [N] of bias_dtype. x_q [M, round_up(K, 128)] int8
+ * (16-byte aligned) and scale_x [M] fp32 are the caller's workspace; on return they hold
+ * the quantized activations and their scales. 1 <= K < 131072. */
+int lsq_w8a8_linear(const void* x, int64_t ldx, const int8_t* tiled, const void* scale_w,
+                    int scale_w_dtype, const void* bias, int bias_dtype, void* y, int64_t ldy,
+                    int dtype, int64_t M, int64_t N, int64_t K, int8_t* x_q, float* scale_x,
+                    void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,4 +1,4 @@
-"""localstrm_amd: MI355X-native weight-only quantized linear layer (INT8 / INT4 x bf16).
+"""localstrm_amd: MI355X-native quantized linear layers (INT8 / INT4 x bf16, W8A8).
 
 Drop-in for LocalStrm's src/kernels/quantization.py hot path; the compute runs in the
 gfx950 HIP kernels of liblsq.so (built by `python -m localstrm_amd.build`).
@@ -6,9 +6,12 @@ gfx950 HIP kernels of liblsq.so (built by `python -m localstrm_amd.build`).
 
 from .quantization import (  # noqa: F401
     VALID_MODES,
+    CachedQuantizedLinear,
     FusedQuantizedLinear,
+    Int8GEMMLinear,
     QuantizedLinear,
     apply_optional_quantization,
+    can_use_int8_gemm,
     format_bytes,
     fuse_linears,
     load_and_quantize_model,
@@ -17,9 +20,12 @@ from .quantization import (  # noqa: F401
 
 __all__ = [
     "VALID_MODES",
+    "CachedQuantizedLinear",
     "FusedQuantizedLinear",
+    "Int8GEMMLinear",
     "QuantizedLinear",
     "apply_optional_quantization",
+    "can_use_int8_gemm",
     "format_bytes",
     "fuse_linears",
     "load_and_quantize_model",

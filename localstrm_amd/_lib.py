@@ -43,6 +43,14 @@ SIGNATURES = {
         _int,
         [_vp, _i64, _vp, _vp, _vp, _int, _i64, _vp, _int, _vp, _i64, _int, _i64, _i64, _i64, _vp],
     ),
+    "lsq_w8a8_tiled_bytes": (_i64, [_i64, _i64]),
+    "lsq_w8a8_retile": (_int, [_vp, _vp, _i64, _i64, _vp]),
+    "lsq_w8a8_untile": (_int, [_vp, _vp, _i64, _i64, _vp]),
+    "lsq_act_quant_i8": (_int, [_vp, _i64, _int, _i64, _i64, _vp, _i64, _vp, _vp]),
+    "lsq_w8a8_linear": (
+        _int,
+        [_vp, _i64, _vp, _vp, _int, _vp, _int, _vp, _i64, _int, _i64, _i64, _i64, _vp, _vp, _vp],
+    ),
 }
 
 _lib = None

@@ -76,6 +76,18 @@ __device__ __forceinline__ float load_as_f32(const void* p, int dt, int64_t i) {
 // Product q * s with a single rounding to fp32 (never contracted into an FMA).
 __device__ __forceinline__ float mul_rn(float a, float b) { return __fmul_rn(a, b); }
 
+// fp32 product and sum that the compiler may not fuse with a neighbouring add or
+// multiply (the reference evaluates them as separate elementwise kernels, each rounding
+// once).
+__device__ __forceinline__ float mul_nc(float a, float b) {
+#pragma clang fp contract(off)
+  return a * b;
+}
+__device__ __forceinline__ float add_nc(float a, float b) {
+#pragma clang fp contract(off)
+  return a + b;
+}
+
 // The reference dequant closed form for one element, returned as the fp32 value of the
 // T-typed result: round_T( float(q) * s_T ), s_T already rounded to T.
 template <int DT>

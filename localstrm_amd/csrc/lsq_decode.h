@@ -28,6 +28,7 @@ struct LinearArgs {
   int64_t M, N, K;
   int64_t group;       // columns per scale group (== K for per-channel)
   int64_t ngroups;
+  const float* xscale = nullptr;  // W8A8 only: per-token activation scales [M]
 };
 
 // Launches the LDS-staged decode kernel when the shape fits it (M <= 64, K % 128 == 0,
@@ -35,6 +36,13 @@ struct LinearArgs {
 // without launching anything when it does not fit.
 template <int DT>
 int launch_decode(int kind, const LinearArgs& a, hipStream_t s);
+
+// W8A8 decode: x is the per-token quantized int8 activation [M, K] (row stride ldx
+// bytes), xscale its scales, w the tiled INT8 layout, scale the per-row weight scale.
+// y = float(sum_k xq * wq) * (xscale[m] * scale[n]) (+ bias), each step one fp32
+// rounding, then one rounding to the output type DT. Same fit rules as launch_decode.
+template <int DT>
+int launch_decode_a8(const LinearArgs& a, hipStream_t s);
 
 // Batched decode, 16 < M <= 64 tokens (activations streamed through LDS in chunks).
 // Same contract as launch_decode.

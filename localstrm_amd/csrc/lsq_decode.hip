@@ -66,12 +66,17 @@ struct DecodeLds {
   int64_t xs, xsum, xtot, ss, sb, red, total;
 };
 
+// Bytes of one staged activation row: K + 8 16-bit values, or (W8A8) K + 16 int8 values.
+__host__ __device__ constexpr int64_t x_row_bytes(int64_t K, bool a8) {
+  return a8 ? K + 16 : (K + 8) * 2;
+}
+
 __host__ __device__ inline DecodeLds decode_lds(int64_t M, int64_t K, int rows, int64_t ngs,
-                                                int red_floats, int mp) {
+                                                int red_floats, int mp, bool a8) {
   DecodeLds l;
   const int64_t nkt = K / kTileK;
   l.xs = 0;
-  l.xsum = align16((M + 1) * (K + 8) * 2);
+  l.xsum = align16((M + 1) * x_row_bytes(K, a8));
   l.xtot = l.xsum + nkt * mp * 4;
   l.ss = l.xtot + mp * 4;
   l.sb = l.ss + align16(rows * ngs * 4);
@@ -81,26 +86,42 @@ __host__ __device__ inline DecodeLds decode_lds(int64_t M, int64_t K, int rows, 
 }
 
 // Decode `nd` staged dwords (kSB per thread in `v`, dword index u * NT + tid + t0) of a
-// float array with dtype `dt` holding `nelem` elements into dst[] as round_T fp32.
-template <int DT, int NT>
+// float array with dtype `dt` holding `nelem` elements into dst[] as round_T fp32
+// (EXACT: the stored value itself, widened to fp32).
+template <int DT, int NT, bool EXACT>
 __device__ __forceinline__ void put_floats(const uint32_t (&v)[kSB], int t0, int tid, int dt,
                                            int nelem, float* dst) {
+  auto cvt = [](float f) { return EXACT ? f : Act<DT>::round(f); };
 #pragma unroll
   for (int u = 0; u < kSB; ++u) {
     const int t = t0 + u * NT + tid;
     if (dt == LSQ_F32) {
-      if (t < nelem) dst[t] = Act<DT>::round(dword_elem(v[u], 0, dt));
+      if (t < nelem) dst[t] = cvt(dword_elem(v[u], 0, dt));
     } else {
-      if (2 * t < nelem) dst[2 * t] = Act<DT>::round(dword_elem(v[u], 0, dt));
-      if (2 * t + 1 < nelem) dst[2 * t + 1] = Act<DT>::round(dword_elem(v[u], 1, dt));
+      if (2 * t < nelem) dst[2 * t] = cvt(dword_elem(v[u], 0, dt));
+      if (2 * t + 1 < nelem) dst[2 * t + 1] = cvt(dword_elem(v[u], 1, dt));
     }
   }
 }
 
-template <int DT, int KIND, int RT, int RG, int KS, int D, bool GROUPED, int MB>
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+// v_mfma_i32_16x16x64_i8 on registers kept as f32x4 bit patterns (the accumulator
+// arrays are shared with the floating-point paths).
+__device__ __forceinline__ f32x4 mma_i8(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_bit_cast(
+      f32x4, __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i32x4, a),
+                                                   __builtin_bit_cast(i32x4, b),
+                                                   __builtin_bit_cast(i32x4, c), 0, 0, 0));
+}
+
+template <int DT, int KIND, int RT, int RG, int KS, int D, bool GROUPED, int MB, bool A8>
 __global__ void __launch_bounds__(64 * RG * KS) decode_kernel(LinearArgs p) {
+  static_assert(!A8 || (KIND == kW8Tiled && !GROUPED), "W8A8 streams the tiled INT8 layout");
   constexpr int MP = 16 * MB;  // token rows covered: MB blocks of 16
   constexpr int NT = 64 * RG * KS;
+  constexpr int XE = A8 ? 16 : 8;  // activations per 16-byte chunk
+  constexpr int XB = A8 ? 1 : 2;   // bytes per activation
   constexpr bool W4 = KIND == kW4Tiled || KIND == kW4Canon;
   constexpr bool TILED = KIND == kW4Tiled || KIND == kW8Tiled;
   constexpr int LPT = W4 ? 1 : 2;  // 16-byte weight loads per lane per (row tile, k tile)
@@ -119,10 +140,10 @@ __global__ void __launch_bounds__(64 * RG * KS) decode_kernel(LinearArgs p) {
   const int ng = static_cast<int>(p.ngroups);
   const int ngs = GROUPED ? ng : 1;  // scale columns per row
   const int gtiles = static_cast<int>(p.group / kTileK);
-  const int ldxs = K + 8;
+  const int ldxb = static_cast<int>(x_row_bytes(K, A8));  // LDS bytes per staged row
 
-  const DecodeLds L = decode_lds(M, K, ROWS, ngs, RED, MP);
-  uint16_t* xs = reinterpret_cast<uint16_t*>(smem + L.xs);
+  const DecodeLds L = decode_lds(M, K, ROWS, ngs, RED, MP, A8);
+  unsigned char* xs = smem + L.xs;
   float* xsum = reinterpret_cast<float*>(smem + L.xsum);
   float* xtot = reinterpret_cast<float*>(smem + L.xtot);
   float* ss = reinterpret_cast<float*>(smem + L.ss);
@@ -146,7 +167,7 @@ __global__ void __launch_bounds__(64 * RG * KS) decode_kernel(LinearArgs p) {
   // ---- descriptors over what this workgroup reads
   const int es_s = p.scale_dt == LSQ_F32 ? 4 : 2;
   const int es_b = p.bias_dt == LSQ_F32 ? 4 : 2;
-  const rsrc_t rx = make_rsrc(p.x, static_cast<uint32_t>(((M - 1) * p.ldx + K) * 2));
+  const rsrc_t rx = make_rsrc(p.x, static_cast<uint32_t>(((M - 1) * p.ldx + K) * XB));
   const uint8_t* wbase;
   uint32_t wbytes;
   if (TILED) {
@@ -173,11 +194,11 @@ __global__ void __launch_bounds__(64 * RG * KS) decode_kernel(LinearArgs p) {
 
   // ---- prologue loads, in the order their data is needed: activations, scales, bias,
   // then the first D weight steps.
-  const int K8 = K / 8;
+  const int K8 = K / XE;  // 16-byte chunks per activation row
   const int nchunks = M * K8;
   auto x_off = [&](int c) -> uint32_t {
     const int m = c / K8;
-    return c < nchunks ? static_cast<uint32_t>((m * p.ldx + (c - m * K8) * 8) * 2) : kOOB;
+    return c < nchunks ? static_cast<uint32_t>((m * p.ldx + (c - m * K8) * XE) * XB) : kOOB;
   };
   // First batch: XS chunks per thread, all issued at once (one memory round trip):
   // 8192 chunks per 512-thread workgroup covers 16 tokens at K = 4096, 32 at 2048, 64 at
@@ -194,6 +215,8 @@ __global__ void __launch_bounds__(64 * RG * KS) decode_kernel(LinearArgs p) {
     if (u * NT < nsd) sv[u] = bload4(rs, t < nsd ? t * 4 : kOOB);  // uniform skip
   }
   const uint32_t bv = bload4(rb, tid < nbd ? tid * 4 : kOOB);  // ROWS * 4 bytes <= 4 * NT
+  float sxv = 0.f;  // W8A8: this thread's token scale
+  if (A8 && tid < M) sxv = p.xscale[tid];
   // ---- activations -> LDS (in the unpack's column order) and per-(k tile, token) sums
   // Sum of a float over each row of 16 lanes, in every lane of the row (DPP, no LDS).
   auto row16_sum = [](float v) {
@@ -212,13 +235,13 @@ __global__ void __launch_bounds__(64 * RG * KS) decode_kernel(LinearArgs p) {
       const int c8 = c - m * K8;
       float sum = 0.f;
       if (c < nchunks) {
-        *reinterpret_cast<u32x4*>(xs + m * ldxs + c8 * 8) = KIND == kW4Canon ? permute_canon(v[u]) : v[u];
-        if (W4) {
+        *reinterpret_cast<u32x4*>(xs + m * ldxb + c8 * 16) = KIND == kW4Canon ? permute_canon(v[u]) : v[u];
+        if constexpr (W4) {
 #pragma unroll
           for (int e = 0; e < 4; ++e) sum += Mma<DT>::lo(v[u][e]) + Mma<DT>::hi(v[u][e]);
         }
       }
-      if (W4) {
+      if constexpr (W4) {
         // 16 consecutive lanes hold the 16 chunks of one (token, k tile); all valid or none
         sum = row16_sum(sum);
         if (c < nchunks && (lane & 15) == 0) xsum[(c8 / 16) * MP + m] = sum;
@@ -230,15 +253,18 @@ __global__ void __launch_bounds__(64 * RG * KS) decode_kernel(LinearArgs p) {
   // loads in flight.
   auto stage_first = [&]() {
     put_x(xv, 0, std::integral_constant<int, XS>());
-    put_floats<DT, NT>(sv, 0, tid, p.scale_dt, nsc, ss);
+    put_floats<DT, NT, A8>(sv, 0, tid, p.scale_dt, nsc, ss);
+    // W8A8 adds the bias as stored (widened to fp32); weight-only rounds it to T first
+    auto cvt = [](float f) { return A8 ? f : Act<DT>::round(f); };
     if (p.bias && tid < nbd) {
       if (es_b == 4) {
-        sb[tid] = Act<DT>::round(dword_elem(bv, 0, LSQ_F32));
+        sb[tid] = cvt(dword_elem(bv, 0, LSQ_F32));
       } else {
-        if (2 * tid < rows_valid) sb[2 * tid] = Act<DT>::round(dword_elem(bv, 0, p.bias_dt));
-        if (2 * tid + 1 < rows_valid) sb[2 * tid + 1] = Act<DT>::round(dword_elem(bv, 1, p.bias_dt));
+        if (2 * tid < rows_valid) sb[2 * tid] = cvt(dword_elem(bv, 0, p.bias_dt));
+        if (2 * tid + 1 < rows_valid) sb[2 * tid + 1] = cvt(dword_elem(bv, 1, p.bias_dt));
       }
     }
+    if (A8 && tid < MP) xtot[tid] = sxv;
   };
   // Keep the scheduler from moving any of the loads above below the weight stream:
   // their consumers then wait only for them, not for the weights.
@@ -282,11 +308,11 @@ __global__ void __launch_bounds__(64 * RG * KS) decode_kernel(LinearArgs p) {
         const int t = t0 + u * NT + tid;
         sv[u] = bload4(rs, t < nsd ? t * 4 : kOOB);
       }
-      put_floats<DT, NT>(sv, t0, tid, p.scale_dt, nsc, ss);
+      put_floats<DT, NT, A8>(sv, t0, tid, p.scale_dt, nsc, ss);
     }
   }
   for (int c = tid; c < K8; c += NT)  // row M: zeros, read by lanes of token rows >= M
-    *reinterpret_cast<u32x4*>(xs + M * ldxs + c * 8) = u32x4{0u, 0u, 0u, 0u};
+    *reinterpret_cast<u32x4*>(xs + M * ldxb + c * 16) = u32x4{0u, 0u, 0u, 0u};
   lds_barrier();
   if (W4 && !GROUPED) {
     if (tid < MP) {
@@ -304,14 +330,16 @@ __global__ void __launch_bounds__(64 * RG * KS) decode_kernel(LinearArgs p) {
   for (int i = 0; i < RT; ++i)
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) acc[i][mb] = f32x4{0.f, 0.f, 0.f, 0.f};
-  const uint16_t* xrow[MB];  // token rows >= M read the zero row
+  const unsigned char* xrow[MB];  // token rows >= M read the zero row
 #pragma unroll
-  for (int mb = 0; mb < MB; ++mb) xrow[mb] = xs + min(16 * mb + r, M) * ldxs;
+  for (int mb = 0; mb < MB; ++mb) xrow[mb] = xs + min(16 * mb + r, M) * ldxb;
   // Constants of the INT4 unpack in registers, so it selects v_and_or_b32 (VOP3 has no
   // literal operands on gfx9).
-  uint32_t nib_mask, magic;
-  asm volatile("v_mov_b32 %0, 0x000f000f" : "=v"(nib_mask));
-  asm volatile("v_mov_b32 %0, %1" : "=v"(magic) : "i"(Mma<DT>::kMagic));
+  uint32_t nib_mask = 0, magic = 0;
+  if constexpr (W4) {
+    asm volatile("v_mov_b32 %0, 0x000f000f" : "=v"(nib_mask));
+    asm volatile("v_mov_b32 %0, %1" : "=v"(magic) : "i"(Mma<DT>::kMagic));
+  }
 
   const int nblocks = (nsteps + D - 1) / D;
   for (int b = 0; b < nblocks; ++b) {
@@ -323,54 +351,81 @@ __global__ void __launch_bounds__(64 * RG * KS) decode_kernel(LinearArgs p) {
       // the MFMAs and the scale math, so that the next load leaves before the MFMA chain.
       const bool live = st < nsteps;  // uniform; dead steps of the last block only refill
       const int kt = k_lo + st;
-      u32x4 a[MB][4];
-      f32x4 xo[MB];
-      float scg[RT];
-      u32x4 bb[RT][4];
-      if (live) {
-#pragma unroll
-        for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-          for (int d = 0; d < 4; ++d)
-            a[mb][d] = *reinterpret_cast<const u32x4*>(xrow[mb] + kt * kTileK + a_col<KIND>(q, d));
-        if (W4 && GROUPED) {
+      if constexpr (A8) {
+        // W8A8: the raw int8 weights are the B operand of v_mfma_i32_16x16x64_i8 as
+        // loaded; lane quad q, load j holds columns 32 q + 16 j .. +15 of the k tile,
+        // and the activation operand is the same 16 columns of the token row.
+        u32x4 a8[MB][2], b8[RT][2];
+        if (live) {
 #pragma unroll
           for (int mb = 0; mb < MB; ++mb)
-            xo[mb] = *reinterpret_cast<const f32x4*>(xsum + kt * MP + 16 * mb + 4 * q);
-          const int g = gtiles == 1 ? kt : kt / gtiles;
 #pragma unroll
-          for (int i = 0; i < RT; ++i) scg[i] = ss[((rtl + i) * kTileN + r) * ngs + g];
+            for (int j = 0; j < 2; ++j)
+              a8[mb][j] = *reinterpret_cast<const u32x4*>(xrow[mb] + kt * kTileK + 32 * q + 16 * j);
+#pragma unroll
+          for (int i = 0; i < RT; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) b8[i][j] = wbuf[s][i][j];
         }
+        issue(wbuf[s], st + D);
+        if (live) {
 #pragma unroll
-        for (int i = 0; i < RT; ++i)
+          for (int i = 0; i < RT; ++i)
 #pragma unroll
-          for (int d = 0; d < 4; ++d)
-            bb[i][d] = W4 ? unpack_w4(wbuf[s][i][0][d], nib_mask, magic)
-                          : convert_w8<DT>(wbuf[s][i][d >> 1][2 * (d & 1)],
-                                           wbuf[s][i][d >> 1][2 * (d & 1) + 1]);
-      }
-      issue(wbuf[s], st + D);
-      if (live) {
+            for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int i = 0; i < RT; ++i) {
-          if (W4 && GROUPED) {
-            f32x4 dacc[MB];
+              for (int mb = 0; mb < MB; ++mb) acc[i][mb] = mma_i8(a8[mb][j], b8[i][j], acc[i][mb]);
+        }
+      } else {
+        u32x4 a[MB][4];
+        f32x4 xo[MB];
+        float scg[RT];
+        u32x4 bb[RT][4];
+        if (live) {
 #pragma unroll
-            for (int mb = 0; mb < MB; ++mb) dacc[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+          for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
             for (int d = 0; d < 4; ++d)
-#pragma unroll
-              for (int mb = 0; mb < MB; ++mb) dacc[mb] = Mma<DT>::mma(a[mb][d], bb[i][d], dacc[mb]);
+              a[mb][d] = *reinterpret_cast<const u32x4*>(xrow[mb] + (kt * kTileK + a_col<KIND>(q, d)) * 2);
+          if (W4 && GROUPED) {
 #pragma unroll
             for (int mb = 0; mb < MB; ++mb)
+              xo[mb] = *reinterpret_cast<const f32x4*>(xsum + kt * MP + 16 * mb + 4 * q);
+            const int g = gtiles == 1 ? kt : kt / gtiles;
 #pragma unroll
-              for (int e = 0; e < 4; ++e)
-                acc[i][mb][e] = fmaf(scg[i], fmaf(-Mma<DT>::kOff4, xo[mb][e], dacc[mb][e]), acc[i][mb][e]);
-          } else {
+            for (int i = 0; i < RT; ++i) scg[i] = ss[((rtl + i) * kTileN + r) * ngs + g];
+          }
+#pragma unroll
+          for (int i = 0; i < RT; ++i)
 #pragma unroll
             for (int d = 0; d < 4; ++d)
+              bb[i][d] = W4 ? unpack_w4(wbuf[s][i][0][d], nib_mask, magic)
+                            : convert_w8<DT>(wbuf[s][i][d >> 1][2 * (d & 1)],
+                                             wbuf[s][i][d >> 1][2 * (d & 1) + 1]);
+        }
+        issue(wbuf[s], st + D);
+        if (live) {
 #pragma unroll
-              for (int mb = 0; mb < MB; ++mb) acc[i][mb] = Mma<DT>::mma(a[mb][d], bb[i][d], acc[i][mb]);
+          for (int i = 0; i < RT; ++i) {
+            if (W4 && GROUPED) {
+              f32x4 dacc[MB];
+#pragma unroll
+              for (int mb = 0; mb < MB; ++mb) dacc[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+              for (int d = 0; d < 4; ++d)
+#pragma unroll
+                for (int mb = 0; mb < MB; ++mb) dacc[mb] = Mma<DT>::mma(a[mb][d], bb[i][d], dacc[mb]);
+#pragma unroll
+              for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                  acc[i][mb][e] = fmaf(scg[i], fmaf(-Mma<DT>::kOff4, xo[mb][e], dacc[mb][e]), acc[i][mb][e]);
+            } else {
+#pragma unroll
+              for (int d = 0; d < 4; ++d)
+#pragma unroll
+                for (int mb = 0; mb < MB; ++mb) acc[i][mb] = Mma<DT>::mma(a[mb][d], bb[i][d], acc[i][mb]);
+            }
           }
         }
       }
@@ -397,8 +452,13 @@ __global__ void __launch_bounds__(64 * RG * KS) decode_kernel(LinearArgs p) {
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
-          for (int e = 0; e < 4; ++e)
-            acc[i][mb][e] += red[((((kk * RG + rg) * RT + i) * MB + mb) * 4 + e) * 64 + lane];
+          for (int e = 0; e < 4; ++e) {
+            const float v = red[((((kk * RG + rg) * RT + i) * MB + mb) * 4 + e) * 64 + lane];
+            if constexpr (A8)  // int32 partial sums (exact, in any order)
+              acc[i][mb][e] = __int_as_float(__float_as_int(acc[i][mb][e]) + __float_as_int(v));
+            else
+              acc[i][mb][e] += v;
+          }
   }
 
   S* y = static_cast<S*>(p.y);
@@ -414,10 +474,17 @@ __global__ void __launch_bounds__(64 * RG * KS) decode_kernel(LinearArgs p) {
       for (int e = 0; e < 4; ++e) {
         const int m = 16 * mb + 4 * q + e;
         if (m < M && n < N) {
-          float v = acc[i][mb][e];
-          if (W4 && !GROUPED) v = fmaf(-Mma<DT>::kOff4, xtot[m], v);
-          if (!GROUPED) v *= sc;
-          y[static_cast<int64_t>(m) * p.ldy + n] = Act<DT>::from_f32(v + bias);
+          if constexpr (A8) {
+            // float(acc) * (sx * sw) [+ bias], each an fp32 rounding, then round to T
+            float v = mul_nc(static_cast<float>(__float_as_int(acc[i][mb][e])), mul_nc(xtot[m], sc));
+            if (p.bias) v = add_nc(v, bias);
+            y[static_cast<int64_t>(m) * p.ldy + n] = Act<DT>::from_f32(v);
+          } else {
+            float v = acc[i][mb][e];
+            if constexpr (W4 && !GROUPED) v = fmaf(-Mma<DT>::kOff4, xtot[m], v);
+            if (!GROUPED) v *= sc;
+            y[static_cast<int64_t>(m) * p.ldy + n] = Act<DT>::from_f32(v + bias);
+          }
         }
       }
   }
@@ -488,13 +555,13 @@ Cfg pick_cfg(int kind, int64_t M, int64_t N, int64_t K) {
   return Cfg{1, 1, 8, 4};
 }
 
-template <int DT, int KIND, int RT, int RG, int KS, int D, bool GROUPED, int MB>
+template <int DT, int KIND, int RT, int RG, int KS, int D, bool GROUPED, int MB, bool A8>
 int launch_one(const LinearArgs& a, hipStream_t s) {
   constexpr int RED = KS > 1 ? (KS - 1) * RG * RT * MB * 4 * 64 : 0;
   const bool grouped = a.group < a.K;
-  const DecodeLds L = decode_lds(a.M, a.K, RG * RT * kTileN, grouped ? a.ngroups : 1, RED, 16 * MB);
+  const DecodeLds L = decode_lds(a.M, a.K, RG * RT * kTileN, grouped ? a.ngroups : 1, RED, 16 * MB, A8);
   if (L.total > max_lds_bytes()) return LSQ_E_LAYOUT;
-  auto kern = decode_kernel<DT, KIND, RT, RG, KS, D, GROUPED, MB>;
+  auto kern = decode_kernel<DT, KIND, RT, RG, KS, D, GROUPED, MB, A8>;
   if (L.total > 64 * 1024) {
     static std::atomic<int> attr_set{0};
     if (!attr_set.load(std::memory_order_acquire)) {
@@ -511,29 +578,29 @@ int launch_one(const LinearArgs& a, hipStream_t s) {
   return static_cast<int>(hipGetLastError());
 }
 
-template <int DT, int KIND, bool GROUPED>
+template <int DT, int KIND, bool GROUPED, bool A8 = false>
 int launch_kind(const LinearArgs& a, hipStream_t s) {
   const Cfg c = pick_cfg(KIND, a.M, a.N, a.K);
   if (a.M > 16) {
     // 17..64 tokens in 2 or 4 blocks of 16; only the configurations pick_cfg returns
 #define LSQ_TRY_MB(RT_, RG_, KS_, D_)                                                   \
     if (c.rt == RT_ && c.rg == RG_ && c.ks == KS_ && c.d == D_)                          \
-      return a.M <= 32 ? launch_one<DT, KIND, RT_, RG_, KS_, D_, GROUPED, 2>(a, s)       \
-                       : launch_one<DT, KIND, RT_, RG_, KS_, D_, GROUPED, 4>(a, s);
+      return a.M <= 32 ? launch_one<DT, KIND, RT_, RG_, KS_, D_, GROUPED, 2, A8>(a, s)   \
+                       : launch_one<DT, KIND, RT_, RG_, KS_, D_, GROUPED, 4, A8>(a, s);
     LSQ_TRY_MB(1, 8, 1, 4)
     LSQ_TRY_MB(1, 4, 2, 8)
     LSQ_TRY_MB(1, 2, 4, 4)
     LSQ_TRY_MB(1, 1, 8, 4)
 #undef LSQ_TRY_MB
-    return a.M <= 32 ? launch_one<DT, KIND, 1, 8, 1, 4, GROUPED, 2>(a, s)
-                     : launch_one<DT, KIND, 1, 8, 1, 4, GROUPED, 4>(a, s);
+    return a.M <= 32 ? launch_one<DT, KIND, 1, 8, 1, 4, GROUPED, 2, A8>(a, s)
+                     : launch_one<DT, KIND, 1, 8, 1, 4, GROUPED, 4, A8>(a, s);
   }
 #define LSQ_TRY(RT_, RG_, KS_, D_)                                        \
   if (c.rt == RT_ && c.rg == RG_ && c.ks == KS_ && c.d == D_)             \
-    return launch_one<DT, KIND, RT_, RG_, KS_, D_, GROUPED, 1>(a, s);
+    return launch_one<DT, KIND, RT_, RG_, KS_, D_, GROUPED, 1, A8>(a, s);
   LSQ_DECODE_CONFIGS(LSQ_TRY)
 #undef LSQ_TRY
-  return launch_one<DT, KIND, 1, 8, 1, 4, GROUPED, 1>(a, s);
+  return launch_one<DT, KIND, 1, 8, 1, 4, GROUPED, 1, A8>(a, s);
 }
 
 }  // namespace
@@ -561,5 +628,19 @@ int launch_decode(int kind, const LinearArgs& a, hipStream_t s) {
 
 template int launch_decode<LSQ_BF16>(int, const LinearArgs&, hipStream_t);
 template int launch_decode<LSQ_F16>(int, const LinearArgs&, hipStream_t);
+
+template <int DT>
+int launch_decode_a8(const LinearArgs& a, hipStream_t s) {
+  if (a.M < 1 || a.M > 64 || a.K % kTileK != 0 || a.K < kTileK || !a.xscale) return LSQ_E_LAYOUT;
+  auto aligned4 = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 3) == 0; };
+  if (!aligned4(a.scale) || (a.bias && !aligned4(a.bias))) return LSQ_E_LAYOUT;
+  if ((a.M - 1) * a.ldx + a.K >= (int64_t(1) << 31)) return LSQ_E_LAYOUT;
+  if (int64_t(128) * a.K >= (int64_t(1) << 31)) return LSQ_E_LAYOUT;
+  return launch_kind<DT, kW8Tiled, false, true>(a, s);
+}
+
+template int launch_decode_a8<LSQ_F32>(const LinearArgs&, hipStream_t);
+template int launch_decode_a8<LSQ_F16>(const LinearArgs&, hipStream_t);
+template int launch_decode_a8<LSQ_BF16>(const LinearArgs&, hipStream_t);
 
 }  // namespace lsq

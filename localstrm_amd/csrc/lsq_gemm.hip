@@ -195,20 +195,25 @@ __global__ void __launch_bounds__(NT) gemm_kernel(LinearArgs p) {
   // ---- activations: DMA straight into LDS. One wave instruction fills 8 rows (1 KB):
   // lane l writes LDS row rb + (l >> 3), position l & 7, which must hold column chunk
   // (l & 7) ^ (((rb + (l >> 3)) >> 1) & 7); rb is a multiple of 8, so that swizzle term
-  // is ((rb >> 1) & 4) | (l >> 4), i.e. one of two lane patterns.
-  uint32_t x_lane_off[2];
+  // is ((rb >> 1) & 4) | (l >> 4). The row goes into the per-lane offset, which the
+  // descriptor's range check covers (the scalar offset is not checked), so rows past M
+  // read zeros; the scalar offset carries only the column of the step.
+  constexpr int kXB = BM / 8 / (NT / 64);  // 4 row blocks of 8 per wave
+  uint32_t x_lane_off[kXB];
 #pragma unroll
-  for (int v = 0; v < 2; ++v)
-    x_lane_off[v] = static_cast<uint32_t>(
-        ((lane >> 3) * p.ldx + 8 * ((lane & 7) ^ ((v << 2) | (lane >> 4)))) * 2);
+  for (int b = 0; b < kXB; ++b) {
+    const int rb = (wid * kXB + b) * 8;  // (rb >> 1) & 4 == (b & 1) * 4
+    x_lane_off[b] = static_cast<uint32_t>(
+        ((rb + (lane >> 3)) * p.ldx + 8 * ((lane & 7) ^ (((b & 1) << 2) | (lane >> 4)))) * 2);
+  }
   auto issue_x = [&](int st, int buf) {
     unsigned char* dst = xs_at(buf);
 #pragma unroll
-    for (int b = 0; b < BM / 8 / (NT / 64); ++b) {  // 4 row blocks per wave
-      const int rb = (wid * (BM / 8 / (NT / 64)) + b) * 8;  // (rb >> 1) & 4 == (b & 1) * 4
+    for (int b = 0; b < kXB; ++b) {
+      const int rb = (wid * kXB + b) * 8;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
           rx, (__attribute__((address_space(3))) void*)(dst + rb * BK * 2), 16,
-          x_lane_off[b & 1], static_cast<int>((rb * p.ldx + gstep(st) * BK) * 2), 0, 0);
+          x_lane_off[b], static_cast<int>(gstep(st) * BK * 2), 0, 0);
     }
   };
 
@@ -464,19 +469,22 @@ __global__ void __launch_bounds__(RNT, 2) gemm_rw_kernel(LinearArgs p) {
   // ---- activations: two LDS stages of 128 rows x 64 columns, chunk c of row r at
   // position c ^ ((r >> 1) & 7); DMA as in gemm_kernel (4 x 1 KB per wave per step).
   constexpr int kStage = RBM * BK * 2;
-  uint32_t x_lane_off[2];
+  constexpr int kXB = RBM / 8 / (RNT / 64);  // 4 row blocks of 8 per wave
+  uint32_t x_lane_off[kXB];  // row in the range-checked per-lane offset, as in gemm_kernel
 #pragma unroll
-  for (int v = 0; v < 2; ++v)
-    x_lane_off[v] = static_cast<uint32_t>(
-        ((lane >> 3) * p.ldx + 8 * ((lane & 7) ^ ((v << 2) | (lane >> 4)))) * 2);
+  for (int b = 0; b < kXB; ++b) {
+    const int rb = (wid * kXB + b) * 8;  // (rb >> 1) & 4 == (b & 1) * 4
+    x_lane_off[b] = static_cast<uint32_t>(
+        ((rb + (lane >> 3)) * p.ldx + 8 * ((lane & 7) ^ (((b & 1) << 2) | (lane >> 4)))) * 2);
+  }
   auto issue_x = [&](int st, int buf) {
     unsigned char* dst = smem + buf * kStage;
 #pragma unroll
-    for (int b = 0; b < RBM / 8 / (RNT / 64); ++b) {
-      const int rb = (wid * (RBM / 8 / (RNT / 64)) + b) * 8;  // (rb >> 1) & 4 == (b & 1) * 4
+    for (int b = 0; b < kXB; ++b) {
+      const int rb = (wid * kXB + b) * 8;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
           rx, (__attribute__((address_space(3))) void*)(dst + rb * BK * 2), 16,
-          x_lane_off[b & 1], static_cast<int>((rb * p.ldx + gstep(st) * BK) * 2), 0, 0);
+          x_lane_off[b], static_cast<int>(gstep(st) * BK * 2), 0, 0);
     }
   };
 

@@ -1,0 +1,491 @@
+// W8A8 linear layer: int8 weights x per-token int8 activations on the int8 MFMA (gfx950).
+//
+// GPU form of Int8GEMMLinear.forward (src/kernels/quantization.py:379-447), the MLP layer
+// of the reference's 'hybrid_int8' mode. The reference quantizes the activations with a
+// chain of elementwise kernels (:411-414), pads M to a multiple of 32 (:416-422), calls
+// torch._int_mm (:425) and rescales in fp32 (:431-440). Here:
+//
+//  * act_quant_kernel: one workgroup per token row: max|x| (exact in the input type),
+//    the scale, and the int8 row, in one pass over x held in registers;
+//  * the decode kernel's W8A8 mode (lsq_decode.hip) for M <= 64: int8 weights streamed
+//    once from the tiled layout straight into v_mfma_i32_16x16x64_i8, no conversion;
+//  * w8a8_gemm_kernel for larger M: both operands DMA'd from HBM into LDS and fed to
+//    v_mfma_i32_32x32x32_i8; the fp32 rescale and bias are the epilogue.
+//
+// Exactness. The int32 sum of int8 products is exact in any order (|sum| < 2^31 for
+// K < 131072), so the only roundings are the reference's own elementwise ones:
+//   scale_x = clamp(round_T(max|x| * fp32(1/127)), min = round_T(1e-8))
+//     (torch evaluates a tensor / Python-scalar division on the GPU as a product with the
+//     fp32 reciprocal; the clamp bound is the scalar converted to T, 0 for fp16)
+//   x_q     = clamp(rint(fp32(x) / scale_x), -128, 127)   (IEEE division, NaN -> 0)
+//   y       = round_T( fp32(acc) * (scale_x * scale_w)  [+ fp32(bias)] )
+// each product and sum rounded once to fp32, never fused, so the output is bit-identical
+// to the reference's sequence of elementwise kernels.
+//
+// Weights. The reference stores weight_q_t [K, N] (int8, N contiguous) for _int_mm. The
+// kernels read the tiled INT8 layout (lsq_internal.h, 16 x 128 tiles of 2 KB) built from
+// weight_q_t by lsq_w8a8_retile, with K padded to a multiple of 128 with zero columns
+// (the activation workspace is padded the same way, so the padding adds nothing).
+
+#include "lsq_common.h"
+#include "lsq_internal.h"
+#include "lsq_decode.h"
+
+#include <atomic>
+#include <cstdlib>
+#include <cstring>
+
+namespace lsq {
+namespace {
+
+__host__ __device__ constexpr int64_t pad_k(int64_t K) { return (K + kTileK - 1) / kTileK * kTileK; }
+
+// ============================================================ activation quantization
+
+constexpr int kAqNT = 256;  // threads per token row
+constexpr int kAqR = 4;     // 16-byte chunks per thread kept in registers between passes
+
+// NaN-propagating max (torch.max returns NaN for a row holding one).
+__device__ __forceinline__ float nan_max(float a, float b) { return (b > a || b != b) ? b : a; }
+
+// rint(v / s) clamped to [-128, 127]; NaN (0 / 0 when the fp16 scale is 0) becomes 0.
+__device__ __forceinline__ int quant1(float v, float s) {
+  float q = __builtin_rintf(__fdiv_rn(v, s));
+  if (q != q) return 0;
+  q = q < -128.f ? -128.f : (q > 127.f ? 127.f : q);
+  return static_cast<int>(q);
+}
+
+template <int DT>
+__global__ void __launch_bounds__(kAqNT) act_quant_kernel(const void* __restrict__ x, int64_t ldx,
+                                                          int K, int Kz, bool vec,
+                                                          int8_t* __restrict__ xq, int64_t ldq,
+                                                          float* __restrict__ sx) {
+  using S = typename Act<DT>::storage;
+  constexpr int E = 16 / static_cast<int>(sizeof(S));  // elements per 16-byte chunk
+  __shared__ float wmax[kAqNT / 64];
+  const int m = blockIdx.x;
+  const int tid = threadIdx.x;
+  const S* xr = static_cast<const S*>(x) + static_cast<int64_t>(m) * ldx;
+  int8_t* qr = xq + static_cast<int64_t>(m) * ldq;
+  auto elem = [](u32x4 v, int e) -> float {
+    if constexpr (E == 4) return __uint_as_float(v[e]);
+    else return Act<DT>::to_f32(static_cast<uint16_t>(v[e >> 1] >> (16 * (e & 1))));
+  };
+
+  // pass 1: max |x| (exact: |x| of a T value is a T value)
+  const int nch = vec ? K / E : 0;
+  u32x4 v[kAqR];
+  float mx = 0.f;
+#pragma unroll
+  for (int r = 0; r < kAqR; ++r) {
+    const int c = tid + r * kAqNT;
+    if (c < nch) {
+      v[r] = *reinterpret_cast<const u32x4*>(xr + c * E);
+#pragma unroll
+      for (int e = 0; e < E; ++e) mx = nan_max(mx, fabsf(elem(v[r], e)));
+    }
+  }
+  for (int c = tid + kAqR * kAqNT; c < nch; c += kAqNT) {
+    const u32x4 w = *reinterpret_cast<const u32x4*>(xr + c * E);
+#pragma unroll
+    for (int e = 0; e < E; ++e) mx = nan_max(mx, fabsf(elem(w, e)));
+  }
+  for (int k = nch * E + tid; k < K; k += kAqNT) mx = nan_max(mx, fabsf(Act<DT>::to_f32(xr[k])));
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) mx = nan_max(mx, __shfl_xor(mx, off, 64));
+  if ((tid & 63) == 0) wmax[tid >> 6] = mx;
+  __syncthreads();
+#pragma unroll
+  for (int w = 0; w < kAqNT / 64; ++w) mx = nan_max(mx, wmax[w]);
+
+  // scale: clamp(round_T(max * fp32(1/127)), round_T(1e-8)); the clamp keeps NaN
+  constexpr float kInv127 = 1.0f / 127.0f;
+  float s = Act<DT>::round(mul_nc(mx, kInv127));
+  const float smin = Act<DT>::round(1e-8f);
+  s = s < smin ? smin : s;
+  if (tid == 0) sx[m] = s;
+
+  // pass 2: quantize, E int8 per chunk
+  auto put = [&](int c, u32x4 w) {
+    uint32_t o[E / 4];
+#pragma unroll
+    for (int d = 0; d < E / 4; ++d) {
+      uint32_t b = 0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) b |= (static_cast<uint32_t>(quant1(elem(w, 4 * d + e), s)) & 0xFFu) << (8 * e);
+      o[d] = b;
+    }
+    if constexpr (E == 8) *reinterpret_cast<uint2*>(qr + c * E) = make_uint2(o[0], o[1]);
+    else *reinterpret_cast<uint32_t*>(qr + c * E) = o[0];
+  };
+#pragma unroll
+  for (int r = 0; r < kAqR; ++r) {
+    const int c = tid + r * kAqNT;
+    if (c < nch) put(c, v[r]);
+  }
+  for (int c = tid + kAqR * kAqNT; c < nch; c += kAqNT) put(c, *reinterpret_cast<const u32x4*>(xr + c * E));
+  for (int k = nch * E + tid; k < K; k += kAqNT) qr[k] = static_cast<int8_t>(quant1(Act<DT>::to_f32(xr[k]), s));
+  for (int k = K + tid; k < Kz; k += kAqNT) qr[k] = 0;  // padding columns
+}
+
+template <int DT>
+int launch_act_quant(const void* x, int64_t ldx, int64_t M, int64_t K, int64_t Kz, int8_t* xq,
+                     int64_t ldq, float* sx, hipStream_t s) {
+  using S = typename Act<DT>::storage;
+  constexpr int E = 16 / static_cast<int>(sizeof(S));
+  const bool vec = (reinterpret_cast<uintptr_t>(x) & 15) == 0 && ldx % E == 0 &&
+                   (reinterpret_cast<uintptr_t>(xq) & 7) == 0 && ldq % 8 == 0;
+  act_quant_kernel<DT><<<dim3(static_cast<unsigned>(M)), dim3(kAqNT), 0, s>>>(
+      x, ldx, static_cast<int>(K), static_cast<int>(Kz), vec, xq, ldq, sx);
+  return static_cast<int>(hipGetLastError());
+}
+
+// ============================================================ re-tile from weight_q_t
+
+// One thread per dword of the tiled layout: dword (tile, half j, lane l, d) holds
+// W[16 rt + (l & 15)][128 kt + 32 (l >> 4) + 16 j + 4 d + e], e = 0..3, with
+// W[n][k] = weight_q_t[k][n]; zero past N or K.
+__global__ void w8a8_retile_kernel(const int8_t* __restrict__ wt, uint32_t* __restrict__ tiled,
+                                   int64_t N, int64_t K, int64_t nkt, int64_t total) {
+  const int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
+  if (i >= total) return;
+  const int d = static_cast<int>(i & 3);
+  const int l = static_cast<int>((i >> 2) & 63);
+  const int j = static_cast<int>((i >> 8) & 1);
+  const int64_t tile = i >> 9;
+  const int64_t rt = tile / nkt, kt = tile - rt * nkt;
+  const int64_t n = 16 * rt + (l & 15);
+  const int64_t k0 = 128 * kt + 32 * (l >> 4) + 16 * j + 4 * d;
+  uint32_t v = 0;
+  if (n < N) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if (k0 + e < K) v |= (static_cast<uint32_t>(static_cast<uint8_t>(wt[(k0 + e) * N + n]))) << (8 * e);
+  }
+  tiled[i] = v;
+}
+
+// Inverse: one thread per element of weight_q_t [K, N].
+__global__ void w8a8_untile_kernel(const int8_t* __restrict__ tiled, int8_t* __restrict__ wt,
+                                   int64_t N, int64_t K, int64_t nkt) {
+  const int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
+  if (i >= N * K) return;
+  const int64_t k = i / N, n = i - k * N;
+  const int64_t rt = n >> 4, kt = k >> 7;
+  const int c = static_cast<int>(k & 127);
+  const int l = static_cast<int>(n & 15) + 16 * (c >> 5);
+  const int j = (c >> 4) & 1;
+  wt[i] = tiled[(rt * nkt + kt) * kTileBytes8 + j * (kTileBytes8 / 2) + l * 16 + (c & 15)];
+}
+
+// ============================================================ prefill GEMM
+//
+// A workgroup computes a 256 x 256 tile of y with 8 waves in a 2 x 4 layout; each wave
+// owns 128 x 64 outputs as 4 x 2 blocks of v_mfma_i32_32x32x32_i8 (int32 accumulators).
+// K advances 128 columns (one k tile) per step; the x_q tile [256, 128] and the weight
+// tile [256 rows, 128] both go from HBM / L2 into LDS with buffer_load ... lds, one step
+// ahead, double-buffered, one barrier per step. Both LDS tiles store row r's 16-byte
+// chunk c at position c ^ ((r >> 1) & 7), so the 16-byte MFMA operand reads (16 rows at
+// one chunk) spread over all 64 banks. Consecutive workgroups take consecutive M tiles of
+// one N tile (they share its weights in L2), and each starts at a different k step
+// (K rotation) so that the ~32 workgroups resident on one XCD do not all miss on the
+// same activation tile at once; the int32 sums do not depend on the order.
+constexpr int QBM = 256, QBN = 256, QBK = 128, QNT = 512;
+constexpr int QWTM = 128, QWTN = 64;
+constexpr int QFM = QWTM / 32, QFN = QWTN / 32;
+constexpr int kQTile = QBM * QBK;     // bytes of one operand tile
+constexpr int kQLds = 4 * kQTile;     // {x, w} x 2 stages
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x16 __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ i32x16 mma32_i8(u32x4 a, u32x4 b, i32x16 c) {
+  return __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(i32x4, a),
+                                               __builtin_bit_cast(i32x4, b), c, 0, 0, 0);
+}
+
+template <int DT>
+__global__ void __launch_bounds__(QNT) w8a8_gemm_kernel(LinearArgs p) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  using S = typename Act<DT>::storage;
+  const int M = static_cast<int>(p.M), N = static_cast<int>(p.N), K = static_cast<int>(p.K);
+  const int nsteps = K / QBK;  // one k tile per step
+  const int mtiles = (M + QBM - 1) / QBM;
+  const int mt = blockIdx.x % mtiles;
+  const int nt = blockIdx.x / mtiles;
+  const int m0 = mt * QBM, n0 = nt * QBN;
+  const int rows_m = min(QBM, M - m0);
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wid & 1, wn = wid >> 1;
+  const int rot = (((blockIdx.x >> 3) & 31) * nsteps) >> 5;
+  auto gstep = [&](int st) { const int g = st + rot; return g >= nsteps ? g - nsteps : g; };
+  auto xs_at = [&](int buf) { return smem + buf * kQTile; };
+  auto ws_at = [&](int buf) { return smem + (2 + buf) * kQTile; };
+
+  // ---- descriptors: rows past M and row tiles past N read zeros (the row part of every
+  // offset is in the range-checked per-lane offset; the scalar offset carries the k step)
+  const rsrc_t rx = make_rsrc(static_cast<const int8_t*>(p.x) + static_cast<int64_t>(m0) * p.ldx,
+                              static_cast<uint32_t>((rows_m - 1) * p.ldx + K));
+  const int rt0 = n0 / kTileN;
+  const int nrt = (N + kTileN - 1) / kTileN;
+  const rsrc_t rw = make_rsrc(p.w + static_cast<int64_t>(rt0) * nsteps * kTileBytes8,
+                              static_cast<uint32_t>(min(QBN / kTileN, nrt - rt0) * nsteps * kTileBytes8));
+
+  // One wave DMA instruction fills 8 rows of a tile (1 KB): lane l writes row
+  // rb + (l >> 3), position l & 7, i.e. chunk (l & 7) ^ ((b & 1) << 2 | (l >> 4)).
+  constexpr int kB = QBM / 8 / (QNT / 64);  // 4 row blocks of 8 per wave per operand
+  uint32_t xo[kB], wo[kB];
+#pragma unroll
+  for (int b = 0; b < kB; ++b) {
+    const int r = (wid * kB + b) * 8 + (lane >> 3);
+    const int c = (lane & 7) ^ (((b & 1) << 2) | (lane >> 4));
+    xo[b] = static_cast<uint32_t>(r * p.ldx + c * 16);
+    // tiled weights: row r is lane (r & 15) + 16 (c >> 1) of half (c & 1) of its tile
+    wo[b] = static_cast<uint32_t>((r >> 4) * nsteps * kTileBytes8 + (c & 1) * (kTileBytes8 / 2) +
+                                  ((r & 15) + 16 * (c >> 1)) * 16);
+  }
+  auto issue = [&](int st, int buf) {
+    const int g = gstep(st);
+#pragma unroll
+    for (int b = 0; b < kB; ++b) {
+      const int rb = (wid * kB + b) * 8;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rx, (__attribute__((address_space(3))) void*)(xs_at(buf) + rb * QBK), 16, xo[b],
+          g * QBK, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rw, (__attribute__((address_space(3))) void*)(ws_at(buf) + rb * QBK), 16, wo[b],
+          g * kTileBytes8, 0, 0);
+    }
+  };
+
+  i32x16 acc[QFM][QFN];
+#pragma unroll
+  for (int i = 0; i < QFM; ++i)
+#pragma unroll
+    for (int j = 0; j < QFN; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0;
+  // MFMA operands: lane l reads row (l & 31) of a 32-row block, 16 columns at
+  // 32 kk + 16 (l >> 5), i.e. chunk 2 kk + (l >> 5), through the swizzle.
+  const int frow = lane & 31;
+  auto frag_off = [&](int kk) {
+    return frow * QBK + (((2 * kk + (lane >> 5)) ^ ((frow >> 1) & 7)) << 4);
+  };
+  auto compute = [&](int buf) {
+    const unsigned char* xb = xs_at(buf) + wm * QWTM * QBK;
+    const unsigned char* wb = ws_at(buf) + wn * QWTN * QBK;
+    u32x4 a[2][QFM], b[2][QFN];
+    auto load = [&](int kk, u32x4 (&aa)[QFM], u32x4 (&bb)[QFN]) {
+      const int off = frag_off(kk);
+#pragma unroll
+      for (int i = 0; i < QFM; ++i) aa[i] = *reinterpret_cast<const u32x4*>(xb + 32 * i * QBK + off);
+#pragma unroll
+      for (int j = 0; j < QFN; ++j) bb[j] = *reinterpret_cast<const u32x4*>(wb + 32 * j * QBK + off);
+    };
+    load(0, a[0], b[0]);
+#pragma unroll
+    for (int kk = 0; kk < QBK / 32; ++kk) {
+      if (kk + 1 < QBK / 32) load(kk + 1, a[(kk + 1) & 1], b[(kk + 1) & 1]);
+#pragma unroll
+      for (int i = 0; i < QFM; ++i)
+#pragma unroll
+        for (int j = 0; j < QFN; ++j) acc[i][j] = mma32_i8(a[kk & 1][i], b[kk & 1][j], acc[i][j]);
+    }
+  };
+
+  constexpr int kWaitAll = (7 << 4);  // vmcnt(0) lgkmcnt(0)
+  issue(0, 0);
+  __builtin_amdgcn_s_waitcnt(kWaitAll);
+  lds_barrier();
+  for (int st = 0; st < nsteps; ++st) {
+    const int buf = st & 1;
+    if (st + 1 < nsteps) issue(st + 1, buf ^ 1);  // into the stage read one step ago
+    compute(buf);
+    __builtin_amdgcn_s_waitcnt(kWaitAll);
+    lds_barrier();
+  }
+
+  // ---- epilogue: y = fp32(acc) * (sx[m] * sw[n]) [+ fp32(bias[n])], rounded to T
+  float* sxs = reinterpret_cast<float*>(smem);  // the tile's token scales (LDS is free now)
+  if (tid < QBM) sxs[tid] = tid < rows_m ? p.xscale[m0 + tid] : 0.f;
+  lds_barrier();
+  float swn[QFN], bsn[QFN];
+#pragma unroll
+  for (int j = 0; j < QFN; ++j) {
+    const int n = n0 + wn * QWTN + 32 * j + (lane & 31);
+    swn[j] = n < N ? load_as_f32(p.scale, p.scale_dt, n) : 0.f;
+    bsn[j] = (p.bias && n < N) ? load_as_f32(p.bias, p.bias_dt, n) : 0.f;
+  }
+  S* y = static_cast<S*>(p.y);
+#pragma unroll
+  for (int i = 0; i < QFM; ++i)
+#pragma unroll
+    for (int j = 0; j < QFN; ++j) {
+      const int n = n0 + wn * QWTN + 32 * j + (lane & 31);
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int ml = wm * QWTM + 32 * i + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+        const int m = m0 + ml;
+        if (m < M && n < N) {
+          float r = mul_nc(static_cast<float>(acc[i][j][v]), mul_nc(sxs[ml], swn[j]));
+          if (p.bias) r = add_nc(r, bsn[j]);
+          y[static_cast<int64_t>(m) * p.ldy + n] = Act<DT>::from_f32(r);
+        }
+      }
+    }
+}
+
+int g_max_lds_q = -1;
+
+int max_lds_q() {
+  int v = g_max_lds_q;
+  if (v < 0) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess)
+      v = 64 * 1024;
+    g_max_lds_q = v;
+  }
+  return v;
+}
+
+template <int DT>
+int launch_w8a8_gemm(const LinearArgs& a, hipStream_t s) {
+  if (a.K % QBK != 0 || a.K < QBK || !a.xscale) return LSQ_E_LAYOUT;
+  if (kQLds > max_lds_q()) return LSQ_E_LAYOUT;
+  if ((a.M - 1) * a.ldx + a.K >= (int64_t(1) << 31) || (a.ldx % 16) != 0) return LSQ_E_LAYOUT;
+  if (int64_t(QBN / kTileN) * a.K * kTileN >= (int64_t(1) << 31)) return LSQ_E_LAYOUT;
+  auto kern = w8a8_gemm_kernel<DT>;
+  static std::atomic<int> attr_set{0};
+  if (!attr_set.load(std::memory_order_acquire)) {
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, kQLds);
+    if (e != hipSuccess) return static_cast<int>(e);
+    attr_set.store(1, std::memory_order_release);
+  }
+  const int64_t tiles = ((a.M + QBM - 1) / QBM) * ((a.N + QBN - 1) / QBN);
+  if (tiles > INT32_MAX) return LSQ_E_SHAPE;
+  kern<<<dim3(static_cast<unsigned>(tiles)), dim3(QNT), kQLds, s>>>(a);
+  return static_cast<int>(hipGetLastError());
+}
+
+// LSQ_W8A8_PATH=gemm sends every M to the GEMM kernel (for comparisons and tests).
+bool force_gemm() {
+  const char* e = std::getenv("LSQ_W8A8_PATH");
+  return e && std::strcmp(e, "gemm") == 0;
+}
+
+// Decode kernel for M <= 64 while the int8 activations fit in LDS; otherwise the same in
+// blocks of 32 or 16 tokens (the weights are streamed once per block), and the GEMM when
+// not even 16 tokens fit or M > 64.
+template <int DT>
+int run_w8a8(const LinearArgs& a, hipStream_t s) {
+  if (a.M <= 64 && !force_gemm()) {
+    int rc = launch_decode_a8<DT>(a, s);
+    if (rc != LSQ_E_LAYOUT) return rc;
+    using Sy = typename Act<DT>::storage;
+    for (int64_t blk : {int64_t(32), int64_t(16)}) {
+      if (blk >= a.M) continue;
+      LinearArgs b = a;
+      b.M = blk;
+      rc = launch_decode_a8<DT>(b, s);  // block 0; LSQ_E_LAYOUT: does not fit, nothing ran
+      if (rc == LSQ_E_LAYOUT) continue;
+      if (rc != LSQ_OK) return rc;
+      for (int64_t m0 = blk; m0 < a.M; m0 += blk) {
+        b.x = static_cast<const int8_t*>(a.x) + m0 * a.ldx;
+        b.y = static_cast<Sy*>(a.y) + m0 * a.ldy;
+        b.xscale = a.xscale + m0;
+        b.M = a.M - m0 < blk ? a.M - m0 : blk;
+        rc = launch_decode_a8<DT>(b, s);
+        if (rc != LSQ_OK) return rc;
+      }
+      return LSQ_OK;
+    }
+  }
+  return launch_w8a8_gemm<DT>(a, s);
+}
+
+bool valid_dt(int dt) { return dt == LSQ_F32 || dt == LSQ_F16 || dt == LSQ_BF16; }
+
+}  // namespace
+}  // namespace lsq
+
+using namespace lsq;
+
+extern "C" int64_t lsq_w8a8_tiled_bytes(int64_t N, int64_t K) {
+  if (N <= 0 || K <= 0) return 0;
+  return (N + kTileN - 1) / kTileN * kTileN * pad_k(K);
+}
+
+extern "C" int lsq_w8a8_retile(const int8_t* weight_q_t, int8_t* tiled, int64_t N, int64_t K,
+                               void* stream) {
+  if (N < 0 || K < 0) return LSQ_E_SHAPE;
+  if (N == 0 || K == 0) return LSQ_OK;
+  if (!weight_q_t || !tiled) return LSQ_E_NULL;
+  if (reinterpret_cast<uintptr_t>(tiled) & 15) return LSQ_E_ALIGN;
+  const int64_t nkt = pad_k(K) / kTileK;
+  const int64_t total = lsq_w8a8_tiled_bytes(N, K) / 4;
+  const int64_t blocks = (total + 255) / 256;
+  if (blocks > INT32_MAX) return LSQ_E_SHAPE;
+  w8a8_retile_kernel<<<dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream)>>>(weight_q_t, reinterpret_cast<uint32_t*>(tiled),
+                                                           N, K, nkt, total);
+  return static_cast<int>(hipGetLastError());
+}
+
+extern "C" int lsq_w8a8_untile(const int8_t* tiled, int8_t* weight_q_t, int64_t N, int64_t K,
+                               void* stream) {
+  if (N < 0 || K < 0) return LSQ_E_SHAPE;
+  if (N == 0 || K == 0) return LSQ_OK;
+  if (!weight_q_t || !tiled) return LSQ_E_NULL;
+  const int64_t blocks = (N * K + 255) / 256;
+  if (blocks > INT32_MAX) return LSQ_E_SHAPE;
+  w8a8_untile_kernel<<<dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream)>>>(tiled, weight_q_t, N, K, pad_k(K) / kTileK);
+  return static_cast<int>(hipGetLastError());
+}
+
+extern "C" int lsq_act_quant_i8(const void* x, int64_t ldx, int dtype, int64_t M, int64_t K,
+                                int8_t* x_q, int64_t ldq, float* scale_x, void* stream) {
+  if (M < 0 || K < 1 || ldx < K || ldq < K) return LSQ_E_SHAPE;
+  if (M > INT32_MAX || K > INT32_MAX / 2) return LSQ_E_SHAPE;
+  if (!valid_dt(dtype)) return LSQ_E_DTYPE;
+  if (M == 0) return LSQ_OK;
+  if (!x || !x_q || !scale_x) return LSQ_E_NULL;
+  const int64_t kz = pad_k(K) < ldq ? pad_k(K) : ldq;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case LSQ_F32: return launch_act_quant<LSQ_F32>(x, ldx, M, K, kz, x_q, ldq, scale_x, s);
+    case LSQ_F16: return launch_act_quant<LSQ_F16>(x, ldx, M, K, kz, x_q, ldq, scale_x, s);
+    default: return launch_act_quant<LSQ_BF16>(x, ldx, M, K, kz, x_q, ldq, scale_x, s);
+  }
+}
+
+extern "C" int lsq_w8a8_linear(const void* x, int64_t ldx, const int8_t* tiled,
+                               const void* scale_w, int scale_w_dtype, const void* bias,
+                               int bias_dtype, void* y, int64_t ldy, int dtype, int64_t M,
+                               int64_t N, int64_t K, int8_t* x_q, float* scale_x, void* stream) {
+  if (M < 0 || N < 0 || K < 1 || ldx < K || ldy < N) return LSQ_E_SHAPE;
+  if (M > INT32_MAX / 2 || N > INT32_MAX / 2 || K >= 131072) return LSQ_E_SHAPE;
+  if (!valid_dt(dtype) || !valid_dt(scale_w_dtype) || (bias && !valid_dt(bias_dtype))) return LSQ_E_DTYPE;
+  if (M == 0 || N == 0) return LSQ_OK;
+  if (!x || !tiled || !scale_w || !y || !x_q || !scale_x) return LSQ_E_NULL;
+  if ((reinterpret_cast<uintptr_t>(tiled) & 15) || (reinterpret_cast<uintptr_t>(x_q) & 15))
+    return LSQ_E_ALIGN;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t kp = pad_k(K);
+  int rc = lsq_act_quant_i8(x, ldx, dtype, M, K, x_q, kp, scale_x, stream);
+  if (rc != LSQ_OK) return rc;
+  LinearArgs a{x_q, kp, reinterpret_cast<const uint8_t*>(tiled), scale_w, scale_w_dtype, bias,
+               bias_dtype, y, ldy, M, N, kp, kp, 1, scale_x};
+  switch (dtype) {
+    case LSQ_F32: rc = run_w8a8<LSQ_F32>(a, s); break;
+    case LSQ_F16: rc = run_w8a8<LSQ_F16>(a, s); break;
+    default: rc = run_w8a8<LSQ_BF16>(a, s); break;
+  }
+  return rc == LSQ_E_LAYOUT ? LSQ_E_SHAPE : rc;
+}

@@ -10,6 +10,11 @@ liblsq.so through its C ABI on the caller's current HIP stream. They never fall 
 a CPU or library implementation; on a CPU tensor, or without the built library, they
 raise.
 
+The 'hybrid_int8' mode's two layer types are here too: `CachedQuantizedLinear`
+(:184-284, dequantized once at load, then a dense layer) and `Int8GEMMLinear` (:287-459,
+W8A8: per-token int8 activations x int8 weights on the gfx950 int8 MFMA, bit-exact with
+the reference's fp32 rescale), with `can_use_int8_gemm` (:152-181).
+
 Extensions beyond the reference (all opt-in, defaults reproduce the reference):
   * `group_size` for INT4: scales `[N, ceil(K/group_size)]`, default `None` = the
     reference's per-output-channel scale `[N, 1]`.
@@ -53,10 +58,10 @@ def _use_tiled_layout() -> bool:
     return os.environ.get("LSQ_WEIGHT_LAYOUT", "tiled").lower() != "canonical"
 
 
-def _require_gpu(t: torch.Tensor, what: str) -> None:
+def _require_gpu(t: torch.Tensor, what: str, owner: str = "QuantizedLinear") -> None:
     if t.device.type != "cuda":
         raise RuntimeError(
-            f"QuantizedLinear.{what}: the quantized kernels run on the GPU only; "
+            f"{owner}.{what}: the quantized kernels run on the GPU only; "
             f"got a tensor on {t.device}. Move the module and its inputs to a HIP device "
             "(module.to('cuda'))."
         )
@@ -490,6 +495,341 @@ def fuse_linears(layers: List[QuantizedLinear]) -> FusedQuantizedLinear:
     return FusedQuantizedLinear(fused, [l.out_features for l in layers])
 
 
+# ---------------------------------------------------------------------------- W8A8
+
+
+def _int8_gemm_disabled() -> bool:
+    return os.getenv("MINIVLLM_DISABLE_INT8_GEMM", "0").lower() in ("1", "true", "yes")
+
+
+def can_use_int8_gemm(device: Optional[Union[torch.device, str]] = None) -> Tuple[bool, str]:
+    """Whether Int8GEMMLinear can run its W8A8 kernels (quantization.py:152-181).
+
+    Same checks in the same order, for this library's requirements: the kill switch
+    MINIVLLM_DISABLE_INT8_GEMM, a HIP device, the device being a gfx950 (the kernels are
+    built for it; the reference asks for SM >= 8.0 instead) and liblsq.so being built.
+    """
+    if _int8_gemm_disabled():
+        return False, "Disabled by MINIVLLM_DISABLE_INT8_GEMM environment variable"
+    if not torch.cuda.is_available():
+        return False, "HIP device is not available"
+    if device is not None:
+        dev = torch.device(device)
+        if dev.type != "cuda":
+            return False, f"Device type is '{dev.type}', but INT8 GEMM requires 'cuda'"
+        dev_idx = dev.index if dev.index is not None else torch.cuda.current_device()
+    else:
+        dev_idx = torch.cuda.current_device()
+    try:
+        arch = torch.cuda.get_device_properties(dev_idx).gcnArchName.split(":")[0]
+    except Exception as e:  # noqa: BLE001
+        return False, f"Failed to query device architecture: {e}"
+    if arch != "gfx950":
+        return False, f"Device architecture {arch} is not gfx950"
+    try:
+        _lib.load()
+    except RuntimeError as e:
+        return False, str(e)
+    return True, f"Supported ({arch})"
+
+
+def _quantize_rows_int8(w: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+    """(int8 q [N, K], fp32 scale [N, 1]): per-row symmetric INT8 (quantization.py:228-231,
+    :341-344), evaluated with torch on the weight's device as the reference does."""
+    w = w.float()
+    max_val = torch.max(torch.abs(w), dim=-1, keepdim=True)[0]
+    scale = torch.clamp(max_val / 127.0, min=1e-8)
+    w_q = torch.clamp(torch.round(w / scale), -128, 127).to(torch.int8)
+    return w_q, scale
+
+
+def _layer_dtype(dtype: Optional[torch.dtype], float_linear: nn.Linear) -> torch.dtype:
+    dt = dtype or float_linear.weight.dtype
+    return dt if dt in (torch.float16, torch.bfloat16, torch.float32) else torch.float16
+
+
+def _footprint(module: nn.Module) -> int:
+    total = 0
+    for b in module.buffers():
+        total += b.numel() * b.element_size()
+    for p in module.parameters():
+        total += p.numel() * p.element_size()
+    return total
+
+
+class CachedQuantizedLinear(nn.Module):
+    """Dense layer holding INT8-quantized-then-dequantized weights (quantization.py:184-284).
+
+    The attention projections of 'hybrid_int8': the weight is quantized per row to INT8
+    and dequantized back to `dtype` once, at construction, so forward is a plain dense
+    F.linear (a library GEMM; there is no quantized arithmetic left to run).
+    """
+
+    def __init__(self, in_features: int, out_features: int, bias: bool = False,
+                 dtype: torch.dtype = torch.float16):
+        super().__init__()
+        self.in_features = in_features
+        self.out_features = out_features
+        self.dtype = dtype
+        self.register_buffer("weight", torch.zeros((out_features, in_features), dtype=dtype))
+        if bias:
+            self.bias = nn.Parameter(torch.zeros(out_features, dtype=dtype))
+        else:
+            self.register_parameter("bias", None)
+
+    @classmethod
+    def from_float(cls, float_linear: nn.Linear,
+                   dtype: Optional[torch.dtype] = None) -> "CachedQuantizedLinear":
+        """Quantize per row to INT8, dequantize to `dtype` (default: the layer's dtype,
+        fp16 when that is not a float type) once (quantization.py:212-240)."""
+        dt = _layer_dtype(dtype, float_linear)
+        layer = cls(float_linear.in_features, float_linear.out_features,
+                    bias=float_linear.bias is not None, dtype=dt)
+        w_q, scale = _quantize_rows_int8(float_linear.weight.data)
+        layer.weight.copy_((w_q.float() * scale).to(dt))
+        if float_linear.bias is not None:
+            layer.bias.data.copy_(float_linear.bias.data.to(dt))
+        layer.to(float_linear.weight.device)
+        return layer
+
+    @classmethod
+    def from_quantized(cls, weight_q: torch.Tensor, scale: torch.Tensor,
+                       bias: Optional[torch.Tensor] = None,
+                       dtype: torch.dtype = torch.float16) -> "CachedQuantizedLinear":
+        """Install INT8 weights [N, K] with scale [N, 1] (quantization.py:242-256)."""
+        out_f, in_f = weight_q.shape
+        layer = cls(in_f, out_f, bias=bias is not None, dtype=dtype)
+        layer.weight.copy_((weight_q.float() * scale.float()).to(dtype))
+        if bias is not None:
+            layer.bias.data.copy_(bias.to(dtype))
+        layer.to(weight_q.device)
+        return layer
+
+    def dequantize(self, dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+        """The cached weight (quantization.py:258-262)."""
+        if dtype is not None and self.weight.dtype != dtype:
+            return self.weight.to(dtype)
+        return self.weight
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        """F.linear with the cached weight and bias cast to x's device and dtype
+        (quantization.py:264-276)."""
+        w = self.weight
+        if w.device != x.device:
+            w = w.to(x.device)
+        if w.dtype != x.dtype:
+            w = w.to(x.dtype)
+        bias = self.bias
+        if bias is not None:
+            if bias.device != x.device:
+                bias = bias.to(x.device)
+            if bias.dtype != x.dtype:
+                bias = bias.to(x.dtype)
+        return F.linear(x, w, bias)
+
+    def memory_footprint_bytes(self) -> int:
+        """Bytes of all buffers and parameters (quantization.py:278-284)."""
+        return _footprint(self)
+
+
+class Int8GEMMLinear(nn.Module):
+    """W8A8 linear layer: per-output-channel INT8 weights, per-token INT8 activations
+    (quantization.py:287-459), the MLP projections of 'hybrid_int8'.
+
+    Same buffers as the reference: `weight_q_t` int8 [in, out] (the transposed weight),
+    `scale_w_t` fp32 [1, out], `bias` in `dtype`; plus `weight_tiled`, a derived,
+    non-persistent copy re-tiled on the GPU for the kernels (rebuilt when the module
+    moves to a GPU or weight_q_t changes). forward runs liblsq's lsq_w8a8_linear:
+    activation quantization, int32 GEMM on the int8 MFMA and the fp32 rescale, with
+    results bit-identical to the reference's native path (quantization.py:404-447).
+
+    Differences from the reference: there is no CPU path (a CPU input raises, like
+    QuantizedLinear), and the fallback the reference takes for the kill switch
+    MINIVLLM_DISABLE_INT8_GEMM and for K or N not a multiple of 8 runs the weight-only
+    INT8 kernels (x times the dequantized weight, fp32 accumulation) instead of
+    F.linear; kernel errors raise instead of falling back.
+    """
+
+    def __init__(self, in_features: int, out_features: int, bias: bool = False,
+                 dtype: torch.dtype = torch.float16):
+        super().__init__()
+        self.in_features = in_features
+        self.out_features = out_features
+        self.output_dtype = dtype
+        self._warned_fallback = False
+        self.register_buffer("weight_q_t", torch.zeros((in_features, out_features), dtype=torch.int8))
+        self.register_buffer("scale_w_t", torch.zeros((1, out_features), dtype=torch.float32))
+        self.register_buffer("weight_tiled", torch.zeros(0, dtype=torch.int8), persistent=False)
+        self._tiled_key = None
+        self._wq_cache = None  # (key, weight_q [N, K]) for the fallback path
+        if bias:
+            self.bias = nn.Parameter(torch.zeros(out_features, dtype=dtype))
+        else:
+            self.register_parameter("bias", None)
+
+    @classmethod
+    def from_float(cls, float_linear: nn.Linear,
+                   dtype: Optional[torch.dtype] = None) -> "Int8GEMMLinear":
+        """Per-row INT8 quantization of an nn.Linear (quantization.py:326-353)."""
+        dt = _layer_dtype(dtype, float_linear)
+        layer = cls(float_linear.in_features, float_linear.out_features,
+                    bias=float_linear.bias is not None, dtype=dt)
+        w_q, scale = _quantize_rows_int8(float_linear.weight.data)
+        layer.weight_q_t.copy_(w_q.t().contiguous())
+        layer.scale_w_t.copy_(scale.t().contiguous())
+        if float_linear.bias is not None:
+            layer.bias.data.copy_(float_linear.bias.data.to(dt))
+        layer.to(float_linear.weight.device)
+        layer._refresh_tiled()
+        return layer
+
+    @classmethod
+    def from_quantized(cls, weight_q: torch.Tensor, scale: torch.Tensor,
+                       bias: Optional[torch.Tensor] = None,
+                       dtype: torch.dtype = torch.float16) -> "Int8GEMMLinear":
+        """Install INT8 weights [N, K] (row-major, as QuantizedLinear.weight_q) with scale
+        [N] or [N, 1] (pattern of quantization.py:242-256). Created on weight_q's device."""
+        if weight_q.dtype != torch.int8 or weight_q.dim() != 2:
+            raise ValueError("weight_q must be a 2-D torch.int8 tensor [out_features, in_features]")
+        n, k = weight_q.shape
+        layer = cls(k, n, bias=bias is not None, dtype=dtype)
+        layer.weight_q_t = weight_q.detach().t().contiguous()
+        layer.scale_w_t = scale.detach().float().reshape(1, n).clone()
+        if bias is not None:
+            layer.bias = nn.Parameter(bias.detach().to(device=weight_q.device, dtype=dtype).clone(),
+                                      requires_grad=False)
+        layer.to(weight_q.device)
+        layer._refresh_tiled()
+        return layer
+
+    # ------------------------------------------------------------------ tiled layout
+
+    def _refresh_tiled(self) -> None:
+        src = self.weight_q_t
+        if src.device.type != "cuda" or self.in_features == 0 or self.out_features == 0:
+            if self.weight_tiled.numel() != 0 or self.weight_tiled.device != src.device:
+                self.weight_tiled = torch.zeros(0, dtype=torch.int8, device=src.device)
+            self._tiled_key = None
+            return
+        if not src.is_contiguous():
+            src = src.contiguous()
+            self.weight_q_t = src
+        lib = _lib.load()
+        nbytes = lib.lsq_w8a8_tiled_bytes(self.out_features, self.in_features)
+        if self.weight_tiled.numel() != nbytes or self.weight_tiled.device != src.device:
+            self.weight_tiled = torch.empty(nbytes, dtype=torch.int8, device=src.device)
+        with torch.cuda.device(src.device):
+            _lib.check(lib.lsq_w8a8_retile(src.data_ptr(), self.weight_tiled.data_ptr(),
+                                           self.out_features, self.in_features,
+                                           _lib.stream_handle(src.device)), "lsq_w8a8_retile")
+        self._tiled_key = (src.data_ptr(), src._version, src.device)
+
+    def _apply(self, fn, recurse=True):
+        super()._apply(fn, recurse)
+        self._wq_cache = None
+        self._refresh_tiled()
+        return self
+
+    def _tiled_for_forward(self) -> torch.Tensor:
+        src = self.weight_q_t
+        if self._tiled_key != (src.data_ptr(), src._version, src.device):
+            self._refresh_tiled()
+        return self.weight_tiled
+
+    # ------------------------------------------------------------------ compute
+
+    def dequantize(self) -> torch.Tensor:
+        """(weight_q_t.t() * scale_w_t.t()) in output_dtype (quantization.py:355-357)."""
+        return (self.weight_q_t.t().float() * self.scale_w_t.t()).to(self.output_dtype)
+
+    def _fallback_forward(self, x: torch.Tensor, reason: str) -> torch.Tensor:
+        """Weight-only INT8 path (the reference dequantizes and calls F.linear,
+        quantization.py:359-377): liblsq's lsq_w8_linear on the transposed weight."""
+        if not self._warned_fallback:
+            _log.warning("Int8GEMMLinear falling back to dynamic dequantization: %s", reason)
+            self._warned_fallback = True
+        _require_gpu(x, "forward", "Int8GEMMLinear")
+        wt = self.weight_q_t
+        key = (wt.data_ptr(), wt._version, wt.device)
+        if self._wq_cache is None or self._wq_cache[0] != key:
+            self._wq_cache = (key, wt.t().contiguous())
+        w_q = self._wq_cache[1]
+        if w_q.device != x.device:
+            raise RuntimeError(f"Int8GEMMLinear.forward: input on {x.device} but weights on {w_q.device}")
+        x2 = x.reshape(-1, self.in_features)
+        if x2.stride(-1) != 1 or (x2.shape[0] > 1 and x2.stride(0) < self.in_features):
+            x2 = x2.contiguous()
+        m = x2.shape[0]
+        y = torch.empty((m, self.out_features), dtype=x.dtype, device=x.device)
+        scale = self.scale_w_t.reshape(-1)
+        scale = scale if scale.is_contiguous() else scale.contiguous()
+        bias = self.bias.detach().to(x.device).contiguous() if self.bias is not None else None
+        ldx = x2.stride(0) if m > 1 else self.in_features
+        with torch.cuda.device(x.device):
+            rc = _lib.load().lsq_w8_linear(
+                x2.data_ptr(), ldx, w_q.data_ptr(), None, scale.data_ptr(),
+                _lib.dtype_code(scale.dtype), _lib.ptr(bias),
+                _lib.dtype_code(bias.dtype) if bias is not None else 0, y.data_ptr(),
+                self.out_features, _lib.dtype_code(x.dtype), m, self.out_features,
+                self.in_features, _lib.stream_handle(x.device))
+        _lib.check(rc, "lsq_w8_linear")
+        return y.reshape(*x.shape[:-1], self.out_features)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        """W8A8 forward (quantization.py:379-447)."""
+        if _int8_gemm_disabled():
+            return self._fallback_forward(x, "MINIVLLM_DISABLE_INT8_GEMM is set")
+        _require_gpu(x, "forward", "Int8GEMMLinear")
+        if x.shape[-1] != self.in_features:
+            raise ValueError(
+                f"Input inner dimension {x.shape[-1]} does not match layer in_features {self.in_features}"
+            )
+        k, n = self.in_features, self.out_features
+        if k % 8 != 0 or n % 8 != 0:
+            return self._fallback_forward(x, f"K ({k}) or N ({n}) not divisible by 8")
+        if self.weight_q_t.device != x.device:
+            self.weight_q_t = self.weight_q_t.to(x.device)
+            self.scale_w_t = self.scale_w_t.to(x.device)
+        code = _lib.dtype_code(x.dtype)
+        x2 = x.reshape(-1, k)
+        if x2.stride(-1) != 1 or (x2.shape[0] > 1 and x2.stride(0) < k):
+            x2 = x2.contiguous()
+        m = x2.shape[0]
+        y = torch.empty((m, n), dtype=x.dtype, device=x.device)
+        if m == 0:
+            return y.reshape(*x.shape[:-1], n)
+        kp = -(-k // TILE_K) * TILE_K
+        x_q = torch.empty((m, kp), dtype=torch.int8, device=x.device)
+        scale_x = torch.empty(m, dtype=torch.float32, device=x.device)
+        scale = self.scale_w_t if self.scale_w_t.is_contiguous() else self.scale_w_t.contiguous()
+        bias = self.bias
+        bias_ptr, bias_code = None, 0
+        if bias is not None:
+            bias = bias.detach()
+            if bias.device != x.device:
+                bias = bias.to(x.device)
+            bias = bias.contiguous()
+            bias_ptr, bias_code = bias.data_ptr(), _lib.dtype_code(bias.dtype)
+        tiled = self._tiled_for_forward()
+        ldx = x2.stride(0) if m > 1 else k
+        with torch.cuda.device(x.device):
+            rc = _lib.load().lsq_w8a8_linear(
+                x2.data_ptr(), ldx, tiled.data_ptr(), scale.data_ptr(), _lib.dtype_code(scale.dtype),
+                bias_ptr, bias_code, y.data_ptr(), n, code, m, n, k, x_q.data_ptr(),
+                scale_x.data_ptr(), _lib.stream_handle(x.device))
+        _lib.check(rc, "lsq_w8a8_linear")
+        return y.reshape(*x.shape[:-1], n)
+
+    def memory_footprint_bytes(self) -> int:
+        """Bytes of all buffers and parameters (quantization.py:453-459), including the
+        derived tiled copy when it exists."""
+        return _footprint(self)
+
+    def extra_repr(self) -> str:
+        return (f"in_features={self.in_features}, out_features={self.out_features}, "
+                f"bias={self.bias is not None}, output_dtype={self.output_dtype}")
+
+
 # ---------------------------------------------------------------------------- helpers
 
 
@@ -517,10 +857,12 @@ def _group_scales(w: torch.Tensor, group_size: int, qmax: float) -> torch.Tensor
 def apply_optional_quantization(
     model: nn.Module, quant_type: str = "none", group_size: Optional[int] = None
 ) -> Tuple[int, int]:
-    """Replace the 7 transformer projections with QuantizedLinear (quantization.py:462-532).
+    """Replace the 7 transformer projections (quantization.py:462-532).
 
-    Returns (orig_weight_bytes, quantized_weight_bytes). `group_size` applies to int4.
-    The 'hybrid_int8' mode (W8A8 + cached fp16 layers) is not part of this library.
+    'int8' / 'int4': QuantizedLinear everywhere. 'hybrid_int8': CachedQuantizedLinear for
+    q/k/v/o, Int8GEMMLinear for gate/up/down when both dimensions are multiples of 8
+    (else QuantizedLinear int8, with a warning). Returns (orig_weight_bytes,
+    quantized_weight_bytes). `group_size` applies to int4.
     """
     quant_type = quant_type.lower()
     if quant_type not in VALID_MODES:
@@ -557,18 +899,24 @@ def apply_optional_quantization(
             f"blocks with standard self_attn (q, k, v, o) and mlp (gate, up, down) projections "
             f"(e.g., LLaMA, Qwen2, Mistral)."
         )
-    if quant_type == "hybrid_int8":
-        raise NotImplementedError(
-            "quantization 'hybrid_int8' (W8A8 Int8GEMMLinear + cached fp16 attention) is not "
-            "provided by localstrm_amd; use 'int8' or 'int4'"
-        )
-
     for parent, proj, mod in targets:
-        setattr(parent, proj, QuantizedLinear.from_float(mod, quant_type, group_size=group_size))
+        if quant_type != "hybrid_int8":
+            new = QuantizedLinear.from_float(mod, quant_type, group_size=group_size)
+        elif proj in ("q_proj", "k_proj", "v_proj", "o_proj"):
+            new = CachedQuantizedLinear.from_float(mod)
+        elif mod.in_features % 8 == 0 and mod.out_features % 8 == 0:
+            new = Int8GEMMLinear.from_float(mod)
+        else:
+            _log.warning(
+                "MLP layer %s shape (%d, %d) not divisible by 8; falling back to dynamic int8",
+                proj, mod.in_features, mod.out_features,
+            )
+            new = QuantizedLinear.from_float(mod, "int8")
+        setattr(parent, proj, new)
 
     quant_bytes = 0
     for m in model.modules():
-        if isinstance(m, QuantizedLinear):
+        if isinstance(m, (QuantizedLinear, Int8GEMMLinear, CachedQuantizedLinear)):
             quant_bytes += m.memory_footprint_bytes()
         elif len(list(m.children())) == 0:
             for p in m.parameters(recurse=False):

@@ -16,6 +16,11 @@ reference's behaviour (no code copied):
   dequant_int4        quantization.py:109-122 same closed form, s[n, k // group_size]
   linear              quantization.py:129-141 F.linear(x, W_T, bias_T), evaluated in
                       float64 then rounded once to T
+  act_scale_i8        quantization.py:412-413 per-token activation scale of
+                      Int8GEMMLinear, in the GPU's evaluation order (below)
+  act_quant_i8        quantization.py:411-414 per-token int8 activations
+  w8a8_linear         quantization.py:404-447 Int8GEMMLinear's native path: int32 GEMM,
+                      fp32 rescale, bias, one rounding to T (bit-exact target)
 
 How each part is pinned (tests/test_oracle.py):
   * round_bf16 / round_f16 against torch's dtype casts on every bf16 boundary case,
@@ -25,7 +30,12 @@ How each part is pinned (tests/test_oracle.py):
   * pack/unpack against a hand-written byte vector, all 256 byte values, round trip;
   * dequant exhaustively over all q values x random scales against torch casts;
   * linear against float64 closed forms (one-hot x, identity W) and torch's CPU GEMM;
-  * group-wise dequant reduces to the per-channel form when group_size = K.
+  * group-wise dequant reduces to the per-channel form when group_size = K;
+  * act_quant_i8 / w8a8_linear against hand-computed answers (scale 1 rows, round-half-
+    even ties, zero rows per dtype), torch's CPU ops for the quantization given the scale,
+    torch._int_mm plus torch's elementwise epilogue for the GEMM and rescale; the scale's
+    device evaluation order (product with fp32 1/127) against torch on the GPU over every
+    bf16 / fp16 value and random fp32 (tests/test_gpu_w8a8.py).
 """
 
 from __future__ import annotations
@@ -197,3 +207,59 @@ def rel_err(a, b) -> float:
     a = np.asarray(a, dtype=np.float64)
     b = np.asarray(b, dtype=np.float64)
     return float(np.max(np.abs(a - b)) / max(float(np.max(np.abs(b))), 1e-6))
+
+
+# ----------------------------------------------------------------------------- W8A8
+
+INV127_F32 = np.float32(1.0) / np.float32(127.0)
+
+
+def act_scale_i8(x, dt: str) -> np.ndarray:
+    """Per-token scale of Int8GEMMLinear.forward (quantization.py:412-413) as fp32 [M, 1]:
+    clamp(max|x| / 127.0, min=1e-8) in the activation type T.
+
+    max|x| is exact in T. torch evaluates `tensor / 127.0` (a Python scalar) on the GPU as
+    tensor * fp32(1/127) in fp32, then rounds to T; the reference only quantizes
+    activations on the GPU (its CPU path is the dequantizing fallback), so that is the
+    order restated here. The clamp bound is 1e-8 converted to T: bf16 1.0012e-8, fp16 0
+    (below the smallest subnormal), fp32 1e-8. NaN propagates.
+    """
+    x32 = np.asarray(x, dtype=np.float32)
+    mx = np.max(np.abs(x32), axis=-1, keepdims=True).astype(np.float32)
+    s = round_to((mx * INV127_F32).astype(np.float32), dt)
+    smin = round_to(np.float32(1e-8), dt)
+    return np.where(s < smin, smin, s).astype(np.float32)
+
+
+def act_quant_i8(x, dt: str) -> tuple[np.ndarray, np.ndarray]:
+    """(x_q int8 [M, K], scale_x fp32 [M, 1]): clamp(round_half_even(fp32(x) / s),
+    -128, 127) (quantization.py:414), fp32 division. A 0 / 0 (fp16 rows whose scale
+    rounds to 0) gives NaN, which converts to 0; with a zero scale the row's outputs are
+    0 * acc whatever x_q holds."""
+    x32 = np.asarray(x, dtype=np.float32)
+    s = act_scale_i8(x32, dt)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        r = np.rint(x32 / s)
+    r = np.clip(r, -128, 127)
+    r = np.where(np.isnan(r), 0, r)
+    return r.astype(np.int8), s
+
+
+def w8a8_linear(x, w_q, scale_w, bias=None, dt: str = BF16) -> np.ndarray:
+    """Int8GEMMLinear's native output (quantization.py:404-447) as fp32 values of T.
+
+    w_q int8 [N, K] (= weight_q_t transposed), scale_w [N] (scale_w_t), bias [N] as the
+    fp32 values of its stored dtype or None. acc = x_q @ w_q^T is exact (int32 range; it
+    is formed in float64, exact for these integer sums); then
+    y = round_T(fp32(acc) * fp32(scale_x * scale_w) [+ bias]), every step one fp32
+    rounding (:432-440, :446).
+    """
+    xq, sx = act_quant_i8(x, dt)
+    acc = xq.astype(np.float64) @ np.asarray(w_q, dtype=np.float64).T
+    if acc.size and np.abs(acc).max() >= 2.0 ** 31:
+        raise OverflowError("int32 accumulator range exceeded")
+    comb = (sx.reshape(-1, 1) * np.asarray(scale_w, dtype=np.float32).reshape(1, -1)).astype(np.float32)
+    out = (acc.astype(np.float32) * comb).astype(np.float32)
+    if bias is not None:
+        out = (out + np.asarray(bias, dtype=np.float32).reshape(1, -1)).astype(np.float32)
+    return round_to(out, dt)

@@ -1,0 +1,286 @@
+"""GPU parity for the W8A8 path (Int8GEMMLinear, src/kernels/quantization.py:287-459).
+
+The bar is bit-exactness: the int32 GEMM is exact and every other step is an IEEE
+elementwise operation, so the kernels' x_q, scale_x and y must equal the oracle's
+(oracle/quant_oracle.py act_quant_i8 / w8a8_linear) bit for bit. The scale's evaluation
+order on the device is pinned against torch itself on the GPU. Every call goes through
+the C ABI (directly, or via Int8GEMMLinear -> ctypes).
+"""
+
+import numpy as np
+import pytest
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from localstrm_amd import CachedQuantizedLinear, Int8GEMMLinear, QuantizedLinear, _lib
+from localstrm_amd import apply_optional_quantization
+from oracle import quant_oracle as qo
+from tests.synthetic import seeded_model
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda:0")
+TDT = {"f32": torch.float32, "f16": torch.float16, "bf16": torch.bfloat16}
+
+
+def _say(msg):
+    print(msg, flush=True)
+
+
+def _pad_k(k):
+    return -(-k // 128) * 128
+
+
+def _bits(a):
+    return np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+
+
+def _act_quant(x2, k, ldq=None):
+    """liblsq act quant of x2 [M, >=K] (GPU, any row stride)."""
+    m = x2.shape[0]
+    ldq = ldq or _pad_k(k)
+    xq = torch.full((m, ldq), 99, dtype=torch.int8, device=DEV)
+    sx = torch.empty(m, dtype=torch.float32, device=DEV)
+    rc = _lib.load().lsq_act_quant_i8(x2.data_ptr(), x2.stride(0), _lib.dtype_code(x2.dtype), m, k,
+                                      xq.data_ptr(), ldq, sx.data_ptr(), _lib.stream_handle(DEV))
+    _lib.check(rc, "lsq_act_quant_i8")
+    torch.cuda.synchronize()
+    return xq, sx
+
+
+def _linear(x2, wq, sw, bias, monkeypatch=None, path=None):
+    """liblsq W8A8 linear: x2 [M, K] (GPU), wq int8 [N, K], sw fp32 [N], bias or None."""
+    m, k = x2.shape
+    n = wq.shape[0]
+    lib = _lib.load()
+    wt = wq.t().contiguous().to(DEV)
+    tiled = torch.empty(lib.lsq_w8a8_tiled_bytes(n, k), dtype=torch.int8, device=DEV)
+    _lib.check(lib.lsq_w8a8_retile(wt.data_ptr(), tiled.data_ptr(), n, k, _lib.stream_handle(DEV)), "retile")
+    y = torch.empty((m, n), dtype=x2.dtype, device=DEV)
+    xq = torch.empty((m, _pad_k(k)), dtype=torch.int8, device=DEV)
+    sx = torch.empty(m, dtype=torch.float32, device=DEV)
+    swd = sw.to(DEV).contiguous()
+    b = bias.to(DEV).contiguous() if bias is not None else None
+    if path is not None:
+        monkeypatch.setenv("LSQ_W8A8_PATH", path)
+    rc = lib.lsq_w8a8_linear(x2.data_ptr(), x2.stride(0), tiled.data_ptr(), swd.data_ptr(),
+                             _lib.dtype_code(swd.dtype), _lib.ptr(b),
+                             _lib.dtype_code(b.dtype) if b is not None else 0, y.data_ptr(), n,
+                             _lib.dtype_code(x2.dtype), m, n, k, xq.data_ptr(), sx.data_ptr(),
+                             _lib.stream_handle(DEV))
+    if path is not None:
+        monkeypatch.delenv("LSQ_W8A8_PATH")
+    _lib.check(rc, "lsq_w8a8_linear")
+    torch.cuda.synchronize()
+    return y, xq, sx
+
+
+# ----------------------------------------------------------------------------- scale
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16", "f32"])
+def test_act_scale_matches_torch_on_the_device(dt):
+    """The oracle's scale (product with fp32 1/127, then round_T, then the clamp) equals
+    torch's own `max|x| / 127.0` clamp on the GPU, over every positive finite bf16 / fp16
+    value and 300k random fp32 magnitudes; liblsq's scale equals both."""
+    _say(f"act scale {dt}")
+    if dt == "bf16":
+        bits = np.arange(1, 0x7F80, dtype=np.uint32) << 16
+        vals = bits.view(np.float32)
+    elif dt == "f16":
+        vals = np.arange(1, 0x7C00, dtype=np.uint16).view(np.float16).astype(np.float32)
+    else:
+        rng = np.random.default_rng(0)
+        vals = (rng.uniform(0.5, 1.0, 300000) * 2.0 ** rng.integers(-40, 40, 300000)).astype(np.float32)
+    sign = np.where(np.arange(vals.size) % 2 == 0, 1.0, -1.0).astype(np.float32)
+    x = torch.from_numpy((vals * sign).reshape(-1, 1)).to(TDT[dt]).to(DEV)
+    x2 = torch.cat([x, x * 0.5], dim=1).contiguous()  # max|row| is the first column
+    dev = torch.clamp(torch.max(torch.abs(x2), dim=-1, keepdim=True)[0] / 127.0, min=1e-8).float()
+    ref = qo.act_scale_i8(x2.float().cpu().numpy(), dt)
+    _, sx = _act_quant(x2, 2)
+    assert np.array_equal(_bits(dev.cpu().numpy()), _bits(ref))
+    assert np.array_equal(_bits(sx.cpu().numpy().reshape(-1, 1)), _bits(ref))
+    if dt == "f32":  # the sample tells the two division orders apart
+        true_div = (np.abs(x2.float().cpu().numpy()).max(axis=1) / np.float32(127.0)).astype(np.float32)
+        assert np.count_nonzero(true_div != ref[:, 0]) > 1000
+
+
+# ----------------------------------------------------------------------------- x_q
+
+
+ACT_CASES = [(1, 896, 896), (7, 100, 100), (64, 3584, 3584), (300, 1024, 1024), (5, 8, 8),
+             (9, 72, 200), (3, 9000, 9000)]
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16", "f32"])
+@pytest.mark.parametrize("m,k,ldx", ACT_CASES)
+def test_act_quant_bit_exact(dt, m, k, ldx):
+    _say(f"act quant {dt} M={m} K={k} ldx={ldx}")
+    g = torch.Generator().manual_seed(m * 7 + k)
+    x = (torch.randn(m, ldx, generator=g) * torch.rand(m, 1, generator=g) * 8).to(TDT[dt])
+    if m >= 5:
+        x[1] = 0                       # zero row
+        x[2, : min(k, 4)] = 3e-7 if dt != "f16" else 6e-8  # tiny row
+        x[2, min(k, 4):] = 0
+        x[3, 0] = 250.0                # one large value
+    xd = x.to(DEV)
+    x2 = xd[:, :k]
+    xq, sx = _act_quant(x2, k)
+    ref_q, ref_s = qo.act_quant_i8(x[:, :k].float().numpy(), dt)
+    xq = xq.cpu().numpy()
+    assert np.array_equal(_bits(sx.cpu().numpy()), _bits(ref_s[:, 0]))
+    assert np.array_equal(xq[:, :k], ref_q)
+    assert (xq[:, k:_pad_k(k)] == 0).all()  # padding columns
+
+
+# ----------------------------------------------------------------------------- linear
+
+
+LIN_CASES = [
+    # (M, N, K): decode-shaped (M <= 64) then GEMM-shaped
+    (1, 272, 896), (5, 272, 896), (16, 1000, 896), (33, 272, 896), (64, 272, 896),
+    (1, 128, 64), (17, 136, 200), (1, 4864, 896),
+    (65, 520, 1024), (300, 264, 256), (257, 136, 64), (513, 1024, 384),
+]
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16", "f32"])
+@pytest.mark.parametrize("m,n,k", LIN_CASES)
+def test_w8a8_linear_bit_exact(dt, m, n, k):
+    _say(f"w8a8 {dt} M={m} N={n} K={k}")
+    g = torch.Generator().manual_seed(m + n + k)
+    x = (torch.randn(m, k, generator=g) * 2).to(TDT[dt])
+    wq = torch.randint(-128, 128, (n, k), generator=g, dtype=torch.int8)
+    sw = torch.rand(n, generator=g) * 0.02 + 1e-3
+    bias = (torch.randn(n, generator=g)).to(TDT[dt]) if (m + n) % 2 else None
+    y, _, _ = _linear(x.to(DEV), wq, sw, bias)
+    ref = qo.w8a8_linear(x.float().numpy(), wq.numpy(), sw.numpy(),
+                         None if bias is None else bias.float().numpy(), dt)
+    got = y.float().cpu().numpy()
+    mism = np.count_nonzero(_bits(got) != _bits(ref))
+    assert mism == 0, f"{mism} of {got.size} outputs differ"
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 272, 896), (33, 272, 896), (64, 520, 1024)])
+def test_w8a8_gemm_kernel_on_decode_shapes(monkeypatch, m, n, k):
+    # the prefill kernel must give the same bits as the decode kernel (and the oracle)
+    _say(f"w8a8 gemm-forced M={m} N={n} K={k}")
+    g = torch.Generator().manual_seed(3 * m + k)
+    x = torch.randn(m, k, generator=g).to(torch.bfloat16).to(DEV)
+    wq = torch.randint(-128, 128, (n, k), generator=g, dtype=torch.int8)
+    sw = torch.rand(n, generator=g) * 0.02 + 1e-3
+    bias = torch.randn(n, generator=g).to(torch.bfloat16)
+    y_dec, _, _ = _linear(x, wq, sw, bias)
+    y_gemm, _, _ = _linear(x, wq, sw, bias, monkeypatch, "gemm")
+    assert torch.equal(y_dec.view(torch.int16), y_gemm.view(torch.int16))
+
+
+@pytest.mark.parametrize("m,n,k", [(64, 256, 4096), (40, 128, 10240)])
+def test_w8a8_large_k_token_blocks_and_gemm(m, n, k):
+    # 64 tokens x K = 4096 do not fit in LDS: blocks of 32; K = 10240 fits no block: GEMM
+    _say(f"w8a8 large K M={m} N={n} K={k}")
+    g = torch.Generator().manual_seed(k)
+    x = torch.randn(m, k, generator=g).to(torch.bfloat16)
+    wq = torch.randint(-128, 128, (n, k), generator=g, dtype=torch.int8)
+    sw = torch.rand(n, generator=g) * 0.02 + 1e-3
+    y, _, _ = _linear(x.to(DEV), wq, sw, None)
+    ref = qo.w8a8_linear(x.float().numpy(), wq.numpy(), sw.numpy(), None, "bf16")
+    assert np.array_equal(_bits(y.float().cpu().numpy()), _bits(ref))
+
+
+def test_w8a8_strided_input_and_scale_dtypes():
+    _say("w8a8 strided x, fp16 scale, fp32 bias")
+    g = torch.Generator().manual_seed(9)
+    m, n, k = 24, 200, 384
+    big = torch.randn(m, k + 64, generator=g).to(torch.float16)
+    x = big.to(DEV)[:, 32:32 + k]
+    wq = torch.randint(-128, 128, (n, k), generator=g, dtype=torch.int8)
+    sw = (torch.rand(n, generator=g) * 0.02 + 1e-3).to(torch.float16)
+    bias = torch.randn(n, generator=g)
+    y, _, _ = _linear(x, wq, sw, bias)
+    ref = qo.w8a8_linear(big[:, 32:32 + k].float().numpy(), wq.numpy(), sw.float().numpy(),
+                         bias.numpy(), "f16")
+    assert np.array_equal(_bits(y.float().cpu().numpy()), _bits(ref))
+
+
+def test_w8a8_retile_round_trip_and_shared_layout():
+    lib = _lib.load()
+    s = _lib.stream_handle(DEV)
+    for n, k in ((50, 200), (272, 896), (16, 128)):
+        wt = torch.randint(-128, 128, (k, n), dtype=torch.int8, device=DEV)
+        tiled = torch.empty(lib.lsq_w8a8_tiled_bytes(n, k), dtype=torch.int8, device=DEV)
+        _lib.check(lib.lsq_w8a8_retile(wt.data_ptr(), tiled.data_ptr(), n, k, s), "retile")
+        back = torch.empty_like(wt)
+        _lib.check(lib.lsq_w8a8_untile(tiled.data_ptr(), back.data_ptr(), n, k, s), "untile")
+        torch.cuda.synchronize()
+        assert torch.equal(back, wt)
+        if k % 128 == 0:  # same bytes as the weight-only INT8 tiled layout of W = wt^T
+            t8 = torch.empty(lib.lsq_w8_tiled_bytes(n, k), dtype=torch.int8, device=DEV)
+            _lib.check(lib.lsq_w8_retile(wt.t().contiguous().data_ptr(), t8.data_ptr(), n, k, s), "w8")
+            torch.cuda.synchronize()
+            assert torch.equal(t8, tiled)
+
+
+# ----------------------------------------------------------------------------- module
+
+
+def test_int8_gemm_linear_module_reference_shapes():
+    # tests/test_hybrid_int8.py:256-280 of the reference: fp16, M % 32 != 0 shapes
+    _say("Int8GEMMLinear module shapes")
+    torch.manual_seed(0)
+    lin = nn.Linear(64, 128, bias=True, device=DEV, dtype=torch.float16)
+    layer = Int8GEMMLinear.from_float(lin, dtype=torch.float16).to(DEV)
+    wq = layer.weight_q_t.t().cpu().numpy()
+    sw = layer.scale_w_t.reshape(-1).cpu().numpy()
+    b = layer.bias.detach().float().cpu().numpy()
+    for shape in [(1, 1, 64), (4, 1, 64), (1, 37, 64), (2, 32, 64)]:
+        x = torch.randn(shape, device=DEV, dtype=torch.float16)
+        with torch.no_grad():
+            ref_out = lin(x)
+            out = layer(x)
+        assert out.shape == (*shape[:-1], 128) and out.dtype == torch.float16
+        cos = F.cosine_similarity(ref_out.float().flatten(), out.float().flatten(), dim=0).item()
+        assert cos > 0.99, (shape, cos)
+        exact = qo.w8a8_linear(x.reshape(-1, 64).float().cpu().numpy(), wq, sw, b, "f16")
+        assert np.array_equal(_bits(out.reshape(-1, 128).float().cpu().numpy()), _bits(exact))
+    with pytest.raises(ValueError, match="does not match layer in_features"):
+        layer(torch.randn(2, 63, device=DEV, dtype=torch.float16))
+
+
+def test_int8_gemm_linear_fallbacks(monkeypatch):
+    # kill switch (test_hybrid_int8.py:285-296) and K % 8 != 0: the weight-only INT8
+    # kernels, against the oracle's dequantized linear
+    _say("Int8GEMMLinear fallbacks")
+    torch.manual_seed(1)
+    for k, n in ((64, 128), (63, 127)):
+        lin = nn.Linear(k, n, bias=True, device=DEV)
+        layer = Int8GEMMLinear.from_float(lin, dtype=torch.bfloat16)
+        x = torch.randn(3, 5, k, device=DEV, dtype=torch.bfloat16)
+        if k % 8 == 0:
+            monkeypatch.setenv("MINIVLLM_DISABLE_INT8_GEMM", "1")
+        with torch.no_grad():
+            y = layer(x)
+        monkeypatch.delenv("MINIVLLM_DISABLE_INT8_GEMM", raising=False)
+        assert layer._warned_fallback and y.shape == (3, 5, n)
+        w = qo.dequant_int8(layer.weight_q_t.t().cpu().numpy(), layer.scale_w_t.reshape(-1, 1).cpu().numpy(), "bf16")
+        ref = qo.linear(x.reshape(-1, k).float().cpu().numpy(), w, layer.bias.detach().float().cpu().numpy(), "bf16")
+        assert qo.rel_err(y.reshape(-1, n).float().cpu().numpy(), ref) <= 1e-2
+
+
+def test_hybrid_int8_model_forward():
+    # the whole synthetic decoder in hybrid_int8 on the GPU against the float model
+    _say("hybrid_int8 model forward")
+    ref_model = seeded_model().to(DEV).half()
+    model = seeded_model()
+    apply_optional_quantization(model, quant_type="hybrid_int8")
+    model = model.to(DEV).half()
+    assert isinstance(model.model.layers[0].mlp.up_proj, Int8GEMMLinear)
+    assert isinstance(model.model.layers[0].self_attn.k_proj, CachedQuantizedLinear)
+    x = torch.randn(2, 9, 64, device=DEV, dtype=torch.float16)
+    with torch.no_grad():
+        ref = ref_model(x).float()
+        out = model(x).float()
+    cos = F.cosine_similarity(ref.flatten(), out.flatten(), dim=0).item()
+    _say(f"  cos={cos:.5f}")
+    assert cos > 0.99

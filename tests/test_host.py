@@ -18,7 +18,14 @@ import pytest
 import torch
 import torch.nn as nn
 
-from localstrm_amd import QuantizedLinear, apply_optional_quantization, load_and_quantize_model
+from localstrm_amd import (
+    CachedQuantizedLinear,
+    Int8GEMMLinear,
+    QuantizedLinear,
+    apply_optional_quantization,
+    can_use_int8_gemm,
+    load_and_quantize_model,
+)
 from localstrm_amd import _lib
 from oracle import quant_oracle as qo
 from tests.synthetic import seeded_model
@@ -114,9 +121,100 @@ def test_unsupported_architecture(mode):
     assert "Supported architectures require transformer blocks" in msg
 
 
-def test_hybrid_int8_is_rejected_loudly():
-    with pytest.raises(NotImplementedError):
-        apply_optional_quantization(seeded_model(), quant_type="hybrid_int8")
+def test_hybrid_int8_routing_and_accounting():
+    # tests/test_hybrid_int8.py:170-192 of the reference
+    model = seeded_model()
+    orig, quant = apply_optional_quantization(model, quant_type="hybrid_int8")
+    for layer in model.model.layers:
+        for p in PROJS:
+            m = getattr(layer.self_attn, p)
+            assert isinstance(m, CachedQuantizedLinear) and m.weight.dtype == torch.float32
+        for p in MLPS:
+            m = getattr(layer.mlp, p)
+            assert isinstance(m, Int8GEMMLinear)
+            assert m.weight_q_t.shape == (m.in_features, m.out_features)
+            assert m.scale_w_t.shape == (1, m.out_features)
+    assert quant < orig and 0.40 < quant / orig < 0.70
+
+
+def test_hybrid_int8_unaligned_mlp_falls_back_to_int8(caplog):
+    # tests/test_hybrid_int8.py:197-225: MLP dims not divisible by 8 -> QuantizedLinear int8
+    class OddMlp(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.gate_proj = nn.Linear(63, 127)
+            self.up_proj = nn.Linear(63, 127)
+            self.down_proj = nn.Linear(127, 63)
+
+    class OddLayer(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.self_attn = seeded_model().model.layers[0].self_attn
+            self.mlp = OddMlp()
+
+    class OddModel(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.layers = nn.ModuleList([OddLayer()])
+
+    m = OddModel()
+    with caplog.at_level("WARNING", logger="mini_vllm.quantization"):
+        apply_optional_quantization(m, quant_type="hybrid_int8")
+    assert isinstance(m.layers[0].self_attn.q_proj, CachedQuantizedLinear)
+    g = m.layers[0].mlp.gate_proj
+    assert isinstance(g, QuantizedLinear) and g.quant_type == "int8"
+    assert "not divisible by 8" in caplog.text
+
+
+def test_cached_quantized_linear_matches_reference_steps():
+    # quantization.py:212-240 and :264-276, a dense layer once built (runs on the CPU)
+    lin = _linear(128, 64, 3)
+    c = CachedQuantizedLinear.from_float(lin, dtype=torch.float32)
+    q, s = qo.quantize_int8(lin.weight.detach().numpy())
+    np.testing.assert_array_equal(c.weight.numpy(), q.astype(np.float32) * s)
+    x = torch.randn(4, 16, 64)
+    ref = lin(x)
+    out = c(x)
+    cos = torch.nn.functional.cosine_similarity(ref.flatten(), out.flatten(), dim=0).item()
+    assert cos > 0.99
+    assert c.memory_footprint_bytes() == 128 * 64 * 4 + 128 * 4
+    c16 = CachedQuantizedLinear.from_quantized(torch.from_numpy(q), torch.from_numpy(s), lin.bias.detach())
+    assert c16.weight.dtype == torch.float16
+    np.testing.assert_array_equal(c16.weight.float().numpy(), qo.round_f16(q.astype(np.float32) * s))
+
+
+def test_int8_gemm_linear_buffers_and_no_cpu_path(monkeypatch):
+    lin = _linear(48, 64, 4)
+    m = Int8GEMMLinear.from_float(lin, dtype=torch.float32)
+    assert set(m.state_dict().keys()) == {"weight_q_t", "scale_w_t", "bias"}
+    q, s = qo.quantize_int8(lin.weight.detach().numpy())
+    np.testing.assert_array_equal(m.weight_q_t.numpy(), q.T)
+    np.testing.assert_array_equal(m.scale_w_t.numpy(), s.T)
+    assert m.dequantize().dtype == torch.float32
+    with pytest.raises(RuntimeError, match="Int8GEMMLinear.forward: .* GPU only"):
+        m(torch.randn(2, 64))
+    # the kill switch takes the fallback (which, like every path here, needs a GPU)
+    monkeypatch.setenv("MINIVLLM_DISABLE_INT8_GEMM", "1")
+    ok, why = can_use_int8_gemm()
+    assert not ok and "MINIVLLM_DISABLE_INT8_GEMM" in why
+    with pytest.raises(RuntimeError, match="GPU only"):
+        m(torch.randn(1, 1, 64))
+    assert m._warned_fallback
+    monkeypatch.delenv("MINIVLLM_DISABLE_INT8_GEMM")
+    if not torch.cuda.is_available():
+        assert can_use_int8_gemm()[0] is False
+    assert can_use_int8_gemm("cpu")[0] is False or not torch.cuda.is_available()
+    mq = Int8GEMMLinear.from_quantized(torch.from_numpy(q), torch.from_numpy(s), dtype=torch.bfloat16)
+    np.testing.assert_array_equal(mq.weight_q_t.numpy(), q.T)
+    assert mq.bias is None and mq.output_dtype == torch.bfloat16
+
+
+def test_load_and_quantize_synthetic_hybrid():
+    # tests/test_hybrid_int8.py:339-352
+    model, orig, quant = load_and_quantize_model(seeded_model(), device="cpu", quantization="hybrid_int8")
+    assert isinstance(model.model.layers[0].self_attn.q_proj, CachedQuantizedLinear)
+    assert isinstance(model.model.layers[0].mlp.gate_proj, Int8GEMMLinear)
+    assert quant < orig
 
 
 @pytest.mark.parametrize("flag", [True, False])
@@ -251,6 +349,26 @@ def test_library_rejects_bad_arguments_without_gpu():
     assert lib.lsq_w4_tiled_bytes(18944, 3584) == 18944 * 3584 // 2
     assert lib.lsq_w4_tiled_bytes(17, 128) == 2 * 1024  # rows padded to 16
     assert lib.lsq_w4_tiled_bytes(16, 100) == 0
+    # W8A8 entry points
+    assert lib.lsq_w8a8_tiled_bytes(18944, 3584) == 18944 * 3584
+    assert lib.lsq_w8a8_tiled_bytes(17, 64) == 32 * 128  # rows to 16, K to 128
+    assert lib.lsq_w8a8_tiled_bytes(0, 64) == 0
+    assert lib.lsq_act_quant_i8(1 << 20, 16, 2, 1, 32, 1 << 20, 32, 1 << 20, None) == -2  # ldx < K
+    assert lib.lsq_act_quant_i8(1 << 20, 32, 5, 1, 32, 1 << 20, 32, 1 << 20, None) == -3
+    assert lib.lsq_act_quant_i8(None, 32, 2, 1, 32, 1 << 20, 32, 1 << 20, None) == -1
+    assert lib.lsq_act_quant_i8(None, 32, 2, 0, 32, None, 32, None, None) == 0  # M = 0
+    args = [1 << 20, 64, 1 << 20, 1 << 20, 0, None, 0, 1 << 20, 64, 2, 1, 64, 64, 1 << 20, 1 << 20, None]
+    assert lib.lsq_w8a8_linear(*args[:12], 0, *args[13:]) == -2  # K = 0
+    bad = list(args)
+    bad[13] = (1 << 20) + 8
+    assert lib.lsq_w8a8_linear(*bad) == -6  # x_q workspace not 16-byte aligned
+    bad = list(args)
+    bad[14] = None
+    assert lib.lsq_w8a8_linear(*bad) == -1
+    bad = list(args)
+    bad[4] = 9
+    assert lib.lsq_w8a8_linear(*bad) == -3
+    assert lib.lsq_w8a8_linear(*args[:10], 0, *args[11:]) == 0  # M = 0
     for code in (-1, -2, -3, -4, -5, -6):
         assert lib.lsq_status_string(code).startswith(b"lsq:")
     with pytest.raises(_lib.LsqError, match="group_size"):

@@ -259,3 +259,96 @@ def test_oracle_matches_exact_golden(name, dt):
     yr = qo.linear(x_t, w, z[f"{name}/bias"], dt)
     # float64 sums can straddle a rounding boundary of T only at exact-ties; none here
     assert np.array_equal(yr, z[f"{name}/y_{dt}"])
+
+
+# ----------------------------------------------------------------------------- W8A8
+
+
+def test_act_quant_known_answers():
+    # a row whose max|x| is 127 has scale 1 in every type, so x_q = round_half_even(x)
+    x = np.array([[127.0, 2.5, -2.5, 3.5, -0.5, 0.5, 1.5, -126.5]], np.float32)
+    for dt in ("bf16", "f16", "f32"):
+        q, s = qo.act_quant_i8(x, dt)
+        assert s[0, 0] == 1.0
+        assert q[0].tolist() == [127, 2, -2, 4, 0, 0, 2, -126]
+    # zero rows take the clamp bound 1e-8 converted to T; fp16 has none (0), so x_q is
+    # 0 / 0 -> 0
+    z = np.zeros((2, 5), np.float32)
+    assert qo.act_scale_i8(z, "bf16")[0, 0] == torch.tensor(1e-8, dtype=torch.bfloat16).float().item()
+    assert qo.act_scale_i8(z, "f32")[0, 0] == np.float32(1e-8)
+    assert qo.act_scale_i8(z, "f16")[0, 0] == 0.0
+    assert (qo.act_quant_i8(z, "f16")[0] == 0).all()
+    # a fp16 row too small for a nonzero scale: nonzero x -> +-inf -> clamped
+    t = np.array([[6e-8, -6e-8, 0.0]], np.float32)
+    q, s = qo.act_quant_i8(qo.round_f16(t), "f16")
+    assert s[0, 0] == 0.0 and q[0].tolist() == [127, -128, 0]
+
+
+def test_act_scale_uses_the_fp32_reciprocal():
+    # 1/127 rounded to fp32 and the product rounded to fp32, then to T (known answers
+    # worked in exact rational arithmetic)
+    from fractions import Fraction
+
+    rcp = np.float32(1.0) / np.float32(127.0)
+    assert Fraction(float(rcp)) != Fraction(1, 127)
+    rng = np.random.default_rng(11)
+    mx = rng.uniform(1e-3, 1e3, size=2000).astype(np.float32)
+    got = qo.act_scale_i8(mx.reshape(-1, 1), "f32")[:, 0]
+    for m, g in zip(mx[:200], got[:200]):
+        exact = Fraction(float(m)) * Fraction(float(rcp))
+        assert Fraction(float(g)) == Fraction(float(np.float32(float(exact))))  # nearest fp32
+    # the two evaluation orders differ on a visible share of fp32 inputs
+    div = (mx / np.float32(127.0)).astype(np.float32)
+    assert np.count_nonzero(div != got) > 20
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16", "f32"])
+def test_act_quant_matches_torch_ops_given_the_scale(dt):
+    # :413-414 with torch's own CPU ops: max|x| and the quantization step from the scale
+    rng = np.random.default_rng(3)
+    x = torch.from_numpy(rng.standard_normal((37, 300)).astype(np.float32) * 3).to(TORCH_DT[dt])
+    x32 = x.float().numpy()
+    xq, s = qo.act_quant_i8(x32, dt)
+    mx = torch.max(torch.abs(x), dim=-1, keepdim=True)[0].float().numpy()
+    np.testing.assert_array_equal(np.max(np.abs(x32), axis=-1, keepdims=True), mx)
+    ref = torch.clamp(torch.round(x.float() / torch.from_numpy(s)), -128, 127).to(torch.int8)
+    np.testing.assert_array_equal(xq, ref.numpy())
+    # torch's CPU division by the scalar is a true division; on this sample it gives the
+    # same scales as the GPU's reciprocal product (the order is pinned on the GPU)
+    if dt != "f32":
+        st = torch.clamp(torch.max(torch.abs(x), dim=-1, keepdim=True)[0] / 127.0, min=1e-8).float()
+        np.testing.assert_array_equal(s, st.numpy())
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16", "f32"])
+@pytest.mark.parametrize("with_bias", [False, True])
+def test_w8a8_linear_matches_int_mm_and_torch_epilogue(dt, with_bias):
+    # steps 6-11 of Int8GEMMLinear.forward (quantization.py:416-447) with torch's CPU
+    # torch._int_mm and elementwise ops, from the oracle's x_q / scale_x
+    rng = np.random.default_rng(5)
+    m, k, n = 37, 96, 40
+    x = qo.round_to(rng.standard_normal((m, k)).astype(np.float32) * 2, dt)
+    w = rng.integers(-128, 128, size=(n, k)).astype(np.int8)
+    sw = rng.uniform(1e-3, 2e-2, size=n).astype(np.float32)
+    bias = qo.round_to(rng.standard_normal(n).astype(np.float32), dt) if with_bias else None
+    y = qo.w8a8_linear(x, w, sw, bias, dt)
+    xq, sx = qo.act_quant_i8(x, dt)
+    xp = torch.nn.functional.pad(torch.from_numpy(xq), (0, 0, 0, 32 - m % 32))
+    acc = torch._int_mm(xp, torch.from_numpy(np.ascontiguousarray(w.T)))[:m]
+    out = acc.float() * (torch.from_numpy(sx) * torch.from_numpy(sw).reshape(1, -1))
+    if with_bias:
+        out = out + torch.from_numpy(bias).to(TORCH_DT[dt]).float()
+    ref = out.to(TORCH_DT[dt]).float().numpy()
+    np.testing.assert_array_equal(y, ref)
+
+
+def test_w8a8_linear_closed_form():
+    # w = 3 I, scale_w = 0.5, rows with max|x| = 127 (scale 1): y = round_T(3 x_q * 0.5 + b)
+    k = 16
+    x = np.tile(np.arange(-7, 9, dtype=np.float32) * 15.875, (3, 1))
+    x[:, 0] = 127.0
+    w = (3 * np.eye(k)).astype(np.int8)
+    b = np.linspace(-1, 1, k).astype(np.float32)
+    y = qo.w8a8_linear(x, w, np.full(k, 0.5, np.float32), qo.round_bf16(b), "bf16")
+    xq = np.rint(x).clip(-128, 127)
+    np.testing.assert_array_equal(y, qo.round_bf16(xq * 1.5 + qo.round_bf16(b)))
