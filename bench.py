@@ -40,6 +40,7 @@ import torch
 METRIC = "W-only INT4/INT8 GEMM: decode GB/s (% HBM peak); prefill TFLOP/s (% MFMA)"
 HBM_PEAK_GBS = 8000.0       # MI355X HBM3E, vendor spec
 MFMA_BF16_PEAK_TF = 2500.0  # MI355X dense bf16, vendor spec
+MFMA_INT8_PEAK_TOPS = 5000.0  # MI355X dense int8, vendor spec
 MALL_BYTES = 256 << 20
 
 
@@ -80,8 +81,10 @@ def make_int4(n: int, k: int, m: int, group: int = 128, x_dtype=torch.bfloat16, 
 
 
 def decode_bytes(kind: str, n: int, k: int, m: int, group: int = 128) -> int:
-    """Algorithmic bytes per call: W + scales + x + y (bf16 activations)."""
-    if kind == "int8":
+    """Algorithmic bytes per call: W + scales + x + y (bf16 activations). W8A8 counts the
+    layer's own inputs and outputs the same way as INT8 (its int8 activation copy is an
+    intermediate)."""
+    if kind in ("int8", "w8a8"):
         return n * k + n * 4 + m * k * 2 + m * n * 2
     return n * k // 2 + n * (-(-k // group)) * 2 + m * k * 2 + m * n * 2
 
@@ -90,14 +93,16 @@ def decode_bytes(kind: str, n: int, k: int, m: int, group: int = 128) -> int:
 
 
 def _layers(kind, w, s, group, copies, device):
-    from localstrm_amd import QuantizedLinear
+    from localstrm_amd import Int8GEMMLinear, QuantizedLinear
 
     out = []
     for i in range(copies):
         wc = w.to(device)
         if i:
             wc = wc.clone()
-        if kind == "int8":
+        if kind == "w8a8":
+            out.append(Int8GEMMLinear.from_quantized(wc, s.to(device), dtype=torch.bfloat16))
+        elif kind == "int8":
             out.append(QuantizedLinear.from_quantized(wc, s.to(device), quant_type="int8"))
         else:
             out.append(QuantizedLinear.from_quantized(wc, s.to(device), quant_type="int4",
@@ -166,7 +171,7 @@ def copies_for(nbytes: int) -> int:
 
 
 def bench_decode(kind: str, n: int, k: int, m: int, steps: int, warmup: int, device, group=128):
-    if kind == "int8":
+    if kind in ("int8", "w8a8"):
         w, s, x = make_int8(n, k, m)
     else:
         w, s, x = make_int4(n, k, m, group)
@@ -178,12 +183,13 @@ def bench_decode(kind: str, n: int, k: int, m: int, steps: int, warmup: int, dev
     flops = 2.0 * m * n * k
     del layers
     torch.cuda.empty_cache()
+    peak = MFMA_INT8_PEAK_TOPS if kind == "w8a8" else MFMA_BF16_PEAK_TF
     return {
-        "kind": kind, "M": m, "N": n, "K": k, "group": None if kind == "int8" else group,
+        "kind": kind, "M": m, "N": n, "K": k, "group": None if kind in ("int8", "w8a8") else group,
         "us_per_call": ms * 1e3, "GB_s": nbytes / (ms * 1e-3) / 1e9,
         "TFLOP_s": flops / (ms * 1e-3) / 1e12, "bytes": nbytes, "weight_copies": copies,
         "frac_hbm": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
-        "frac_mfma": flops / (ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TF,
+        "frac_mfma": flops / (ms * 1e-3) / 1e12 / peak,
     }
 
 
@@ -316,7 +322,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true")
     ap.add_argument("--case", default=None,
-                    help="kind,N,K,M (e.g. int4,14336,4096,2048), or 'stack' for the batch-32 "
+                    help="kind,N,K,M (kind int8 | int4 | w8a8; e.g. int4,14336,4096,2048), or "
+                         "'stack' for the batch-32 "
                          "decode step through the Qwen2.5-0.5B-architecture stack: time only "
                          "that case and print its line (used for the rocprofv3 summaries in "
                          "profiles/)")
@@ -357,6 +364,10 @@ def main() -> int:
             sweep.append(bench_decode("int4", 14336, 4096, m, max(10, args.steps // 20),
                                       max(2, args.warmup // 4), device))
         sweep.append(bench_decode("int8", 4864, 896, 1, args.steps, args.warmup, device))
+        for m in (1, 64):
+            sweep.append(bench_decode("w8a8", N, K, m, args.steps, args.warmup, device))
+        sweep.append(bench_decode("w8a8", 14336, 4096, 2048, max(10, args.steps // 20),
+                                  max(2, args.warmup // 4), device))
         sweep.append(bench_stack(max(5, args.steps // 20), 2, device))
         sweep.append(bench_stack(max(5, args.steps // 20), 2, device, fused=True))
     cpu = None if args.no_cpu else cpu_baseline(N, K, M)

@@ -150,8 +150,10 @@ int lsq_act_quant_i8(const void* x, int64_t ldx, int dtype, int64_t M, int64_t K
  * stride ldx). Replaces Int8GEMMLinear.forward's native path, quantization.py:404-447
  * (activation quantization, torch._int_mm, rescale, bias, cast). `tiled` is the output of
  * lsq_w8a8_retile; bias is NULL or [N] of bias_dtype. x_q [M, round_up(K, 128)] int8
- * (16-byte aligned) and scale_x [M] fp32 are the caller's workspace; on return they hold
- * the quantized activations and their scales. 1 <= K < 131072. */
+ * (16-byte aligned) and scale_x [M] fp32 are the caller's workspace for the quantized
+ * activations and their scales; decode-sized calls quantize inside the GEMV kernel and
+ * leave them untouched, so their contents afterwards are unspecified (lsq_act_quant_i8
+ * computes them on their own). 1 <= K < 131072. */
 int lsq_w8a8_linear(const void* x, int64_t ldx, const int8_t* tiled, const void* scale_w,
                     int scale_w_dtype, const void* bias, int bias_dtype, void* y, int64_t ldy,
                     int dtype, int64_t M, int64_t N, int64_t K, int8_t* x_q, float* scale_x,

@@ -95,6 +95,39 @@ __device__ __forceinline__ float dequant_elem(int q, float s_T) {
   return Act<DT>::round(mul_rn(static_cast<float>(q), s_T));
 }
 
+// ---------------------------------------------------------------- W8A8 activations
+// Per-token scale from the row's max|x| (as fp32): clamp(round_T(max * fp32(1/127)),
+// min = round_T(1e-8)), the GPU evaluation of quantization.py:412-413 (torch multiplies
+// by the fp32 reciprocal when dividing a tensor by a Python scalar). NaN stays NaN.
+template <int DT>
+__device__ __forceinline__ float a8_scale(float mx) {
+  constexpr float kInv127 = 1.0f / 127.0f;
+  const float s = Act<DT>::round(mul_nc(mx, kInv127));
+  const float smin = Act<DT>::round(1e-8f);
+  return s < smin ? smin : s;
+}
+
+// clamp(rint(v / s), -128, 127) with IEEE division (quantization.py:414); NaN (0 / 0 when
+// a fp16 scale is 0) becomes 0.
+__device__ __forceinline__ int quant_i8(float v, float s) {
+  float q = __builtin_rintf(__fdiv_rn(v, s));
+  if (q != q) return 0;
+  q = q < -128.f ? -128.f : (q > 127.f ? 127.f : q);
+  return static_cast<int>(q);
+}
+
+// quant_i8(v, s) with a product instead of the division: t = v * rcp(s) is within 2^-14
+// of v / s (|v / s| < 192 by construction of s, fp16 subnormal scales included; v_rcp_f32
+// is accurate to 1 ulp), so when t is more than 2^-10 from every half-integer, rint of
+// the IEEE quotient v / s equals rint(t). Otherwise (a near-tie, s = 0, or a non-finite
+// value, where t - rint(t) is NaN) the exact division decides. `r` is rcp(s), once per row.
+__device__ __forceinline__ int quant_i8_fast(float v, float s, float r) {
+  const float t = mul_nc(v, r);
+  const float q = __builtin_rintf(t);
+  if (!(__builtin_fabsf(t - q) < 0.5f - 0x1p-10f)) return quant_i8(v, s);
+  return static_cast<int>(q < -128.f ? -128.f : (q > 127.f ? 127.f : q));
+}
+
 // ---------------------------------------------------------------- wavefront helpers
 
 __device__ __forceinline__ float wave_sum(float v) {

@@ -37,12 +37,15 @@ struct LinearArgs {
 template <int DT>
 int launch_decode(int kind, const LinearArgs& a, hipStream_t s);
 
-// W8A8 decode: x is the per-token quantized int8 activation [M, K] (row stride ldx
-// bytes), xscale its scales, w the tiled INT8 layout, scale the per-row weight scale.
-// y = float(sum_k xq * wq) * (xscale[m] * scale[n]) (+ bias), each step one fp32
-// rounding, then one rounding to the output type DT. Same fit rules as launch_decode.
+// W8A8 decode: w the tiled INT8 layout, scale the per-row weight scale;
+// y = float(sum_k xq * wq) * (scale_x[m] * scale[n]) (+ bias), each step one fp32
+// rounding, then one rounding to the output type DT. fused = false: x is the per-token
+// quantized int8 activation [M, K] (row stride ldx bytes) with its scales in xscale.
+// fused = true: x is the DT-typed activation (row stride ldx elements, 16-byte aligned)
+// and every workgroup quantizes it while staging (only when all of x fits the prologue's
+// first load batch). Same fit rules as launch_decode otherwise.
 template <int DT>
-int launch_decode_a8(const LinearArgs& a, hipStream_t s);
+int launch_decode_a8(const LinearArgs& a, bool fused, hipStream_t s);
 
 // Batched decode, 16 < M <= 64 tokens (activations streamed through LDS in chunks).
 // Same contract as launch_decode.

@@ -106,6 +106,26 @@ __device__ __forceinline__ void put_floats(const uint32_t (&v)[kSB], int t0, int
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 
+// W8A8 modes of the decode kernel: activations pre-quantized to int8 (x_q, scale_x from
+// lsq_act_quant_i8), or quantized inside the kernel from the T-typed x.
+constexpr int kA8Pre = 1, kA8Fused = 2;
+
+// 16-byte activation chunks each thread loads in the prologue's first batch: 8192 chunks
+// per 512-thread workgroup covers 16 tokens at K = 4096, 32 at 2048, 64 at 1024.
+__host__ __device__ constexpr int prologue_chunks(int nt) {
+  return nt >= 8192 ? 1 : (nt >= 512 ? 8192 / nt : 16);
+}
+
+// Max of a non-negative float (as its bits) over each row of 16 lanes, in every lane of the
+// row (DPP; the bit order of non-negative floats is their value order, NaN above all).
+__device__ __forceinline__ uint32_t row16_umax(uint32_t v) {
+  v = max(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0xB1, 0xF, 0xF, false)));
+  v = max(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x4E, 0xF, 0xF, false)));
+  v = max(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x141, 0xF, 0xF, false)));
+  v = max(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x140, 0xF, 0xF, false)));
+  return v;
+}
+
 // v_mfma_i32_16x16x64_i8 on registers kept as f32x4 bit patterns (the accumulator
 // arrays are shared with the floating-point paths).
 __device__ __forceinline__ f32x4 mma_i8(u32x4 a, u32x4 b, f32x4 c) {
@@ -115,13 +135,14 @@ __device__ __forceinline__ f32x4 mma_i8(u32x4 a, u32x4 b, f32x4 c) {
                                                    __builtin_bit_cast(i32x4, c), 0, 0, 0));
 }
 
-template <int DT, int KIND, int RT, int RG, int KS, int D, bool GROUPED, int MB, bool A8>
+template <int DT, int KIND, int RT, int RG, int KS, int D, bool GROUPED, int MB, int A8>
 __global__ void __launch_bounds__(64 * RG * KS) decode_kernel(LinearArgs p) {
   static_assert(!A8 || (KIND == kW8Tiled && !GROUPED), "W8A8 streams the tiled INT8 layout");
   constexpr int MP = 16 * MB;  // token rows covered: MB blocks of 16
   constexpr int NT = 64 * RG * KS;
-  constexpr int XE = A8 ? 16 : 8;  // activations per 16-byte chunk
-  constexpr int XB = A8 ? 1 : 2;   // bytes per activation
+  // bytes per activation as loaded, and activations per 16-byte chunk
+  constexpr int XB = A8 == kA8Pre ? 1 : static_cast<int>(sizeof(typename Act<DT>::storage));
+  constexpr int XE = 16 / XB;
   constexpr bool W4 = KIND == kW4Tiled || KIND == kW4Canon;
   constexpr bool TILED = KIND == kW4Tiled || KIND == kW8Tiled;
   constexpr int LPT = W4 ? 1 : 2;  // 16-byte weight loads per lane per (row tile, k tile)
@@ -140,9 +161,9 @@ __global__ void __launch_bounds__(64 * RG * KS) decode_kernel(LinearArgs p) {
   const int ng = static_cast<int>(p.ngroups);
   const int ngs = GROUPED ? ng : 1;  // scale columns per row
   const int gtiles = static_cast<int>(p.group / kTileK);
-  const int ldxb = static_cast<int>(x_row_bytes(K, A8));  // LDS bytes per staged row
+  const int ldxb = static_cast<int>(x_row_bytes(K, A8 != 0));  // LDS bytes per staged row
 
-  const DecodeLds L = decode_lds(M, K, ROWS, ngs, RED, MP, A8);
+  const DecodeLds L = decode_lds(M, K, ROWS, ngs, RED, MP, A8 != 0);
   unsigned char* xs = smem + L.xs;
   float* xsum = reinterpret_cast<float*>(smem + L.xsum);
   float* xtot = reinterpret_cast<float*>(smem + L.xtot);
@@ -154,6 +175,8 @@ __global__ void __launch_bounds__(64 * RG * KS) decode_kernel(LinearArgs p) {
   const int lane = tid & 63;
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform per wave
   const int rg = wid % RG;
+  uint32_t* xmax = reinterpret_cast<uint32_t*>(xtot);  // fused W8A8: per-token max|x| bits
+  if (A8 == kA8Fused && tid < MP) xmax[tid] = 0u;
   const int ks = wid / RG;
   const int r = lane & 15;
   const int q = lane >> 4;
@@ -203,7 +226,7 @@ __global__ void __launch_bounds__(64 * RG * KS) decode_kernel(LinearArgs p) {
   // First batch: XS chunks per thread, all issued at once (one memory round trip):
   // 8192 chunks per 512-thread workgroup covers 16 tokens at K = 4096, 32 at 2048, 64 at
   // 1024. Larger inputs take a second, batched pass after the weight stream is issued.
-  constexpr int XS = NT >= 8192 ? 1 : (NT >= 512 ? 8192 / NT : 16);
+  constexpr int XS = prologue_chunks(NT);
   u32x4 xv[XS];
 #pragma unroll
   for (int u = 0; u < XS; ++u)
@@ -215,8 +238,8 @@ __global__ void __launch_bounds__(64 * RG * KS) decode_kernel(LinearArgs p) {
     if (u * NT < nsd) sv[u] = bload4(rs, t < nsd ? t * 4 : kOOB);  // uniform skip
   }
   const uint32_t bv = bload4(rb, tid < nbd ? tid * 4 : kOOB);  // ROWS * 4 bytes <= 4 * NT
-  float sxv = 0.f;  // W8A8: this thread's token scale
-  if (A8 && tid < M) sxv = p.xscale[tid];
+  float sxv = 0.f;  // pre-quantized W8A8: this thread's token scale
+  if (A8 == kA8Pre && tid < M) sxv = p.xscale[tid];
   // ---- activations -> LDS (in the unpack's column order) and per-(k tile, token) sums
   // Sum of a float over each row of 16 lanes, in every lane of the row (DPP, no LDS).
   auto row16_sum = [](float v) {
@@ -251,9 +274,59 @@ __global__ void __launch_bounds__(64 * RG * KS) decode_kernel(LinearArgs p) {
   // Staging of what the prologue loaded, done after the first weight steps are issued:
   // these loads were issued before the weights, so waiting for them leaves the weight
   // loads in flight.
+  // Fused W8A8: per-token max|x| (16-lane DPP max, then one LDS atomic max per row of 16
+  // lanes, which always lie in one token row since K8 and NT are multiples of 16), then
+  // each thread quantizes the chunks it holds and stores them as int8 rows.
+  auto put_xq = [&]() {
+    lds_barrier();  // xmax[] zeroed at entry
+#pragma unroll
+    for (int u = 0; u < XS; ++u) {
+      if (u * NT >= nchunks) break;  // uniform
+      const int c = u * NT + tid;
+      uint32_t mx = 0u;
+      if (c < nchunks) {
+#pragma unroll
+        for (int e = 0; e < XE; ++e) {
+          const float f = XB == 4 ? __uint_as_float(xv[u][e])
+                                  : Act<DT>::to_f32(static_cast<uint16_t>(xv[u][e >> 1] >> (16 * (e & 1))));
+          mx = max(mx, __float_as_uint(fabsf(f)));
+        }
+      }
+      mx = row16_umax(mx);
+      if (c < nchunks && (lane & 15) == 0) atomicMax(&xmax[c / K8], mx);
+    }
+    lds_barrier();
+#pragma unroll
+    for (int u = 0; u < XS; ++u) {
+      if (u * NT >= nchunks) break;  // uniform
+      const int c = u * NT + tid;
+      if (c < nchunks) {
+        const int m = c / K8;
+        const int c8 = c - m * K8;
+        const float sc = a8_scale<DT>(__uint_as_float(xmax[m]));
+        const float rc = __builtin_amdgcn_rcpf(sc);
+        uint32_t o[XE / 4];
+#pragma unroll
+        for (int d = 0; d < XE / 4; ++d) {
+          uint32_t b = 0;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int ee = 4 * d + e;
+            const float f = XB == 4 ? __uint_as_float(xv[u][ee])
+                                    : Act<DT>::to_f32(static_cast<uint16_t>(xv[u][ee >> 1] >> (16 * (ee & 1))));
+            b |= (static_cast<uint32_t>(quant_i8_fast(f, sc, rc)) & 0xFFu) << (8 * e);
+          }
+          o[d] = b;
+        }
+        if constexpr (XE == 8) *reinterpret_cast<uint2*>(xs + m * ldxb + c8 * 8) = make_uint2(o[0], o[1]);
+        else *reinterpret_cast<uint32_t*>(xs + m * ldxb + c8 * 4) = o[0];
+      }
+    }
+  };
   auto stage_first = [&]() {
-    put_x(xv, 0, std::integral_constant<int, XS>());
-    put_floats<DT, NT, A8>(sv, 0, tid, p.scale_dt, nsc, ss);
+    if constexpr (A8 == kA8Fused) put_xq();
+    else put_x(xv, 0, std::integral_constant<int, XS>());
+    put_floats<DT, NT, (A8 != 0)>(sv, 0, tid, p.scale_dt, nsc, ss);
     // W8A8 adds the bias as stored (widened to fp32); weight-only rounds it to T first
     auto cvt = [](float f) { return A8 ? f : Act<DT>::round(f); };
     if (p.bias && tid < nbd) {
@@ -264,7 +337,7 @@ __global__ void __launch_bounds__(64 * RG * KS) decode_kernel(LinearArgs p) {
         if (2 * tid + 1 < rows_valid) sb[2 * tid + 1] = cvt(dword_elem(bv, 1, p.bias_dt));
       }
     }
-    if (A8 && tid < MP) xtot[tid] = sxv;
+    if (A8 == kA8Pre && tid < MP) xtot[tid] = sxv;
   };
   // Keep the scheduler from moving any of the loads above below the weight stream:
   // their consumers then wait only for them, not for the weights.
@@ -294,9 +367,10 @@ __global__ void __launch_bounds__(64 * RG * KS) decode_kernel(LinearArgs p) {
   // Activations or scales beyond the first batch (many tokens, or many scale groups) are
   // loaded and staged now, while the first D weight steps are in flight (the loop's waits
   // also cover the weights, which are needed next anyway).
+  // (the fused W8A8 launch is only made when all activations fit in the first batch)
   const bool big = nchunks > NT * XS || nsd > NT * kSB;  // uniform
   if (big) {
-    for (int c0 = NT * XS; c0 < nchunks; c0 += NT * kXB) {
+    for (int c0 = NT * XS; A8 != kA8Fused && c0 < nchunks; c0 += NT * kXB) {
       u32x4 xb[kXB];
 #pragma unroll
       for (int u = 0; u < kXB; ++u) xb[u] = bload16<0>(rx, x_off(c0 + u * NT + tid));
@@ -308,10 +382,11 @@ __global__ void __launch_bounds__(64 * RG * KS) decode_kernel(LinearArgs p) {
         const int t = t0 + u * NT + tid;
         sv[u] = bload4(rs, t < nsd ? t * 4 : kOOB);
       }
-      put_floats<DT, NT, A8>(sv, t0, tid, p.scale_dt, nsc, ss);
+      put_floats<DT, NT, (A8 != 0)>(sv, t0, tid, p.scale_dt, nsc, ss);
     }
   }
-  for (int c = tid; c < K8; c += NT)  // row M: zeros, read by lanes of token rows >= M
+  // row M: zeros, read by lanes of token rows >= M (K bytes for int8 rows, 2 K for 16-bit)
+  for (int c = tid; c < (A8 ? K / 16 : K / 8); c += NT)
     *reinterpret_cast<u32x4*>(xs + M * ldxb + c * 16) = u32x4{0u, 0u, 0u, 0u};
   lds_barrier();
   if (W4 && !GROUPED) {
@@ -476,7 +551,8 @@ __global__ void __launch_bounds__(64 * RG * KS) decode_kernel(LinearArgs p) {
         if (m < M && n < N) {
           if constexpr (A8) {
             // float(acc) * (sx * sw) [+ bias], each an fp32 rounding, then round to T
-            float v = mul_nc(static_cast<float>(__float_as_int(acc[i][mb][e])), mul_nc(xtot[m], sc));
+            const float sxm = A8 == kA8Fused ? a8_scale<DT>(xtot[m]) : xtot[m];
+            float v = mul_nc(static_cast<float>(__float_as_int(acc[i][mb][e])), mul_nc(sxm, sc));
             if (p.bias) v = add_nc(v, bias);
             y[static_cast<int64_t>(m) * p.ldy + n] = Act<DT>::from_f32(v);
           } else {
@@ -555,11 +631,15 @@ Cfg pick_cfg(int kind, int64_t M, int64_t N, int64_t K) {
   return Cfg{1, 1, 8, 4};
 }
 
-template <int DT, int KIND, int RT, int RG, int KS, int D, bool GROUPED, int MB, bool A8>
+template <int DT, int KIND, int RT, int RG, int KS, int D, bool GROUPED, int MB, int A8>
 int launch_one(const LinearArgs& a, hipStream_t s) {
   constexpr int RED = KS > 1 ? (KS - 1) * RG * RT * MB * 4 * 64 : 0;
+  if (A8 == kA8Fused) {  // every activation chunk must be in the prologue's first batch
+    constexpr int XE = 16 / static_cast<int>(sizeof(typename Act<DT>::storage));
+    if (a.M * (a.K / XE) > int64_t(64 * RG * KS) * prologue_chunks(64 * RG * KS)) return LSQ_E_LAYOUT;
+  }
   const bool grouped = a.group < a.K;
-  const DecodeLds L = decode_lds(a.M, a.K, RG * RT * kTileN, grouped ? a.ngroups : 1, RED, 16 * MB, A8);
+  const DecodeLds L = decode_lds(a.M, a.K, RG * RT * kTileN, grouped ? a.ngroups : 1, RED, 16 * MB, A8 != 0);
   if (L.total > max_lds_bytes()) return LSQ_E_LAYOUT;
   auto kern = decode_kernel<DT, KIND, RT, RG, KS, D, GROUPED, MB, A8>;
   if (L.total > 64 * 1024) {
@@ -578,7 +658,7 @@ int launch_one(const LinearArgs& a, hipStream_t s) {
   return static_cast<int>(hipGetLastError());
 }
 
-template <int DT, int KIND, bool GROUPED, bool A8 = false>
+template <int DT, int KIND, bool GROUPED, int A8 = 0>
 int launch_kind(const LinearArgs& a, hipStream_t s) {
   const Cfg c = pick_cfg(KIND, a.M, a.N, a.K);
   if (a.M > 16) {
@@ -630,17 +710,21 @@ template int launch_decode<LSQ_BF16>(int, const LinearArgs&, hipStream_t);
 template int launch_decode<LSQ_F16>(int, const LinearArgs&, hipStream_t);
 
 template <int DT>
-int launch_decode_a8(const LinearArgs& a, hipStream_t s) {
-  if (a.M < 1 || a.M > 64 || a.K % kTileK != 0 || a.K < kTileK || !a.xscale) return LSQ_E_LAYOUT;
+int launch_decode_a8(const LinearArgs& a, bool fused, hipStream_t s) {
+  if (a.M < 1 || a.M > 64 || a.K % kTileK != 0 || a.K < kTileK) return LSQ_E_LAYOUT;
+  if (!fused && !a.xscale) return LSQ_E_LAYOUT;
   auto aligned4 = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 3) == 0; };
   if (!aligned4(a.scale) || (a.bias && !aligned4(a.bias))) return LSQ_E_LAYOUT;
-  if ((a.M - 1) * a.ldx + a.K >= (int64_t(1) << 31)) return LSQ_E_LAYOUT;
+  const int64_t xb = fused ? static_cast<int64_t>(sizeof(typename Act<DT>::storage)) : 1;
+  if (fused && ((reinterpret_cast<uintptr_t>(a.x) & 15) || (a.ldx * xb) % 16)) return LSQ_E_LAYOUT;
+  if (((a.M - 1) * a.ldx + a.K) * xb >= (int64_t(1) << 31)) return LSQ_E_LAYOUT;
   if (int64_t(128) * a.K >= (int64_t(1) << 31)) return LSQ_E_LAYOUT;
-  return launch_kind<DT, kW8Tiled, false, true>(a, s);
+  return fused ? launch_kind<DT, kW8Tiled, false, kA8Fused>(a, s)
+               : launch_kind<DT, kW8Tiled, false, kA8Pre>(a, s);
 }
 
-template int launch_decode_a8<LSQ_F32>(const LinearArgs&, hipStream_t);
-template int launch_decode_a8<LSQ_F16>(const LinearArgs&, hipStream_t);
-template int launch_decode_a8<LSQ_BF16>(const LinearArgs&, hipStream_t);
+template int launch_decode_a8<LSQ_F32>(const LinearArgs&, bool, hipStream_t);
+template int launch_decode_a8<LSQ_F16>(const LinearArgs&, bool, hipStream_t);
+template int launch_decode_a8<LSQ_BF16>(const LinearArgs&, bool, hipStream_t);
 
 }  // namespace lsq

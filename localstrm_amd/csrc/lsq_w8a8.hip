@@ -5,10 +5,12 @@
 // chain of elementwise kernels (:411-414), pads M to a multiple of 32 (:416-422), calls
 // torch._int_mm (:425) and rescales in fp32 (:431-440). Here:
 //
-//  * act_quant_kernel: one workgroup per token row: max|x| (exact in the input type),
-//    the scale, and the int8 row, in one pass over x held in registers;
-//  * the decode kernel's W8A8 mode (lsq_decode.hip) for M <= 64: int8 weights streamed
+//  * the decode kernel's W8A8 modes (lsq_decode.hip) for M <= 64: int8 weights streamed
 //    once from the tiled layout straight into v_mfma_i32_16x16x64_i8, no conversion;
+//    for small x (M * K <= 16384) every workgroup quantizes x itself while staging it,
+//    so the layer is one launch;
+//  * act_quant_kernel otherwise: one workgroup per token row: max|x| (exact in the input
+//    type), the scale, and the int8 row, from x held in registers;
 //  * w8a8_gemm_kernel for larger M: both operands DMA'd from HBM into LDS and fed to
 //    v_mfma_i32_32x32x32_i8; the fp32 rescale and bias are the epilogue.
 //
@@ -47,14 +49,6 @@ constexpr int kAqR = 4;     // 16-byte chunks per thread kept in registers betwe
 
 // NaN-propagating max (torch.max returns NaN for a row holding one).
 __device__ __forceinline__ float nan_max(float a, float b) { return (b > a || b != b) ? b : a; }
-
-// rint(v / s) clamped to [-128, 127]; NaN (0 / 0 when the fp16 scale is 0) becomes 0.
-__device__ __forceinline__ int quant1(float v, float s) {
-  float q = __builtin_rintf(__fdiv_rn(v, s));
-  if (q != q) return 0;
-  q = q < -128.f ? -128.f : (q > 127.f ? 127.f : q);
-  return static_cast<int>(q);
-}
 
 template <int DT>
 __global__ void __launch_bounds__(kAqNT) act_quant_kernel(const void* __restrict__ x, int64_t ldx,
@@ -99,11 +93,8 @@ __global__ void __launch_bounds__(kAqNT) act_quant_kernel(const void* __restrict
 #pragma unroll
   for (int w = 0; w < kAqNT / 64; ++w) mx = nan_max(mx, wmax[w]);
 
-  // scale: clamp(round_T(max * fp32(1/127)), round_T(1e-8)); the clamp keeps NaN
-  constexpr float kInv127 = 1.0f / 127.0f;
-  float s = Act<DT>::round(mul_nc(mx, kInv127));
-  const float smin = Act<DT>::round(1e-8f);
-  s = s < smin ? smin : s;
+  const float s = a8_scale<DT>(mx);
+  const float rs = __builtin_amdgcn_rcpf(s);
   if (tid == 0) sx[m] = s;
 
   // pass 2: quantize, E int8 per chunk
@@ -113,7 +104,7 @@ __global__ void __launch_bounds__(kAqNT) act_quant_kernel(const void* __restrict
     for (int d = 0; d < E / 4; ++d) {
       uint32_t b = 0;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) b |= (static_cast<uint32_t>(quant1(elem(w, 4 * d + e), s)) & 0xFFu) << (8 * e);
+      for (int e = 0; e < 4; ++e) b |= (static_cast<uint32_t>(quant_i8_fast(elem(w, 4 * d + e), s, rs)) & 0xFFu) << (8 * e);
       o[d] = b;
     }
     if constexpr (E == 8) *reinterpret_cast<uint2*>(qr + c * E) = make_uint2(o[0], o[1]);
@@ -125,7 +116,7 @@ __global__ void __launch_bounds__(kAqNT) act_quant_kernel(const void* __restrict
     if (c < nch) put(c, v[r]);
   }
   for (int c = tid + kAqR * kAqNT; c < nch; c += kAqNT) put(c, *reinterpret_cast<const u32x4*>(xr + c * E));
-  for (int k = nch * E + tid; k < K; k += kAqNT) qr[k] = static_cast<int8_t>(quant1(Act<DT>::to_f32(xr[k]), s));
+  for (int k = nch * E + tid; k < K; k += kAqNT) qr[k] = static_cast<int8_t>(quant_i8_fast(Act<DT>::to_f32(xr[k]), s, rs));
   for (int k = K + tid; k < Kz; k += kAqNT) qr[k] = 0;  // padding columns
 }
 
@@ -373,26 +364,45 @@ int launch_w8a8_gemm(const LinearArgs& a, hipStream_t s) {
   return static_cast<int>(hipGetLastError());
 }
 
-// LSQ_W8A8_PATH=gemm sends every M to the GEMM kernel (for comparisons and tests).
-bool force_gemm() {
+// LSQ_W8A8_PATH selects a path for comparisons and tests: "gemm" sends every M to the
+// GEMM kernel, "unfused" quantizes activations in their own kernel for decode shapes too,
+// "fused" quantizes inside the decode kernel whenever x fits its first load batch.
+bool path_is(const char* want) {
   const char* e = std::getenv("LSQ_W8A8_PATH");
-  return e && std::strcmp(e, "gemm") == 0;
+  return e && std::strcmp(e, want) == 0;
 }
 
-// Decode kernel for M <= 64 while the int8 activations fit in LDS; otherwise the same in
-// blocks of 32 or 16 tokens (the weights are streamed once per block), and the GEMM when
-// not even 16 tokens fit or M > 64.
+// Every workgroup of the fused decode quantizes all of x again, which costs more than
+// the separate quantization launch once a workgroup's share passes ~16K activations
+// (measured: 18944 x 3584 gains 3.5 us at M = 1, loses 2.4 us at M = 8).
+constexpr int64_t kFusedMaxElems = 16384;
+
+// M <= 64: the decode kernel quantizing x itself when x is small (above) and fits its
+// first load batch; otherwise x is quantized by act_quant_kernel and the decode kernel
+// streams x_q while it fits in LDS, else runs in blocks of 32 or 16 tokens (the weights
+// are streamed once per block). M > 64, or no block fits: the GEMM on x_q.
 template <int DT>
-int run_w8a8(const LinearArgs& a, hipStream_t s) {
-  if (a.M <= 64 && !force_gemm()) {
-    int rc = launch_decode_a8<DT>(a, s);
+int run_w8a8(const LinearArgs& ax, const LinearArgs& a, hipStream_t s) {
+  const bool gemm = path_is("gemm");
+  const bool fused = path_is("fused") || (ax.M * ax.K <= kFusedMaxElems && !path_is("unfused"));
+  if (a.M <= 64 && !gemm && fused) {
+    const int rc = launch_decode_a8<DT>(ax, true, s);
+    if (rc != LSQ_E_LAYOUT) return rc;
+  }
+  // a.x / a.xscale are the caller's x_q / scale_x workspace
+  int rc = launch_act_quant<DT>(ax.x, ax.ldx, a.M, ax.K, a.K,
+                                const_cast<int8_t*>(static_cast<const int8_t*>(a.x)), a.ldx,
+                                const_cast<float*>(a.xscale), s);
+  if (rc != LSQ_OK) return rc;
+  if (a.M <= 64 && !gemm) {
+    rc = launch_decode_a8<DT>(a, false, s);
     if (rc != LSQ_E_LAYOUT) return rc;
     using Sy = typename Act<DT>::storage;
     for (int64_t blk : {int64_t(32), int64_t(16)}) {
       if (blk >= a.M) continue;
       LinearArgs b = a;
       b.M = blk;
-      rc = launch_decode_a8<DT>(b, s);  // block 0; LSQ_E_LAYOUT: does not fit, nothing ran
+      rc = launch_decode_a8<DT>(b, false, s);  // block 0; LSQ_E_LAYOUT: does not fit, nothing ran
       if (rc == LSQ_E_LAYOUT) continue;
       if (rc != LSQ_OK) return rc;
       for (int64_t m0 = blk; m0 < a.M; m0 += blk) {
@@ -400,7 +410,7 @@ int run_w8a8(const LinearArgs& a, hipStream_t s) {
         b.y = static_cast<Sy*>(a.y) + m0 * a.ldy;
         b.xscale = a.xscale + m0;
         b.M = a.M - m0 < blk ? a.M - m0 : blk;
-        rc = launch_decode_a8<DT>(b, s);
+        rc = launch_decode_a8<DT>(b, false, s);
         if (rc != LSQ_OK) return rc;
       }
       return LSQ_OK;
@@ -476,16 +486,19 @@ extern "C" int lsq_w8a8_linear(const void* x, int64_t ldx, const int8_t* tiled,
   if (!x || !tiled || !scale_w || !y || !x_q || !scale_x) return LSQ_E_NULL;
   if ((reinterpret_cast<uintptr_t>(tiled) & 15) || (reinterpret_cast<uintptr_t>(x_q) & 15))
     return LSQ_E_ALIGN;
+  if (M > INT32_MAX || K > INT32_MAX / 2) return LSQ_E_SHAPE;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int64_t kp = pad_k(K);
-  int rc = lsq_act_quant_i8(x, ldx, dtype, M, K, x_q, kp, scale_x, stream);
-  if (rc != LSQ_OK) return rc;
-  LinearArgs a{x_q, kp, reinterpret_cast<const uint8_t*>(tiled), scale_w, scale_w_dtype, bias,
-               bias_dtype, y, ldy, M, N, kp, kp, 1, scale_x};
+  // ax: the layer on x as given (fused decode; K must be a multiple of 128 there);
+  // a: the same layer on the quantized workspace x_q [M, kp]
+  const uint8_t* tw = reinterpret_cast<const uint8_t*>(tiled);
+  LinearArgs ax{x, ldx, tw, scale_w, scale_w_dtype, bias, bias_dtype, y, ldy, M, N, K, kp, 1, nullptr};
+  LinearArgs a{x_q, kp, tw, scale_w, scale_w_dtype, bias, bias_dtype, y, ldy, M, N, kp, kp, 1, scale_x};
+  int rc;
   switch (dtype) {
-    case LSQ_F32: rc = run_w8a8<LSQ_F32>(a, s); break;
-    case LSQ_F16: rc = run_w8a8<LSQ_F16>(a, s); break;
-    default: rc = run_w8a8<LSQ_BF16>(a, s); break;
+    case LSQ_F32: rc = run_w8a8<LSQ_F32>(ax, a, s); break;
+    case LSQ_F16: rc = run_w8a8<LSQ_F16>(ax, a, s); break;
+    default: rc = run_w8a8<LSQ_BF16>(ax, a, s); break;
   }
   return rc == LSQ_E_LAYOUT ? LSQ_E_SHAPE : rc;
 }

@@ -134,6 +134,60 @@ def test_act_quant_bit_exact(dt, m, k, ldx):
     assert (xq[:, k:_pad_k(k)] == 0).all()  # padding columns
 
 
+def _near_tie_rows(dt, m, k, seed):
+    """Rows whose values sit on or next to half-integer multiples of the row's scale
+    (the cases where rint(v * rcp(s)) and rint(v / s) could part ways)."""
+    rng = np.random.default_rng(seed)
+    rows = []
+    for i in range(m):
+        mx = np.float32(rng.uniform(0.05, 300.0))
+        s = qo.act_scale_i8(np.array([[mx]], np.float32), dt)[0, 0]
+        kk = rng.integers(-127, 127, size=k).astype(np.float32)
+        d = rng.choice(np.array([0.0, 2.0 ** -12, -2.0 ** -12, 2.0 ** -20, -2.0 ** -20, 0.25], np.float32), size=k)
+        v = qo.round_to((kk + np.float32(0.5) + d) * s, dt)
+        v[0] = qo.round_to(np.array([mx], np.float32), dt)[0]
+        v = np.where(np.abs(v) > np.abs(v[0]), np.float32(0.0), v)  # keep v[0] the row max
+        rows.append(v)
+    return np.stack(rows).astype(np.float32)
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16", "f32"])
+def test_act_quant_near_ties_bit_exact(dt):
+    _say(f"act quant near ties {dt}")
+    x32 = _near_tie_rows(dt, 64, 512, 1)
+    xq, sx = _act_quant(torch.from_numpy(x32).to(TDT[dt]).to(DEV), 512)
+    ref_q, ref_s = qo.act_quant_i8(x32, dt)
+    assert np.array_equal(_bits(sx.cpu().numpy()), _bits(ref_s[:, 0]))
+    assert np.array_equal(xq.cpu().numpy()[:, :512], ref_q)
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16", "f32"])
+@pytest.mark.parametrize("m", [1, 4, 16])
+def test_w8a8_fused_quant_near_ties_bit_exact(monkeypatch, dt, m):
+    # the decode kernel's own quantization on the same near-tie rows
+    _say(f"w8a8 fused near ties {dt} M={m}")
+    k, n = 512, 272
+    x32 = _near_tie_rows(dt, m, k, 2 + m)
+    g = torch.Generator().manual_seed(m)
+    wq = torch.randint(-128, 128, (n, k), generator=g, dtype=torch.int8)
+    sw = torch.rand(n, generator=g) * 0.02 + 1e-3
+    y, _, _ = _linear(torch.from_numpy(x32).to(TDT[dt]).to(DEV), wq, sw, None, monkeypatch, "fused")
+    ref = qo.w8a8_linear(x32, wq.numpy(), sw.numpy(), None, dt)
+    assert np.array_equal(_bits(y.float().cpu().numpy()), _bits(ref))
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16", "f32"])
+@pytest.mark.parametrize("m,n,k", [(8, 272, 896), (16, 1000, 3584), (64, 272, 896)])
+def test_w8a8_forced_fused_decode_bit_exact(monkeypatch, dt, m, n, k):
+    # the in-kernel quantization on inputs the heuristic would send to the separate kernel
+    _say(f"w8a8 fused-forced {dt} M={m} N={n} K={k}")
+    x, wq, sw, bias = _lin_inputs(dt, m, n, k)
+    y, _, _ = _linear(x.to(DEV), wq, sw, bias, monkeypatch, "fused")
+    ref = qo.w8a8_linear(x.float().numpy(), wq.numpy(), sw.numpy(),
+                         None if bias is None else bias.float().numpy(), dt)
+    assert np.array_equal(_bits(y.float().cpu().numpy()), _bits(ref))
+
+
 # ----------------------------------------------------------------------------- linear
 
 
@@ -145,21 +199,45 @@ LIN_CASES = [
 ]
 
 
-@pytest.mark.parametrize("dt", ["bf16", "f16", "f32"])
-@pytest.mark.parametrize("m,n,k", LIN_CASES)
-def test_w8a8_linear_bit_exact(dt, m, n, k):
-    _say(f"w8a8 {dt} M={m} N={n} K={k}")
+def _lin_inputs(dt, m, n, k):
     g = torch.Generator().manual_seed(m + n + k)
     x = (torch.randn(m, k, generator=g) * 2).to(TDT[dt])
+    if m >= 3:
+        x[1] = 0                                           # zero row: scale = clamp bound
+        x[2] = 6e-8 if dt == "f16" else 3e-7               # fp16: scale rounds to 0
     wq = torch.randint(-128, 128, (n, k), generator=g, dtype=torch.int8)
     sw = torch.rand(n, generator=g) * 0.02 + 1e-3
     bias = (torch.randn(n, generator=g)).to(TDT[dt]) if (m + n) % 2 else None
+    return x, wq, sw, bias
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16", "f32"])
+@pytest.mark.parametrize("m,n,k", LIN_CASES)
+def test_w8a8_linear_bit_exact(dt, m, n, k):
+    # decode shapes with small x quantize inside the GEMV kernel (one launch)
+    _say(f"w8a8 {dt} M={m} N={n} K={k}")
+    x, wq, sw, bias = _lin_inputs(dt, m, n, k)
     y, _, _ = _linear(x.to(DEV), wq, sw, bias)
     ref = qo.w8a8_linear(x.float().numpy(), wq.numpy(), sw.numpy(),
                          None if bias is None else bias.float().numpy(), dt)
     got = y.float().cpu().numpy()
     mism = np.count_nonzero(_bits(got) != _bits(ref))
     assert mism == 0, f"{mism} of {got.size} outputs differ"
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16", "f32"])
+@pytest.mark.parametrize("m,n,k", [(1, 272, 896), (5, 1000, 896), (16, 272, 2048), (64, 272, 896)])
+def test_w8a8_unfused_decode_bit_exact(monkeypatch, dt, m, n, k):
+    # the same shapes through act_quant_kernel + the decode kernel on x_q
+    _say(f"w8a8 unfused {dt} M={m} N={n} K={k}")
+    x, wq, sw, bias = _lin_inputs(dt, m, n, k)
+    y, xq, sx = _linear(x.to(DEV), wq, sw, bias, monkeypatch, "unfused")
+    ref_q, ref_s = qo.act_quant_i8(x.float().numpy(), dt)
+    assert np.array_equal(xq.cpu().numpy()[:, :k], ref_q)
+    assert np.array_equal(_bits(sx.cpu().numpy()), _bits(ref_s[:, 0]))
+    ref = qo.w8a8_linear(x.float().numpy(), wq.numpy(), sw.numpy(),
+                         None if bias is None else bias.float().numpy(), dt)
+    assert np.array_equal(_bits(y.float().cpu().numpy()), _bits(ref))
 
 
 @pytest.mark.parametrize("m,n,k", [(1, 272, 896), (33, 272, 896), (64, 520, 1024)])
