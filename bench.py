@@ -36,6 +36,7 @@ import sys
 import time
 
 import torch
+import torch.nn.functional as F
 
 METRIC = "W-only INT4/INT8 GEMM: decode GB/s (% HBM peak); prefill TFLOP/s (% MFMA)"
 HBM_PEAK_GBS = 8000.0       # MI355X HBM3E, vendor spec
@@ -272,6 +273,69 @@ def bench_stack(steps: int, warmup: int, device, m: int = 32, n_layers: int = 24
     }
 
 
+def bench_mlp(steps: int, warmup: int, device, m: int = 32, n_layers: int = 24, group: int = 128,
+              fused: bool = False):
+    """The MLP blocks of one decode step of the same stack: down(silu(gate(x)) * up(x))
+    (modeling_qwen2.py:46-48) for 24 layers, INT4 group-128, batch m. Unfused: gate, up,
+    down launches plus torch's silu and mul (5 launches per layer). fused=True:
+    fuse_linears([gate, up], act="silu_mul") (one launch with the SiLU.mul epilogue) and
+    down (2 launches per layer)."""
+    from localstrm_amd import QuantizedLinear, fuse_linears
+
+    shapes = [l for l in QWEN05_LINEARS if l[0] in ("gate", "up", "down")]
+    protos = []
+    for _, n, k, _ in shapes:
+        p, s, _ = make_int4(n, k, 1, group, seed=n * 7 + k)
+        protos.append((p.to(device), s.to(device), k))
+    per_step = n_layers * sum(n * k // 2 + n * (-(-k // group)) * 2 + m * k * 2 + m * n * 2
+                              for _, n, k, _ in shapes)
+    copies = max(2, -(-2 * MALL_BYTES // per_step))
+
+    def one_layer():
+        g, u, d = [QuantizedLinear.from_quantized(p.clone(), s, quant_type="int4", in_features=k,
+                                                  group_size=group) for (p, s, k) in protos]
+        if fused:
+            gu = fuse_linears([g, u], act="silu_mul")
+            return lambda x: d(gu(x))
+        return lambda x: d(F.silu(g(x)) * u(x))
+
+    stacks = [[one_layer() for _ in range(n_layers)] for _ in range(copies)]
+    x = torch.randn(m, 896, generator=_gen(5)).to(torch.bfloat16).to(device)
+    stream = torch.cuda.Stream()
+    with torch.no_grad():
+        def run(i):
+            for mlp in stacks[i % copies]:
+                mlp(x)
+        for i in range(max(warmup, 1)):
+            run(i)
+        torch.cuda.synchronize()
+        stream.wait_stream(torch.cuda.current_stream())
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(stream):
+            with torch.cuda.graph(graph, stream=stream):
+                for i in range(steps):
+                    run(i)
+        graph.replay()
+        torch.cuda.synchronize()
+        start = torch.cuda.Event(enable_timing=True)
+        stop = torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(stream):
+            start.record(stream)
+            graph.replay()
+            stop.record(stream)
+        stop.synchronize()
+        del graph
+    ms = start.elapsed_time(stop) / steps
+    del stacks
+    torch.cuda.empty_cache()
+    return {
+        "kind": "int4 mlp" + (" fused silu_mul" if fused else ""), "M": m, "layers": n_layers,
+        "launches": n_layers * (2 if fused else 5), "group": group, "us_per_call": ms * 1e3,
+        "GB_s": per_step / (ms * 1e-3) / 1e9, "bytes": per_step, "stack_copies": copies,
+        "frac_hbm": per_step / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+    }
+
+
 # ----------------------------------------------------------------------------- CPU baseline
 
 
@@ -346,6 +410,10 @@ def main() -> int:
         print(json.dumps(bench_stack(max(2, args.steps), args.warmup, device,
                                      fused=args.case == "stack-fused")), flush=True)
         return 0
+    if args.case in ("mlp", "mlp-fused"):
+        print(json.dumps(bench_mlp(max(2, args.steps), args.warmup, device,
+                                   fused=args.case == "mlp-fused")), flush=True)
+        return 0
     if args.case:
         kind, n, k, m = args.case.split(",")
         r = bench_decode(kind, int(n), int(k), int(m), args.steps, args.warmup, device)
@@ -370,6 +438,8 @@ def main() -> int:
                                   max(2, args.warmup // 4), device))
         sweep.append(bench_stack(max(5, args.steps // 20), 2, device))
         sweep.append(bench_stack(max(5, args.steps // 20), 2, device, fused=True))
+        sweep.append(bench_mlp(max(5, args.steps // 20), 2, device))
+        sweep.append(bench_mlp(max(5, args.steps // 20), 2, device, fused=True))
     cpu = None if args.no_cpu else cpu_baseline(N, K, M)
 
     ms = head["us_per_call"] / 1e3

@@ -35,6 +35,10 @@ extern "C" {
 #define LSQ_F16 1
 #define LSQ_BF16 2
 
+/* epilogues of lsq_w8_linear_act / lsq_w4_linear_act */
+#define LSQ_ACT_NONE 0
+#define LSQ_ACT_SILU_MUL 1     /* y = silu(gate) * up over gate / up rows interleaved by 16 */
+
 /* argument errors (negative); positive values are hipError_t */
 #define LSQ_OK 0
 #define LSQ_E_NULL (-1)        /* a required pointer is NULL */
@@ -117,6 +121,33 @@ int lsq_w4_linear(const void* x, int64_t ldx, const uint8_t* weight_packed,
                   const uint8_t* tiled, const void* scale, int scale_dtype,
                   int64_t group_size, const void* bias, int bias_dtype, void* y, int64_t ldy,
                   int dtype, int64_t M, int64_t N, int64_t K, void* stream);
+
+/* ---- Fused gate / up with the SiLU.mul epilogue ----
+ * The MLP of the reference's decoder layers computes down_proj(silu(gate_proj(x)) *
+ * up_proj(x)) (modeling_qwen2.py:46-48), two launches and two elementwise kernels. No
+ * reference counterpart for these entry points: they serve a gate / up pair fused into one
+ * weight whose rows alternate 16 gate rows and the 16 up rows of the same outputs (row
+ * tile 2t = gate rows 16t..16t+15, tile 2t+1 = up rows 16t..16t+15), N = 2 * I rows,
+ * N % 32 == 0. With act = LSQ_ACT_SILU_MUL, y is [M, I] (row stride ldy >= I) and
+ *   y[m, j] = round_T( round_T(silu(g)) * u ),  g, u = the two layers' outputs in T
+ * (each as lsq_w8_linear / lsq_w4_linear computes it). The fused epilogue runs in the
+ * decode kernel (fp16 / bf16, M <= 64, K % 128 == 0, x in LDS); other shapes return
+ * LSQ_E_LAYOUT without launching anything: run the plain entry point on the interleaved
+ * weight and lsq_silu_mul on its output. act = LSQ_ACT_NONE is the plain entry point. */
+int lsq_w8_linear_act(const void* x, int64_t ldx, const int8_t* weight_q, const int8_t* tiled,
+                      const void* scale, int scale_dtype, const void* bias, int bias_dtype,
+                      void* y, int64_t ldy, int dtype, int64_t M, int64_t N, int64_t K, int act,
+                      void* stream);
+int lsq_w4_linear_act(const void* x, int64_t ldx, const uint8_t* weight_packed,
+                      const uint8_t* tiled, const void* scale, int scale_dtype,
+                      int64_t group_size, const void* bias, int bias_dtype, void* y, int64_t ldy,
+                      int dtype, int64_t M, int64_t N, int64_t K, int act, void* stream);
+
+/* out[m, j] = round_T(round_T(silu(g)) * u) from the interleaved output in [M, 2 I] (row
+ * stride ld_in) of a fused gate / up layer: g = in[m, 32 (j/16) + j%16], u the element 16
+ * further. I % 16 == 0. No reference counterpart (F.silu(gate) * up, modeling_qwen2.py:48). */
+int lsq_silu_mul(const void* in, int64_t ld_in, void* out, int64_t ld_out, int dtype, int64_t M,
+                 int64_t I, void* stream);
 
 /* ---- W8A8: Int8GEMMLinear (the MLP layers of the reference's 'hybrid_int8' mode) ----
  * Weights: weight_q_t int8 [K, N] (N contiguous) and scale_w_t [N] (fp32 in the

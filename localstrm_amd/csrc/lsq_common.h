@@ -95,6 +95,15 @@ __device__ __forceinline__ float dequant_elem(int q, float s_T) {
   return Act<DT>::round(mul_rn(static_cast<float>(q), s_T));
 }
 
+// The value of x as computed, kept from being folded into a following conversion: gfx950
+// can multiply (or FMA) and round straight to fp16 / bf16 in one instruction (v_fma_mix),
+// which rounds once where the separate fp32 operation and conversion round twice. Code
+// that must round like an fp32 result converted to T passes the fp32 value through here.
+__device__ __forceinline__ float opaque(float x) {
+  __asm__ volatile("" : "+v"(x));
+  return x;
+}
+
 // ---------------------------------------------------------------- W8A8 activations
 // Per-token scale from the row's max|x| (as fp32): clamp(round_T(max * fp32(1/127)),
 // min = round_T(1e-8)), the GPU evaluation of quantization.py:412-413 (torch multiplies
@@ -102,7 +111,7 @@ __device__ __forceinline__ float dequant_elem(int q, float s_T) {
 template <int DT>
 __device__ __forceinline__ float a8_scale(float mx) {
   constexpr float kInv127 = 1.0f / 127.0f;
-  const float s = Act<DT>::round(mul_nc(mx, kInv127));
+  const float s = Act<DT>::round(opaque(mul_nc(mx, kInv127)));  // fp32 product, then T
   const float smin = Act<DT>::round(1e-8f);
   return s < smin ? smin : s;
 }

@@ -29,6 +29,8 @@ struct LinearArgs {
   int64_t group;       // columns per scale group (== K for per-channel)
   int64_t ngroups;
   const float* xscale = nullptr;  // W8A8 only: per-token activation scales [M]
+  int act = 0;                    // LSQ_ACT_SILU_MUL: gate / up rows interleaved by 16-row
+                                  // tiles, y [M, N / 2] = silu(gate) * up (decode kernel only)
 };
 
 // Launches the LDS-staged decode kernel when the shape fits it (M <= 64, K % 128 == 0,

@@ -63,7 +63,7 @@ constexpr int kSB = 8;  // scale dwords in flight per thread while staging
 // per-(k tile, token) activation sums, per-token totals, the workgroup's scales and bias
 // as fp32 (already rounded to the activation type), cross-slice partial sums.
 struct DecodeLds {
-  int64_t xs, xsum, xtot, ss, sb, red, total;
+  int64_t xs, xsum, xtot, ss, sb, red, xch, total;
 };
 
 // Bytes of one staged activation row: K + 8 16-bit values, or (W8A8) K + 16 int8 values.
@@ -72,7 +72,8 @@ __host__ __device__ constexpr int64_t x_row_bytes(int64_t K, bool a8) {
 }
 
 __host__ __device__ inline DecodeLds decode_lds(int64_t M, int64_t K, int rows, int64_t ngs,
-                                                int red_floats, int mp, bool a8) {
+                                                int red_floats, int mp, bool a8,
+                                                int xch_floats = 0) {
   DecodeLds l;
   const int64_t nkt = K / kTileK;
   l.xs = 0;
@@ -81,7 +82,8 @@ __host__ __device__ inline DecodeLds decode_lds(int64_t M, int64_t K, int rows, 
   l.ss = l.xtot + mp * 4;
   l.sb = l.ss + align16(rows * ngs * 4);
   l.red = l.sb + align16(rows * 4);
-  l.total = l.red + static_cast<int64_t>(red_floats) * 4;
+  l.xch = l.red + static_cast<int64_t>(red_floats) * 4;
+  l.total = l.xch + static_cast<int64_t>(xch_floats) * 4;
   return l;
 }
 
@@ -163,7 +165,10 @@ __global__ void __launch_bounds__(64 * RG * KS) decode_kernel(LinearArgs p) {
   const int gtiles = static_cast<int>(p.group / kTileK);
   const int ldxb = static_cast<int>(x_row_bytes(K, A8 != 0));  // LDS bytes per staged row
 
-  const DecodeLds L = decode_lds(M, K, ROWS, ngs, RED, MP, A8 != 0);
+  // SiLU.mul epilogue: each up-row wave hands its outputs to the gate-row wave beside it
+  const bool act = !A8 && p.act == LSQ_ACT_SILU_MUL;  // uniform
+  const int XCH = act ? (RG / 2) * RT * MB * 4 * 64 : 0;
+  const DecodeLds L = decode_lds(M, K, ROWS, ngs, RED, MP, A8 != 0, XCH);
   unsigned char* xs = smem + L.xs;
   float* xsum = reinterpret_cast<float*>(smem + L.xsum);
   float* xtot = reinterpret_cast<float*>(smem + L.xtot);
@@ -519,24 +524,70 @@ __global__ void __launch_bounds__(64 * RG * KS) decode_kernel(LinearArgs p) {
             red[(((((ks - 1) * RG + rg) * RT + i) * MB + mb) * 4 + e) * 64 + lane] = acc[i][mb][e];
     }
     lds_barrier();
-    if (ks > 0) return;
+    if (ks == 0) {  // (waves of the other slices stay alive for the SiLU.mul barrier)
 #pragma unroll
-    for (int kk = 0; kk < KS - 1; ++kk)
+      for (int kk = 0; kk < KS - 1; ++kk)
 #pragma unroll
-      for (int i = 0; i < RT; ++i)
+        for (int i = 0; i < RT; ++i)
+#pragma unroll
+          for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const float v = red[((((kk * RG + rg) * RT + i) * MB + mb) * 4 + e) * 64 + lane];
+              if constexpr (A8)  // int32 partial sums (exact, in any order)
+                acc[i][mb][e] = __int_as_float(__float_as_int(acc[i][mb][e]) + __float_as_int(v));
+              else
+                acc[i][mb][e] += v;
+            }
+    }
+  }
+
+  S* y = static_cast<S*>(p.y);
+  if constexpr (!A8) {
+    if (act) {
+      // Row tile 2t holds gate rows 16t.., tile 2t + 1 the up rows of the same outputs
+      // (RT == 1 and RG even, so the pair is waves rg, rg + 1 of one workgroup). Each
+      // value is first rounded to T as its own layer would output it; then
+      // y = round_T(round_T(silu(g)) * u), as F.silu(gate) * up evaluates it.
+      float* xch = reinterpret_cast<float*>(smem + L.xch);
+      const int rl = rtl * kTileN + r;
+      const float sc = GROUPED ? 1.f : ss[rl];
+      const float bias = p.bias ? sb[rl] : 0.f;
+      float vt[MB][4];
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          float v = acc[0][mb][e];
+          if constexpr (W4 && !GROUPED) v = fmaf(-Mma<DT>::kOff4, xtot[16 * mb + 4 * q + e], v);
+          vt[mb][e] = Act<DT>::round(opaque(GROUPED ? v + bias : fmaf(v, sc, bias)));
+        }
+      const bool up = (rg & 1) != 0;
+      if (ks == 0 && up) {
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) xch[(((rg >> 1) * MB + mb) * 4 + e) * 64 + lane] = vt[mb][e];
+      }
+      lds_barrier();
+      if (ks == 0 && !up) {
+        const int j = ((rt_wg + rtl) >> 1) * kTileN + r;  // output column
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            const float v = red[((((kk * RG + rg) * RT + i) * MB + mb) * 4 + e) * 64 + lane];
-            if constexpr (A8)  // int32 partial sums (exact, in any order)
-              acc[i][mb][e] = __int_as_float(__float_as_int(acc[i][mb][e]) + __float_as_int(v));
-            else
-              acc[i][mb][e] += v;
+            const int m = 16 * mb + 4 * q + e;
+            const float g = vt[mb][e];
+            const float u = xch[(((rg >> 1) * MB + mb) * 4 + e) * 64 + lane];
+            const float sg = Act<DT>::round(opaque(g / (1.f + __expf(-g))));
+            // fp32 product, then the rounding to T (not one fused multiply-round)
+            if (m < M && 2 * j < N) y[static_cast<int64_t>(m) * p.ldy + j] = Act<DT>::from_f32(opaque(sg * u));
           }
+      }
+      return;
+    }
   }
-
-  S* y = static_cast<S*>(p.y);
+  if (ks > 0) return;
 #pragma unroll
   for (int i = 0; i < RT; ++i) {
     const int rl = (rtl + i) * kTileN + r;  // row within the workgroup
@@ -554,12 +605,12 @@ __global__ void __launch_bounds__(64 * RG * KS) decode_kernel(LinearArgs p) {
             const float sxm = A8 == kA8Fused ? a8_scale<DT>(xtot[m]) : xtot[m];
             float v = mul_nc(static_cast<float>(__float_as_int(acc[i][mb][e])), mul_nc(sxm, sc));
             if (p.bias) v = add_nc(v, bias);
-            y[static_cast<int64_t>(m) * p.ldy + n] = Act<DT>::from_f32(v);
+            y[static_cast<int64_t>(m) * p.ldy + n] = Act<DT>::from_f32(opaque(v));
           } else {
             float v = acc[i][mb][e];
             if constexpr (W4 && !GROUPED) v = fmaf(-Mma<DT>::kOff4, xtot[m], v);
-            if (!GROUPED) v *= sc;
-            y[static_cast<int64_t>(m) * p.ldy + n] = Act<DT>::from_f32(v + bias);
+            // scale and bias as one explicit FMA, so every code shape rounds alike
+            y[static_cast<int64_t>(m) * p.ldy + n] = Act<DT>::from_f32(opaque(GROUPED ? v + bias : fmaf(v, sc, bias)));
           }
         }
       }
@@ -639,7 +690,10 @@ int launch_one(const LinearArgs& a, hipStream_t s) {
     if (a.M * (a.K / XE) > int64_t(64 * RG * KS) * prologue_chunks(64 * RG * KS)) return LSQ_E_LAYOUT;
   }
   const bool grouped = a.group < a.K;
-  const DecodeLds L = decode_lds(a.M, a.K, RG * RT * kTileN, grouped ? a.ngroups : 1, RED, 16 * MB, A8 != 0);
+  const int XCH = (!A8 && a.act == LSQ_ACT_SILU_MUL) ? (RG / 2) * RT * MB * 4 * 64 : 0;
+  if (XCH && (RT != 1 || RG % 2 != 0)) return LSQ_E_LAYOUT;
+  const DecodeLds L = decode_lds(a.M, a.K, RG * RT * kTileN, grouped ? a.ngroups : 1, RED, 16 * MB,
+                                 A8 != 0, XCH);
   if (L.total > max_lds_bytes()) return LSQ_E_LAYOUT;
   auto kern = decode_kernel<DT, KIND, RT, RG, KS, D, GROUPED, MB, A8>;
   if (L.total > 64 * 1024) {
@@ -660,7 +714,8 @@ int launch_one(const LinearArgs& a, hipStream_t s) {
 
 template <int DT, int KIND, bool GROUPED, int A8 = 0>
 int launch_kind(const LinearArgs& a, hipStream_t s) {
-  const Cfg c = pick_cfg(KIND, a.M, a.N, a.K);
+  Cfg c = pick_cfg(KIND, a.M, a.N, a.K);
+  if (a.act && (c.rt != 1 || c.rg % 2 != 0)) c = Cfg{1, 2, 4, 4};  // gate / up tile pairs
   if (a.M > 16) {
     // 17..64 tokens in 2 or 4 blocks of 16; only the configurations pick_cfg returns
 #define LSQ_TRY_MB(RT_, RG_, KS_, D_)                                                   \

@@ -332,9 +332,8 @@ __global__ void __launch_bounds__(64 * RG * KS) decode_mb_kernel(LinearArgs p) {
       for (int e = 0; e < 4; ++e) {
         const int m = 16 * mb + 4 * q + e;
         if (m < M) {
-          float v = acc[mb][e];
-          if (!GROUPED) v *= sc;
-          y[static_cast<int64_t>(m) * p.ldy + n] = Act<DT>::from_f32(v + bias);
+          const float v = acc[mb][e];
+          y[static_cast<int64_t>(m) * p.ldy + n] = Act<DT>::from_f32(opaque(GROUPED ? v + bias : fmaf(v, sc, bias)));
         }
       }
   }

@@ -108,11 +108,19 @@ static bool x_aligned16(const void* x, int64_t ldx) {
 template <int DT>
 static int dispatch(bool w4, const void* x, int64_t ldx, const uint8_t* w, const uint8_t* tiled,
                     const void* scale, int scale_dt, int64_t group, const void* bias, int bias_dt,
-                    void* y, int64_t ldy, int64_t M, int64_t N, int64_t K, hipStream_t s) {
+                    void* y, int64_t ldy, int64_t M, int64_t N, int64_t K, hipStream_t s,
+                    int act = LSQ_ACT_NONE) {
   const int64_t ng = (K + group - 1) / group;
   if constexpr (DT != LSQ_F32) {
     const bool mfma_ok = K % kTileK == 0 && x_aligned16(x, ldx) &&
                          (reinterpret_cast<uintptr_t>(w) & 15) == 0;
+    if (act != LSQ_ACT_NONE) {  // the fused epilogue exists in the decode kernel only
+      if (!mfma_ok || M > 64) return LSQ_E_LAYOUT;
+      LinearArgs a{x, ldx, tiled ? tiled : w, scale, scale_dt, bias, bias_dt, y, ldy,
+                   M, N, K, group, ng};
+      a.act = act;
+      return launch_decode<DT>(w4 ? (tiled ? kW4Tiled : kW4Canon) : (tiled ? kW8Tiled : kW8), a, s);
+    }
     if (mfma_ok) {
       LinearArgs a{x, ldx, tiled ? tiled : w, scale, scale_dt, bias, bias_dt, y, ldy,
                    M, N, K, group, ng};
@@ -126,8 +134,39 @@ static int dispatch(bool w4, const void* x, int64_t ldx, const uint8_t* w, const
       if (rc != LSQ_E_LAYOUT) return rc;
     }
   }
+  if (act != LSQ_ACT_NONE) return LSQ_E_LAYOUT;
   return launch_generic<DT>(w4, x, ldx, w, scale, scale_dt, group, bias, bias_dt, y, ldy, M, N, K,
                             s);
+}
+
+// ============================================================ SiLU.mul over interleaved rows
+
+// out[m, j] = round_T(round_T(silu(g)) * u), g = in[m, 32 (j / 16) + j % 16] and
+// u = in[m, 32 (j / 16) + 16 + j % 16]: the 16-row gate / up interleave of a fused
+// gate / up layer (F.silu(gate_proj(x)) * up_proj(x), modeling_qwen2.py:46-48).
+template <int DT>
+__global__ void __launch_bounds__(256) silu_mul_kernel(const typename Act<DT>::storage* __restrict__ in,
+                                                       int64_t ldi, typename Act<DT>::storage* __restrict__ out,
+                                                       int64_t ldo, int64_t M, int64_t I) {
+  const int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
+  if (i >= M * I) return;
+  const int64_t m = i / I, j = i - m * I;
+  const int64_t c = 32 * (j >> 4) + (j & 15);
+  const float g = Act<DT>::to_f32(in[m * ldi + c]);
+  const float u = Act<DT>::to_f32(in[m * ldi + c + 16]);
+  const float sg = Act<DT>::round(opaque(g / (1.f + __expf(-g))));
+  out[m * ldo + j] = Act<DT>::from_f32(opaque(sg * u));  // fp32 product, then round to T
+}
+
+template <int DT>
+static int launch_silu_mul(const void* in, int64_t ldi, void* out, int64_t ldo, int64_t M, int64_t I,
+                           hipStream_t s) {
+  using S = typename Act<DT>::storage;
+  const int64_t blocks = (M * I + 255) / 256;
+  if (blocks > INT32_MAX) return LSQ_E_SHAPE;
+  silu_mul_kernel<DT><<<dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s>>>(
+      static_cast<const S*>(in), ldi, static_cast<S*>(out), ldo, M, I);
+  return static_cast<int>(hipGetLastError());
 }
 
 }  // namespace lsq
@@ -151,12 +190,13 @@ extern "C" const char* lsq_status_string(int status) {
   return "lsq: unknown status";
 }
 
-extern "C" int lsq_w8_linear(const void* x, int64_t ldx, const int8_t* weight_q,
-                             const int8_t* tiled, const void* scale, int scale_dtype,
-                             const void* bias, int bias_dtype, void* y, int64_t ldy, int dtype,
-                             int64_t M, int64_t N, int64_t K, void* stream) {
-  const int rc = check_common(x, ldx, weight_q, scale, y, ldy, dtype, bias_dtype, bias, M, N, K);
+static int w8_linear(const void* x, int64_t ldx, const int8_t* weight_q, const int8_t* tiled,
+                     const void* scale, int scale_dtype, const void* bias, int bias_dtype, void* y,
+                     int64_t ldy, int dtype, int64_t M, int64_t N, int64_t K, void* stream, int act) {
+  const int64_t ny = act == LSQ_ACT_SILU_MUL ? N / 2 : N;  // output columns
+  const int rc = check_common(x, ldx, weight_q, scale, y, ldy, dtype, bias_dtype, bias, M, ny, K);
   if (rc != LSQ_OK) return rc;
+  if (act != LSQ_ACT_NONE && (act != LSQ_ACT_SILU_MUL || N % 32 != 0)) return LSQ_E_LAYOUT;
   if (scale_dtype != LSQ_F32 && scale_dtype != LSQ_F16 && scale_dtype != LSQ_BF16) return LSQ_E_DTYPE;
   if (tiled && (reinterpret_cast<uintptr_t>(tiled) & 15)) return LSQ_E_ALIGN;
   if (tiled && K % kTileK != 0) return LSQ_E_LAYOUT;
@@ -166,18 +206,36 @@ extern "C" int lsq_w8_linear(const void* x, int64_t ldx, const int8_t* weight_q,
   const uint8_t* t = reinterpret_cast<const uint8_t*>(tiled);
   const int64_t group = K > 0 ? K : 1;
   switch (dtype) {
-    case LSQ_F32: return dispatch<LSQ_F32>(false, x, ldx, w, t, scale, scale_dtype, group, bias, bias_dtype, y, ldy, M, N, K, s);
-    case LSQ_F16: return dispatch<LSQ_F16>(false, x, ldx, w, t, scale, scale_dtype, group, bias, bias_dtype, y, ldy, M, N, K, s);
-    default: return dispatch<LSQ_BF16>(false, x, ldx, w, t, scale, scale_dtype, group, bias, bias_dtype, y, ldy, M, N, K, s);
+    case LSQ_F32: return dispatch<LSQ_F32>(false, x, ldx, w, t, scale, scale_dtype, group, bias, bias_dtype, y, ldy, M, N, K, s, act);
+    case LSQ_F16: return dispatch<LSQ_F16>(false, x, ldx, w, t, scale, scale_dtype, group, bias, bias_dtype, y, ldy, M, N, K, s, act);
+    default: return dispatch<LSQ_BF16>(false, x, ldx, w, t, scale, scale_dtype, group, bias, bias_dtype, y, ldy, M, N, K, s, act);
   }
 }
 
-extern "C" int lsq_w4_linear(const void* x, int64_t ldx, const uint8_t* weight_packed,
-                             const uint8_t* tiled, const void* scale, int scale_dtype,
-                             int64_t group_size, const void* bias, int bias_dtype, void* y,
-                             int64_t ldy, int dtype, int64_t M, int64_t N, int64_t K, void* stream) {
-  const int rc = check_common(x, ldx, weight_packed, scale, y, ldy, dtype, bias_dtype, bias, M, N, K);
+extern "C" int lsq_w8_linear(const void* x, int64_t ldx, const int8_t* weight_q,
+                             const int8_t* tiled, const void* scale, int scale_dtype,
+                             const void* bias, int bias_dtype, void* y, int64_t ldy, int dtype,
+                             int64_t M, int64_t N, int64_t K, void* stream) {
+  return w8_linear(x, ldx, weight_q, tiled, scale, scale_dtype, bias, bias_dtype, y, ldy, dtype, M,
+                   N, K, stream, LSQ_ACT_NONE);
+}
+
+extern "C" int lsq_w8_linear_act(const void* x, int64_t ldx, const int8_t* weight_q,
+                                 const int8_t* tiled, const void* scale, int scale_dtype,
+                                 const void* bias, int bias_dtype, void* y, int64_t ldy, int dtype,
+                                 int64_t M, int64_t N, int64_t K, int act, void* stream) {
+  return w8_linear(x, ldx, weight_q, tiled, scale, scale_dtype, bias, bias_dtype, y, ldy, dtype, M,
+                   N, K, stream, act);
+}
+
+static int w4_linear(const void* x, int64_t ldx, const uint8_t* weight_packed, const uint8_t* tiled,
+                     const void* scale, int scale_dtype, int64_t group_size, const void* bias,
+                     int bias_dtype, void* y, int64_t ldy, int dtype, int64_t M, int64_t N, int64_t K,
+                     void* stream, int act) {
+  const int64_t ny = act == LSQ_ACT_SILU_MUL ? N / 2 : N;  // output columns
+  const int rc = check_common(x, ldx, weight_packed, scale, y, ldy, dtype, bias_dtype, bias, M, ny, K);
   if (rc != LSQ_OK) return rc;
+  if (act != LSQ_ACT_NONE && (act != LSQ_ACT_SILU_MUL || N % 32 != 0)) return LSQ_E_LAYOUT;
   if (group_size < 1) return LSQ_E_GROUP;
   if (scale_dtype != LSQ_F32 && scale_dtype != LSQ_F16 && scale_dtype != LSQ_BF16) return LSQ_E_DTYPE;
   if (tiled && (reinterpret_cast<uintptr_t>(tiled) & 15)) return LSQ_E_ALIGN;
@@ -186,8 +244,39 @@ extern "C" int lsq_w4_linear(const void* x, int64_t ldx, const uint8_t* weight_p
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int64_t group = K > 0 ? (group_size < K ? group_size : K) : 1;
   switch (dtype) {
-    case LSQ_F32: return dispatch<LSQ_F32>(true, x, ldx, weight_packed, tiled, scale, scale_dtype, group, bias, bias_dtype, y, ldy, M, N, K, s);
-    case LSQ_F16: return dispatch<LSQ_F16>(true, x, ldx, weight_packed, tiled, scale, scale_dtype, group, bias, bias_dtype, y, ldy, M, N, K, s);
-    default: return dispatch<LSQ_BF16>(true, x, ldx, weight_packed, tiled, scale, scale_dtype, group, bias, bias_dtype, y, ldy, M, N, K, s);
+    case LSQ_F32: return dispatch<LSQ_F32>(true, x, ldx, weight_packed, tiled, scale, scale_dtype, group, bias, bias_dtype, y, ldy, M, N, K, s, act);
+    case LSQ_F16: return dispatch<LSQ_F16>(true, x, ldx, weight_packed, tiled, scale, scale_dtype, group, bias, bias_dtype, y, ldy, M, N, K, s, act);
+    default: return dispatch<LSQ_BF16>(true, x, ldx, weight_packed, tiled, scale, scale_dtype, group, bias, bias_dtype, y, ldy, M, N, K, s, act);
+  }
+}
+
+extern "C" int lsq_w4_linear(const void* x, int64_t ldx, const uint8_t* weight_packed,
+                             const uint8_t* tiled, const void* scale, int scale_dtype,
+                             int64_t group_size, const void* bias, int bias_dtype, void* y,
+                             int64_t ldy, int dtype, int64_t M, int64_t N, int64_t K, void* stream) {
+  return w4_linear(x, ldx, weight_packed, tiled, scale, scale_dtype, group_size, bias, bias_dtype, y,
+                   ldy, dtype, M, N, K, stream, LSQ_ACT_NONE);
+}
+
+extern "C" int lsq_w4_linear_act(const void* x, int64_t ldx, const uint8_t* weight_packed,
+                                 const uint8_t* tiled, const void* scale, int scale_dtype,
+                                 int64_t group_size, const void* bias, int bias_dtype, void* y,
+                                 int64_t ldy, int dtype, int64_t M, int64_t N, int64_t K, int act,
+                                 void* stream) {
+  return w4_linear(x, ldx, weight_packed, tiled, scale, scale_dtype, group_size, bias, bias_dtype, y,
+                   ldy, dtype, M, N, K, stream, act);
+}
+
+extern "C" int lsq_silu_mul(const void* in, int64_t ld_in, void* out, int64_t ld_out, int dtype,
+                            int64_t M, int64_t I, void* stream) {
+  if (M < 0 || I < 0 || I % 16 != 0 || ld_in < 2 * I || ld_out < I) return LSQ_E_SHAPE;
+  if (dtype != LSQ_F32 && dtype != LSQ_F16 && dtype != LSQ_BF16) return LSQ_E_DTYPE;
+  if (M == 0 || I == 0) return LSQ_OK;
+  if (!in || !out) return LSQ_E_NULL;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case LSQ_F32: return launch_silu_mul<LSQ_F32>(in, ld_in, out, ld_out, M, I, s);
+    case LSQ_F16: return launch_silu_mul<LSQ_F16>(in, ld_in, out, ld_out, M, I, s);
+    default: return launch_silu_mul<LSQ_BF16>(in, ld_in, out, ld_out, M, I, s);
   }
 }

@@ -324,7 +324,7 @@ __global__ void __launch_bounds__(QNT) w8a8_gemm_kernel(LinearArgs p) {
         if (m < M && n < N) {
           float r = mul_nc(static_cast<float>(acc[i][j][v]), mul_nc(sxs[ml], swn[j]));
           if (p.bias) r = add_nc(r, bsn[j]);
-          y[static_cast<int64_t>(m) * p.ldy + n] = Act<DT>::from_f32(r);
+          y[static_cast<int64_t>(m) * p.ldy + n] = Act<DT>::from_f32(opaque(r));
         }
       }
     }

@@ -395,6 +395,49 @@ class QuantizedLinear(nn.Module):
         _lib.check(rc, f"lsq_{'w8' if self.quant_type == 'int8' else 'w4'}_linear")
         return y.reshape(*x.shape[:-1], self.out_features)
 
+    def _silu_mul_forward(self, x: torch.Tensor) -> torch.Tensor:
+        """silu(gate) * up for a layer whose rows interleave 16 gate rows and the 16 up rows
+        of the same outputs (built by fuse_linears(..., act="silu_mul")): the decode
+        kernel's fused epilogue when the shape allows, else the plain forward followed by
+        liblsq's elementwise lsq_silu_mul. Returns [..., out_features // 2]."""
+        _require_gpu(x, "forward")
+        if x.shape[-1] != self.in_features:
+            return self._hip_forward(x)  # raises the shape error
+        n_out = self.out_features // 2
+        x2 = x.reshape(-1, self.in_features)
+        if x2.stride(-1) != 1 or (x2.shape[0] > 1 and x2.stride(0) < self.in_features):
+            x2 = x2.contiguous()
+        m = x2.shape[0]
+        y = torch.empty((m, n_out), dtype=x.dtype, device=x.device)
+        lib = _lib.load()
+        stream = _lib.stream_handle(x.device)
+        if m > 0 and x.dtype in (torch.float16, torch.bfloat16):
+            bias = self.bias.detach().to(x.device).contiguous() if self.bias is not None else None
+            scale = self.scale if self.scale.is_contiguous() else self.scale.contiguous()
+            tiled = self._tiled_for_forward()
+            ldx = x2.stride(0) if m > 1 else self.in_features
+            bias_args = (_lib.ptr(bias), _lib.dtype_code(bias.dtype) if bias is not None else 0)
+            if self.quant_type == "int8":
+                rc = lib.lsq_w8_linear_act(x2.data_ptr(), ldx, self.weight_q.data_ptr(), _lib.ptr(tiled),
+                                           scale.data_ptr(), _lib.dtype_code(scale.dtype), *bias_args,
+                                           y.data_ptr(), n_out, _lib.dtype_code(x.dtype), m,
+                                           self.out_features, self.in_features, _lib.ACT_SILU_MUL, stream)
+            else:
+                rc = lib.lsq_w4_linear_act(x2.data_ptr(), ldx, self.weight_packed.data_ptr(),
+                                           _lib.ptr(tiled), scale.data_ptr(), _lib.dtype_code(scale.dtype),
+                                           self._group_for_kernel(), *bias_args, y.data_ptr(), n_out,
+                                           _lib.dtype_code(x.dtype), m, self.out_features,
+                                           self.in_features, _lib.ACT_SILU_MUL, stream)
+            if rc == 0:
+                return y.reshape(*x.shape[:-1], n_out)
+            if rc != -5:  # LSQ_E_LAYOUT: no fused epilogue for this shape
+                _lib.check(rc, "lsq_linear_act")
+        y2 = self._hip_forward(x2)
+        if m > 0:
+            _lib.check(lib.lsq_silu_mul(y2.data_ptr(), self.out_features, y.data_ptr(), n_out,
+                                        _lib.dtype_code(x.dtype), m, n_out, stream), "lsq_silu_mul")
+        return y.reshape(*x.shape[:-1], n_out)
+
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         """y = x @ dequantize(x.dtype).T + bias.to(x.dtype) (quantization.py:129-141)."""
         if self.quant_type not in ("int8", "int4"):
@@ -436,32 +479,64 @@ class FusedQuantizedLinear(nn.Module):
     the same hidden state). The layers' weights, scales and biases are concatenated along
     the output dimension into one QuantizedLinear (`fused`); forward runs it once and
     returns one output per layer, as views of the single output (last dimension split
-    into `splits`). Every output element is computed exactly as its own layer would
-    compute it; only the launch count changes.
+    into `splits`). Every output element is computed as its own layer computes it (same
+    dequantized weights, fp32 accumulation; the order of the fp32 partial sums follows the
+    kernel configuration of the fused shape); only the launch count changes.
+
+    act="silu_mul" (a gate / up pair, rows interleaved by 16): forward returns the single
+    tensor F.silu(gate(x)) * up(x) (modeling_qwen2.py:48), from one launch in the decode
+    kernel's fused epilogue, else from the plain launch plus one elementwise kernel.
     """
 
-    def __init__(self, fused: QuantizedLinear, splits: List[int]):
+    def __init__(self, fused: QuantizedLinear, splits: List[int], act: Optional[str] = None):
         super().__init__()
+        if act not in (None, "silu_mul"):
+            raise ValueError(f"act must be None or 'silu_mul', got {act!r}")
         self.fused = fused
         self.splits = [int(v) for v in splits]
+        self.act = act
         self.in_features = fused.in_features
-        self.out_features = fused.out_features
+        self.out_features = fused.out_features if act is None else fused.out_features // 2
 
-    def forward(self, x: torch.Tensor) -> Tuple[torch.Tensor, ...]:
-        return tuple(torch.split(self.fused(x), self.splits, dim=-1))
+    def forward(self, x: torch.Tensor):
+        """act None: one output per fused layer. act 'silu_mul' (a gate / up pair): the
+        single tensor F.silu(gate(x)) * up(x)."""
+        if self.act is None:
+            return tuple(torch.split(self.fused(x), self.splits, dim=-1))
+        needs_grad = torch.is_grad_enabled() and (
+            x.requires_grad or (self.fused.bias is not None and self.fused.bias.requires_grad))
+        if not needs_grad:
+            return self.fused._silu_mul_forward(x)
+        y2 = self.fused(x)  # differentiable path: de-interleave, then torch's ops
+        y2 = y2.reshape(*y2.shape[:-1], self.out_features // 16, 2, 16)
+        g = y2[..., 0, :].reshape(*y2.shape[:-3], self.out_features)
+        u = y2[..., 1, :].reshape(*y2.shape[:-3], self.out_features)
+        return F.silu(g) * u
 
     def memory_footprint_bytes(self) -> int:
         return self.fused.memory_footprint_bytes()
 
     def extra_repr(self) -> str:
-        return f"splits={self.splits}"
+        return f"splits={self.splits}" + (f", act={self.act}" if self.act else "")
 
 
-def fuse_linears(layers: List[QuantizedLinear]) -> FusedQuantizedLinear:
+def _interleave16(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """Rows of a and b (same shape [I, ...], I % 16 == 0) in the order a[0:16], b[0:16],
+    a[16:32], b[16:32], ... (the gate / up tile pairs of the SiLU.mul epilogue)."""
+    i = a.shape[0]
+    rest = a.shape[1:]
+    return torch.stack([a.reshape(i // 16, 16, *rest), b.reshape(i // 16, 16, *rest)], dim=1).reshape(2 * i, *rest)
+
+
+def fuse_linears(layers: List[QuantizedLinear], act: Optional[str] = None) -> FusedQuantizedLinear:
     """Fuse quantized layers with the same input into one launch (see
     FusedQuantizedLinear). All layers must share quant_type (int8 / int4), in_features,
     group size, scale dtype and device; a layer without bias contributes zeros when
-    others have one."""
+    others have one.
+
+    act="silu_mul" takes exactly [gate_proj, up_proj] (same out_features I, a multiple of
+    16) and fuses them with rows interleaved by 16, so that forward returns
+    F.silu(gate(x)) * up(x) from one launch (the MLP of modeling_qwen2.py:46-48)."""
     if not layers:
         raise ValueError("fuse_linears needs at least one layer")
     first = layers[0]
@@ -479,12 +554,20 @@ def fuse_linears(layers: List[QuantizedLinear]) -> FusedQuantizedLinear:
             raise ValueError(f"fuse_linears: scale dtype {l.scale.dtype} differs from {first.scale.dtype}")
         if l._canonical().device != first._canonical().device:
             raise ValueError("fuse_linears: layers are on different devices")
-    weight = torch.cat([l._canonical() for l in layers], dim=0)
-    scale = torch.cat([l.scale for l in layers], dim=0)
+    if act not in (None, "silu_mul"):
+        raise ValueError(f"fuse_linears: act must be None or 'silu_mul', got {act!r}")
+    if act == "silu_mul":
+        if len(layers) != 2 or layers[0].out_features != layers[1].out_features:
+            raise ValueError("fuse_linears(act='silu_mul') takes [gate_proj, up_proj] of equal out_features")
+        if first.out_features % 16 != 0:
+            raise ValueError(f"fuse_linears(act='silu_mul') needs out_features % 16 == 0, got {first.out_features}")
+    join = (lambda ts: _interleave16(ts[0], ts[1])) if act == "silu_mul" else (lambda ts: torch.cat(ts, dim=0))
+    weight = join([l._canonical() for l in layers])
+    scale = join([l.scale for l in layers])
     bias = None
     if any(l.bias is not None for l in layers):
         bdt = next(l.bias.dtype for l in layers if l.bias is not None)
-        bias = torch.cat([
+        bias = join([
             l.bias.detach().to(bdt) if l.bias is not None
             else torch.zeros(l.out_features, dtype=bdt, device=weight.device)
             for l in layers
@@ -492,7 +575,7 @@ def fuse_linears(layers: List[QuantizedLinear]) -> FusedQuantizedLinear:
     fused = QuantizedLinear.from_quantized(weight, scale, bias, quant_type=qt,
                                            in_features=first.in_features,
                                            group_size=first.group_size)
-    return FusedQuantizedLinear(fused, [l.out_features for l in layers])
+    return FusedQuantizedLinear(fused, [l.out_features for l in layers], act=act)
 
 
 # ---------------------------------------------------------------------------- W8A8

@@ -21,6 +21,7 @@ reference's behaviour (no code copied):
   act_quant_i8        quantization.py:411-414 per-token int8 activations
   w8a8_linear         quantization.py:404-447 Int8GEMMLinear's native path: int32 GEMM,
                       fp32 rescale, bias, one rounding to T (bit-exact target)
+  silu_mul            modeling_qwen2.py:48 F.silu(gate) * up on T-valued layer outputs
 
 How each part is pinned (tests/test_oracle.py):
   * round_bf16 / round_f16 against torch's dtype casts on every bf16 boundary case,
@@ -35,7 +36,9 @@ How each part is pinned (tests/test_oracle.py):
     even ties, zero rows per dtype), torch's CPU ops for the quantization given the scale,
     torch._int_mm plus torch's elementwise epilogue for the GEMM and rescale; the scale's
     device evaluation order (product with fp32 1/127) against torch on the GPU over every
-    bf16 / fp16 value and random fp32 (tests/test_gpu_w8a8.py).
+    bf16 / fp16 value and random fp32 (tests/test_gpu_w8a8.py);
+  * silu_mul against torch's CPU F.silu and product, and closed forms (silu(0) = 0,
+    large |g|).
 """
 
 from __future__ import annotations
@@ -263,3 +266,16 @@ def w8a8_linear(x, w_q, scale_w, bias=None, dt: str = BF16) -> np.ndarray:
     if bias is not None:
         out = (out + np.asarray(bias, dtype=np.float32).reshape(1, -1)).astype(np.float32)
     return round_to(out, dt)
+
+
+# ----------------------------------------------------------------------------- SiLU.mul
+
+
+def silu_mul(g, u, dt: str) -> np.ndarray:
+    """round_T(round_T(silu(g)) * u) for T-valued g, u (fp32 arrays): F.silu evaluates
+    g / (1 + exp(-g)) in fp32 and rounds to T, the product is one more fp32 product
+    rounded to T (modeling_qwen2.py:48)."""
+    g32 = np.asarray(g, dtype=np.float32)
+    with np.errstate(over="ignore"):
+        sg = round_to((g32 / (np.float32(1.0) + np.exp(-g32))).astype(np.float32), dt)
+    return round_to((sg * np.asarray(u, dtype=np.float32)).astype(np.float32), dt)

@@ -1,0 +1,89 @@
+"""GPU checks of the fused gate / up layer with the SiLU.mul epilogue
+(fuse_linears(..., act="silu_mul"); the MLP of modeling_qwen2.py:46-48).
+
+y = round_T(round_T(silu(g)) * u) with g, u the two layers' outputs. Against the oracle
+(oracle/quant_oracle.py silu_mul on the separate layers' outputs) to the 1e-2 contract
+(g and u come from a differently configured launch, so they can differ in the last
+place); the decode kernel's fused epilogue and the fallback (plain fused launch +
+lsq_silu_mul) bit-exact against each other.
+"""
+
+import numpy as np
+import pytest
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from localstrm_amd import QuantizedLinear, _lib, fuse_linears
+from oracle import quant_oracle as qo
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda:0")
+TDT = {"f16": torch.float16, "bf16": torch.bfloat16, "f32": torch.float32}
+
+
+def _say(msg):
+    print(msg, flush=True)
+
+
+def _pair(kind, n, k, group, seed):
+    torch.manual_seed(seed)
+    gate = QuantizedLinear.from_float(nn.Linear(k, n, bias=False), kind, group_size=group)
+    up = QuantizedLinear.from_float(nn.Linear(k, n, bias=True), kind, group_size=group)
+    return gate.to(DEV), up.to(DEV)
+
+
+CASES = [
+    ("int8", None, 4864, 896, 1), ("int8", None, 4864, 896, 16), ("int8", None, 4864, 896, 64),
+    ("int4", 128, 4864, 896, 1), ("int4", 128, 4864, 896, 33), ("int4", None, 272, 896, 5),
+    ("int8", None, 1024, 4864, 32),   # x does not fit LDS: fallback path
+    ("int4", 128, 1024, 1024, 200),   # prefill: fallback path
+    ("int8", None, 96, 128, 3),       # one workgroup, partial
+]
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+@pytest.mark.parametrize("kind,group,n,k,m", CASES)
+def test_silu_mul_fused_matches_separate_layers(dt, kind, group, n, k, m):
+    _say(f"silu_mul {kind} g={group} N={n} K={k} M={m} {dt}")
+    gate, up = _pair(kind, n, k, group, n + k + m)
+    fused = fuse_linears([gate, up], act="silu_mul")
+    x = (torch.randn(m, k, generator=torch.Generator().manual_seed(m)) * 0.5).to(TDT[dt]).to(DEV)
+    with torch.no_grad():
+        y = fused(x)
+        g, u = gate(x), up(x)
+        y2 = fused.fused(x)  # the plain interleaved output
+    assert y.shape == (m, n) and y.dtype == TDT[dt]
+    ref = qo.silu_mul(g.float().cpu().numpy(), u.float().cpu().numpy(), dt)
+    err = qo.rel_err(y.float().cpu().numpy(), ref)
+    _say(f"  rel_err={err:.2e}")
+    assert err <= 1e-2
+    # fallback on the same interleaved output: bit-exact with the fused epilogue
+    yb = torch.empty_like(y)
+    _lib.check(_lib.load().lsq_silu_mul(y2.data_ptr(), 2 * n, yb.data_ptr(), n, _lib.dtype_code(x.dtype),
+                                        m, n, _lib.stream_handle(DEV)), "lsq_silu_mul")
+    torch.cuda.synchronize()
+    assert torch.equal(yb.view(torch.int16), y.view(torch.int16))
+    # torch's own ops on the de-interleaved halves
+    t = y2.reshape(m, n // 16, 2, 16)
+    tref = F.silu(t[:, :, 0, :].reshape(m, n)) * t[:, :, 1, :].reshape(m, n)
+    assert qo.rel_err(y.float().cpu().numpy(), tref.float().cpu().numpy()) <= 1e-2
+
+
+def test_silu_mul_f32_and_autograd():
+    _say("silu_mul fp32 and autograd")
+    gate, up = _pair("int8", 64, 128, None, 3)
+    fused = fuse_linears([gate, up], act="silu_mul")
+    x = torch.randn(2, 3, 128, device=DEV)
+    with torch.no_grad():
+        y = fused(x)
+        ref = qo.silu_mul(gate(x).cpu().numpy(), up(x).cpu().numpy(), "f32")
+    assert y.shape == (2, 3, 64)
+    assert qo.rel_err(y.cpu().numpy(), ref) <= 1e-5
+    xg = torch.randn(4, 128, device=DEV, dtype=torch.bfloat16, requires_grad=True)
+    yg = fused(xg)
+    yg.float().sum().backward()
+    assert xg.grad is not None and xg.grad.shape == xg.shape
+    with torch.no_grad():
+        assert qo.rel_err(yg.float().cpu().numpy(), fused(xg).float().cpu().numpy()) <= 1e-2

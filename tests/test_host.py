@@ -375,6 +375,28 @@ def test_library_rejects_bad_arguments_without_gpu():
         _lib.check(-4, "probe")
 
 
+def test_fuse_linears_silu_mul_interleaves_gate_and_up():
+    from localstrm_amd import fuse_linears
+
+    gate = QuantizedLinear.from_float(_linear(48, 64, 11, bias=False), "int8")
+    up = QuantizedLinear.from_float(_linear(48, 64, 12, bias=True), "int8")
+    f = fuse_linears([gate, up], act="silu_mul")
+    assert f.out_features == 48 and f.fused.out_features == 96 and f.act == "silu_mul"
+    w = f.fused.weight_q
+    for t in range(3):
+        assert torch.equal(w[32 * t:32 * t + 16], gate.weight_q[16 * t:16 * t + 16])
+        assert torch.equal(w[32 * t + 16:32 * t + 32], up.weight_q[16 * t:16 * t + 16])
+    assert torch.equal(f.fused.bias.detach()[16:32], up.bias.detach()[:16])
+    assert (f.fused.bias.detach()[:16] == 0).all()
+    with pytest.raises(ValueError, match="gate_proj, up_proj"):
+        fuse_linears([gate, up, up], act="silu_mul")
+    odd = QuantizedLinear.from_float(_linear(40, 64, 13), "int8")
+    with pytest.raises(ValueError, match="% 16"):
+        fuse_linears([odd, odd], act="silu_mul")
+    with pytest.raises(ValueError, match="act"):
+        fuse_linears([gate, up], act="gelu")
+
+
 def test_fuse_linears_concatenates_and_validates():
     """fuse_linears builds one layer whose rows are the layers' rows in order (CPU side:
     construction only, no kernel call)."""

@@ -352,3 +352,29 @@ def test_w8a8_linear_closed_form():
     y = qo.w8a8_linear(x, w, np.full(k, 0.5, np.float32), qo.round_bf16(b), "bf16")
     xq = np.rint(x).clip(-128, 127)
     np.testing.assert_array_equal(y, qo.round_bf16(xq * 1.5 + qo.round_bf16(b)))
+
+
+# ----------------------------------------------------------------------------- SiLU.mul
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16", "f32"])
+def test_silu_mul_matches_torch_ops(dt):
+    rng = np.random.default_rng(8)
+    g = qo.round_to(rng.standard_normal(20000).astype(np.float32) * 4, dt)
+    u = qo.round_to(rng.standard_normal(20000).astype(np.float32) * 2, dt)
+    ours = qo.silu_mul(g, u, dt)
+    gt = torch.from_numpy(g).to(TORCH_DT[dt])
+    ut = torch.from_numpy(u).to(TORCH_DT[dt])
+    ref = (F.silu(gt) * ut).float().numpy()
+    # exp is correctly rounded in neither library: a rare last-place difference in fp32 may
+    # move a T rounding; everything else is the same op order
+    rel = np.abs(ours - ref) / np.maximum(np.abs(ref), 1e-6)
+    if dt == "f32":
+        assert np.max(rel) < 2.0 ** -20  # a few fp32 ulps
+    else:
+        assert np.mean(ours == ref) > 0.999
+        assert np.max(rel) < 2.0 ** -7   # at most one ulp of T
+    # closed forms: silu(0) = 0, silu(g) -> g for large g, -> -0 for very negative g
+    assert qo.silu_mul(np.float32([0.0]), np.float32([3.0]), dt)[0] == 0.0
+    assert qo.silu_mul(np.float32([60.0]), np.float32([0.5]), dt)[0] == 30.0
+    assert qo.silu_mul(np.float32([-200.0]), np.float32([1.0]), dt)[0] == 0.0
