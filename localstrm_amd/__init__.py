@@ -4,6 +4,7 @@ Drop-in for LocalStrm's src/kernels/quantization.py hot path; the compute runs i
 gfx950 HIP kernels of liblsq.so (built by `python -m localstrm_amd.build`).
 """
 
+from .checkpoint import load_packed, save_packed  # noqa: F401
 from .quantization import (  # noqa: F401
     VALID_MODES,
     CachedQuantizedLinear,
@@ -29,5 +30,7 @@ __all__ = [
     "format_bytes",
     "fuse_linears",
     "load_and_quantize_model",
+    "load_packed",
     "pack_int4",
+    "save_packed",
 ]

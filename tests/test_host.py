@@ -421,3 +421,50 @@ def test_fuse_linears_concatenates_and_validates():
         fuse_linears([q, w8[0]])
     with pytest.raises(ValueError):
         fuse_linears([])
+
+
+# ----------------------------------------------------------------------------- packed checkpoints
+
+
+@pytest.mark.parametrize("mode,group", [("int8", None), ("int4", None), ("int4", 32), ("hybrid_int8", None)])
+def test_packed_checkpoint_round_trip_cpu(tmp_path, mode, group):
+    from localstrm_amd import load_packed, save_packed
+
+    model = seeded_model()
+    apply_optional_quantization(model, quant_type=mode, group_size=group)
+    path = str(tmp_path / "packed.safetensors")
+    n = save_packed(model, path)
+    assert n == 2 * 7
+    fresh = seeded_model(seed=7)  # float skeleton with other weights
+    assert load_packed(fresh, path) == n
+    sd_a, sd_b = model.state_dict(), fresh.state_dict()
+    quant_keys = [k for k in sd_a if ".self_attn." in k or ".mlp." in k]
+    for k in quant_keys:
+        assert sd_a[k].dtype == sd_b[k].dtype and torch.equal(sd_a[k], sd_b[k]), k
+    for la, lb in zip(model.model.layers, fresh.model.layers):
+        for p in PROJS:
+            assert type(getattr(la.self_attn, p)) is type(getattr(lb.self_attn, p))
+        for p in MLPS:
+            a, b = getattr(la.mlp, p), getattr(lb.mlp, p)
+            assert type(a) is type(b)
+            if isinstance(a, QuantizedLinear):
+                assert (a.quant_type, a.group_size) == (b.quant_type, b.group_size)
+
+
+def test_packed_checkpoint_rejects_foreign_files(tmp_path):
+    from safetensors.torch import save_file
+
+    from localstrm_amd import load_packed, save_packed
+
+    path = str(tmp_path / "other.safetensors")
+    save_file({"a": torch.zeros(2)}, path, metadata={"format": "something-else"})
+    with pytest.raises(ValueError, match="not a localstrm_amd.packed file"):
+        load_packed(seeded_model(), path)
+    with pytest.raises(ValueError, match="no quantized layers"):
+        save_packed(seeded_model(), str(tmp_path / "none.safetensors"))
+    model = seeded_model()
+    apply_optional_quantization(model, quant_type="int8")
+    good = str(tmp_path / "good.safetensors")
+    save_packed(model, good)
+    with pytest.raises(ValueError, match="no module named"):
+        load_packed(nn.Sequential(nn.Linear(4, 4)), good)
