@@ -336,6 +336,70 @@ def bench_mlp(steps: int, warmup: int, device, m: int = 32, n_layers: int = 24, 
     }
 
 
+def bench_paged(steps: int, warmup: int, device, b: int = 32, h: int = 14, hkv: int = 2, d: int = 64,
+                seq: int = 2048, bs: int = 16, n_layers: int = 24, int8: bool = True):
+    """Paged attention of one decode step over n_layers layers (each with its own KV pool),
+    batch b at context seq: Qwen2.5-0.5B attention shapes (14 query / 2 KV heads, head 64),
+    INT8 KV with fp16 per-token scales (the reference's kv_cache_dtype 'int8'), scattered
+    blocks of 16 tokens. Bytes = K + V + scales + q + out."""
+    from localstrm_amd import paged_attention_decode
+
+    g = _gen(3)
+    nblk = -(-seq // bs)
+    nb = b * nblk
+    pools = []
+    for _ in range(n_layers):
+        if int8:
+            kp = torch.randint(-128, 128, (nb, bs, hkv, d), generator=g, dtype=torch.int8).to(device)
+            vp = torch.randint(-128, 128, (nb, bs, hkv, d), generator=g, dtype=torch.int8).to(device)
+            ks = (torch.rand(nb, bs, hkv, 1, generator=g) * 0.02 + 0.002).half().to(device)
+            vs = (torch.rand(nb, bs, hkv, 1, generator=g) * 0.02 + 0.002).half().to(device)
+        else:
+            kp = torch.randn(nb, bs, hkv, d, generator=g).half().to(device)
+            vp = torch.randn(nb, bs, hkv, d, generator=g).half().to(device)
+            ks = vs = None
+        pools.append((kp, vp, ks, vs))
+    bt = torch.randperm(nb, generator=g).reshape(b, nblk).to(device)
+    sl = torch.full((b,), seq, dtype=torch.int64, device=device)
+    q = torch.randn(b, h, 1, d, generator=g).half().to(device)
+    esz = 1 if int8 else 2
+    per_step = n_layers * (2 * b * seq * hkv * d * esz + (2 * b * seq * hkv * 2 if int8 else 0)
+                           + 2 * b * h * d * 2)
+    stream = torch.cuda.Stream()
+    with torch.no_grad():
+        def run():
+            for kp, vp, ks, vs in pools:
+                paged_attention_decode(q, kp, vp, bt, sl, bs, ks, vs, max_sl=seq)
+        for _ in range(max(warmup, 1)):
+            run()
+        torch.cuda.synchronize()
+        stream.wait_stream(torch.cuda.current_stream())
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(stream):
+            with torch.cuda.graph(graph, stream=stream):
+                for _ in range(steps):
+                    run()
+        graph.replay()
+        torch.cuda.synchronize()
+        start = torch.cuda.Event(enable_timing=True)
+        stop = torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(stream):
+            start.record(stream)
+            graph.replay()
+            stop.record(stream)
+        stop.synchronize()
+        del graph
+    ms = start.elapsed_time(stop) / steps
+    del pools
+    torch.cuda.empty_cache()
+    return {
+        "kind": "paged attention" + (" int8 kv" if int8 else " fp16 kv"), "B": b, "H": h, "Hkv": hkv,
+        "D": d, "seq": seq, "layers": n_layers, "us_per_call": ms * 1e3,
+        "us_per_layer": ms * 1e3 / n_layers, "GB_s": per_step / (ms * 1e-3) / 1e9,
+        "bytes": per_step, "frac_hbm": per_step / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+    }
+
+
 # ----------------------------------------------------------------------------- CPU baseline
 
 
@@ -410,6 +474,15 @@ def main() -> int:
         print(json.dumps(bench_stack(max(2, args.steps), args.warmup, device,
                                      fused=args.case == "stack-fused")), flush=True)
         return 0
+    if args.case and args.case.startswith("paged"):
+        # paged[,B,seq[,fp16]]: Qwen2.5-0.5B attention shapes, 24 layers
+        parts = args.case.split(",")
+        bsz = int(parts[1]) if len(parts) > 1 else 32
+        seq = int(parts[2]) if len(parts) > 2 else 2048
+        int8 = not (len(parts) > 3 and parts[3] == "fp16")
+        print(json.dumps(bench_paged(max(2, args.steps), args.warmup, device, b=bsz, seq=seq,
+                                     int8=int8)), flush=True)
+        return 0
     if args.case in ("mlp", "mlp-fused"):
         print(json.dumps(bench_mlp(max(2, args.steps), args.warmup, device,
                                    fused=args.case == "mlp-fused")), flush=True)
@@ -440,6 +513,7 @@ def main() -> int:
         sweep.append(bench_stack(max(5, args.steps // 20), 2, device, fused=True))
         sweep.append(bench_mlp(max(5, args.steps // 20), 2, device))
         sweep.append(bench_mlp(max(5, args.steps // 20), 2, device, fused=True))
+        sweep.append(bench_paged(max(5, args.steps // 20), 2, device))
     cpu = None if args.no_cpu else cpu_baseline(N, K, M)
 
     ms = head["us_per_call"] / 1e3

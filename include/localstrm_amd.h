@@ -34,6 +34,7 @@ extern "C" {
 #define LSQ_F32 0
 #define LSQ_F16 1
 #define LSQ_BF16 2
+#define LSQ_I8 3               /* KV cache entries only (lsq_paged_attention_decode) */
 
 /* epilogues of lsq_w8_linear_act / lsq_w4_linear_act */
 #define LSQ_ACT_NONE 0
@@ -189,6 +190,32 @@ int lsq_w8a8_linear(const void* x, int64_t ldx, const int8_t* tiled, const void*
                     int scale_w_dtype, const void* bias, int bias_dtype, void* y, int64_t ldy,
                     int dtype, int64_t M, int64_t N, int64_t K, int8_t* x_q, float* scale_x,
                     void* stream);
+
+/* ---- Paged attention for one decode step (INT8 or T-typed KV cache) ----
+ * Replaces paged_attention_decode (src/kernels/paged_attention.py:33-173) for a query of
+ * one token per sequence: query [B, H, D] (the reference's [B, H, 1, D]), k_pool / v_pool
+ * [num_blocks, block_size, Hkv, D] of kv_dtype (LSQ_I8 with k_scales / v_scales
+ * [num_blocks, block_size, Hkv] of scale_dtype, or the query's dtype with NULL scales),
+ * block_tables int64 [B, >= ceil(max_seq_len / block_size)] (row stride bt_stride),
+ * seq_lens int64 [B]. A token t of sequence b attends when t < max_seq_len and, without a
+ * mask, t < seq_lens[b]; with a mask (bool bytes, row stride mask_stride, one row per
+ * sequence or, mask_rows_per_b = Hkv, one per (sequence, KV head) as the reference's
+ * repeat_interleave'd mask), when mask[row][t]. head_mapping 0: query head h uses KV head
+ * h / (H / Hkv) ("contiguous"); 1: h % Hkv ("interleaved"). Keys / values are dequantized
+ * as round_T(k * scale) (the reference's keys.to(T) * k_scales), scores scaled by
+ * 1 / sqrt(D), softmax and the value sum in fp32, out [B, H, D] rounded once to T.
+ * H / Hkv <= 16, D in {64, 128} (an fp32 cache: 64), num_blocks * block_size * Hkv < 2^31.
+ * workspace: lsq_paged_attention_workspace_bytes(...)
+ * bytes of device memory (0 when max_seq_len <= 256; then it may be NULL). */
+int64_t lsq_paged_attention_workspace_bytes(int64_t B, int64_t H, int64_t D, int64_t max_seq_len);
+int lsq_paged_attention_decode(const void* query, const void* k_pool, const void* v_pool,
+                               int kv_dtype, const void* k_scales, const void* v_scales,
+                               int scale_dtype, const int64_t* block_tables, int64_t bt_stride,
+                               const int64_t* seq_lens, const uint8_t* mask, int64_t mask_stride,
+                               int64_t mask_rows_per_b, void* out, int dtype, int64_t B,
+                               int64_t H, int64_t Hkv, int64_t D, int64_t block_size,
+                               int64_t max_seq_len, int head_mapping, void* workspace,
+                               int64_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

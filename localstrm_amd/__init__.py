@@ -5,6 +5,7 @@ gfx950 HIP kernels of liblsq.so (built by `python -m localstrm_amd.build`).
 """
 
 from .checkpoint import load_packed, save_packed  # noqa: F401
+from .paged_attention import paged_attention_decode  # noqa: F401
 from .quantization import (  # noqa: F401
     VALID_MODES,
     CachedQuantizedLinear,
@@ -32,5 +33,6 @@ __all__ = [
     "load_and_quantize_model",
     "load_packed",
     "pack_int4",
+    "paged_attention_decode",
     "save_packed",
 ]

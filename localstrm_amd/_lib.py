@@ -15,7 +15,7 @@ import torch
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "liblsq.so")
 
-F32, F16, BF16 = 0, 1, 2
+F32, F16, BF16, I8 = 0, 1, 2, 3
 ACT_NONE, ACT_SILU_MUL = 0, 1
 DTYPE_CODE = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
 
@@ -54,6 +54,12 @@ SIGNATURES = {
          _vp],
     ),
     "lsq_silu_mul": (_int, [_vp, _i64, _vp, _i64, _int, _i64, _i64, _vp]),
+    "lsq_paged_attention_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64]),
+    "lsq_paged_attention_decode": (
+        _int,
+        [_vp, _vp, _vp, _int, _vp, _vp, _int, _vp, _i64, _vp, _vp, _i64, _i64, _vp, _int, _i64,
+         _i64, _i64, _i64, _i64, _i64, _int, _vp, _i64, _vp],
+    ),
     "lsq_w8a8_tiled_bytes": (_i64, [_i64, _i64]),
     "lsq_w8a8_retile": (_int, [_vp, _vp, _i64, _i64, _vp]),
     "lsq_w8a8_untile": (_int, [_vp, _vp, _i64, _i64, _vp]),

@@ -99,8 +99,10 @@ __device__ __forceinline__ float dequant_elem(int q, float s_T) {
 // can multiply (or FMA) and round straight to fp16 / bf16 in one instruction (v_fma_mix),
 // which rounds once where the separate fp32 operation and conversion round twice. Code
 // that must round like an fp32 result converted to T passes the fp32 value through here.
+// (Not volatile: a volatile asm would also pin the surrounding memory operations in
+// place, serializing loads around every use.)
 __device__ __forceinline__ float opaque(float x) {
-  __asm__ volatile("" : "+v"(x));
+  __asm__("" : "+v"(x));
   return x;
 }
 

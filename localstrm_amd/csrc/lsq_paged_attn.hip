@@ -1,0 +1,369 @@
+// Paged attention for one decode step, with an INT8 or T-typed KV cache (gfx950).
+//
+// GPU form of paged_attention_decode (src/kernels/paged_attention.py:33-173): one query
+// token per sequence attends to its cached keys / values, which live in fixed-size blocks
+// of a shared pool found through the sequence's block table. The reference gathers every
+// block into a contiguous copy, dequantizes it (keys.to(T) * scales), expands the GQA
+// heads and calls F.scaled_dot_product_attention. Here nothing is copied:
+//
+//  * paged_attn_split_kernel: one workgroup per (sequence, KV head, split of 256 tokens);
+//    thread t takes token t of the split: it walks the block table to the token's row,
+//    dequantizes its key (round_T(k * scale)) and forms the scores of all G query heads
+//    that share this KV head (q of the G heads in LDS); softmax statistics per head over
+//    the split; then lane d of each wave accumulates p * v for 64 of the split's tokens
+//    (value rows read coalesced, one row per token), the four waves' partials added in
+//    LDS. One split writes the normalized output; several write (max, sum, partial
+//    output) to the caller's workspace;
+//  * paged_attn_combine_kernel: rescales and adds the splits of each (sequence, head).
+// HBM-bound: every key / value byte (plus its scale) is read once per step.
+//
+// Numerics: scores and softmax in fp32 with the SDPA default scale 1 / sqrt(D), the
+// value sum in fp32, one rounding to T at the end; keys and values are the T-valued
+// dequantized entries, as the reference feeds them to SDPA.
+
+#include "lsq_common.h"
+
+#include <cmath>
+#include <cstdint>
+
+namespace lsq {
+namespace {
+
+constexpr int kPaNT = 256;   // threads per workgroup = tokens per split
+constexpr int kPaMaxG = 16;  // query heads per KV head
+
+struct PagedArgs {
+  const void* q;          // [B, H, D] (dtype DT)
+  const void* kp;         // [NB, BS, Hkv, D] int8 or DT
+  const void* vp;
+  const void* ks;         // [NB, BS, Hkv] scales (int8 cache only)
+  const void* vs;
+  int scale_dt;
+  const int64_t* bt;      // block tables, row stride ldbt
+  int64_t ldbt;
+  const int64_t* sl;      // sequence lengths [B]
+  const uint8_t* mask;    // optional boolean mask rows (row stride ldm), else sl decides
+  int64_t ldm;
+  int mask_rows_per_b;    // 1 or Hkv (a mask repeated per KV head)
+  void* out;              // [B, H, D] (dtype DT)
+  float* ws;              // [B, H, nsplit, D + 2] partials when nsplit > 1
+  int B, H, Hkv, G, BS, nsplit, max_sl, interleaved;
+  float sm_scale;
+};
+
+// Dequantized key / value element e of a 16-byte chunk (int8: 16 elements, T: 8), as T.
+template <int DT, bool I8>
+__device__ __forceinline__ float kv_elem(u32x4 v, int e, float s) {
+  if constexpr (I8) {
+    const int q = static_cast<int8_t>(v[e >> 2] >> (8 * (e & 3)));
+    return Act<DT>::round(opaque(static_cast<float>(q) * s));
+  } else if constexpr (DT == LSQ_F32) {
+    return __uint_as_float(v[e]);
+  } else {
+    return Act<DT>::to_f32(static_cast<uint16_t>(v[e >> 1] >> (16 * (e & 1))));
+  }
+}
+
+// Max / sum of a float over each row of 16 lanes, in every lane of the row (DPP).
+__device__ __forceinline__ float dpp_f(float v, int ctrl) {
+  switch (ctrl) {
+    case 0: return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
+    case 1: return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
+    case 2: return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false));
+    default: return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false));
+  }
+}
+__device__ __forceinline__ float row16_max(float v) {
+#pragma unroll
+  for (int c = 0; c < 4; ++c) v = fmaxf(v, dpp_f(v, c));
+  return v;
+}
+__device__ __forceinline__ float row16_sum(float v) {
+#pragma unroll
+  for (int c = 0; c < 4; ++c) v += dpp_f(v, c);
+  return v;
+}
+
+template <int DT, bool I8, int D>
+__global__ void __launch_bounds__(kPaNT) paged_attn_split_kernel(PagedArgs p) {
+  using S = typename Act<DT>::storage;
+  constexpr int ESZ = I8 ? 1 : static_cast<int>(sizeof(S));  // bytes per cache element
+  constexpr int EPC = 16 / ESZ;                              // elements per 16-byte chunk
+  constexpr int kVtLd = kPaNT + 16;                          // transposed tile row (bytes)
+  __shared__ __align__(16) float qs[kPaMaxG * D];
+  __shared__ __align__(16) float sp[kPaMaxG * kPaNT];
+  __shared__ float stat[2 * kPaMaxG];  // per head: max, sum
+  __shared__ __align__(16) float vsc[kPaNT];
+  __shared__ __align__(16) unsigned char tile[D * kVtLd * ESZ];  // values, vt[d][token]
+  __shared__ __align__(16) float accs[4 * kPaMaxG * D];           // per-wave partial outputs
+
+  const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int G = p.G;
+  auto head = [&](int g) { return p.interleaved ? g * p.Hkv + kvh : kvh * G + g; };
+  const S* q = static_cast<const S*>(p.q);
+  for (int i = tid; i < G * D; i += kPaNT) {
+    const int g = i / D, d = i - (i / D) * D;
+    qs[i] = Act<DT>::to_f32(q[(static_cast<int64_t>(b) * p.H + head(g)) * D + d]);
+  }
+  const int seq = static_cast<int>(p.sl[b]);
+  auto valid_tok = [&](int t) -> bool {
+    if (t >= p.max_sl) return false;
+    if (p.mask) {
+      const int row = b * p.mask_rows_per_b + (p.mask_rows_per_b > 1 ? kvh : 0);
+      return p.mask[static_cast<int64_t>(row) * p.ldm + t] != 0;
+    }
+    return t < seq;
+  };
+
+  // ---- this thread's token: pool row (-1: masked), key and value rows. Loads are
+  // unconditional (a masked token reads row 0, its results are discarded) so that they
+  // are all in flight together.
+  const int t0 = split * kPaNT;
+  const int t = t0 + tid;
+  const bool valid = valid_tok(t);
+  int my_row = -1;
+  if (valid) {
+    const int64_t blk = p.bt[static_cast<int64_t>(b) * p.ldbt + t / p.BS];
+    my_row = static_cast<int>((blk * p.BS + t % p.BS) * p.Hkv + kvh);
+  }
+  const int64_t lrow = my_row < 0 ? 0 : my_row;
+  const float ks = I8 ? load_as_f32(p.ks, p.scale_dt, lrow) : 1.f;
+  const float vs = I8 ? load_as_f32(p.vs, p.scale_dt, lrow) : 1.f;
+  u32x4 kraw[D / EPC], vraw[D / EPC];
+  {
+    const unsigned char* kr = static_cast<const unsigned char*>(p.kp) + lrow * D * ESZ;
+    const unsigned char* vr = static_cast<const unsigned char*>(p.vp) + lrow * D * ESZ;
+#pragma unroll
+    for (int c = 0; c < D / EPC; ++c) kraw[c] = *reinterpret_cast<const u32x4*>(kr + c * 16);
+#pragma unroll
+    for (int c = 0; c < D / EPC; ++c) vraw[c] = *reinterpret_cast<const u32x4*>(vr + c * 16);
+  }
+  // value row -> transposed tile (elements as stored), scale (0 for a masked token)
+#pragma unroll
+  for (int c = 0; c < D / EPC; ++c)
+#pragma unroll
+    for (int e = 0; e < EPC; ++e) {
+      const int d = c * EPC + e;
+      if constexpr (I8)
+        tile[d * kVtLd + tid] = static_cast<unsigned char>(vraw[c][e >> 2] >> (8 * (e & 3)));
+      else if constexpr (ESZ == 4)
+        reinterpret_cast<uint32_t*>(tile)[d * kVtLd + tid] = vraw[c][e];
+      else
+        reinterpret_cast<uint16_t*>(tile)[d * kVtLd + tid] =
+            static_cast<uint16_t>(vraw[c][e >> 1] >> (16 * (e & 1)));
+    }
+  vsc[tid] = my_row < 0 ? 0.f : vs;
+  __syncthreads();
+
+  // ---- scores: the key, dequantized once to T-valued floats, against each head's q
+  constexpr float kNegInf = -__builtin_huge_valf();
+#pragma unroll
+  for (int h0 = 0; h0 < D; h0 += 64) {  // 64 dimensions at a time (registers)
+    float kf[64];
+#pragma unroll
+    for (int e = 0; e < 64; ++e) {
+      const int d = h0 + e;
+      const u32x4 w = kraw[d / EPC];
+      const int ee = d % EPC;
+      if constexpr (I8) {
+        const int qv = static_cast<int8_t>(w[ee >> 2] >> (8 * (ee & 3)));
+        kf[e] = Act<DT>::round(opaque(static_cast<float>(qv) * ks));
+      } else if constexpr (DT == LSQ_F32) {
+        kf[e] = __uint_as_float(w[ee]);
+      } else {
+        kf[e] = Act<DT>::to_f32(static_cast<uint16_t>(w[ee >> 1] >> (16 * (ee & 1))));
+      }
+    }
+    for (int g = 0; g < G; ++g) {
+      float dot = 0.f;
+#pragma unroll
+      for (int e = 0; e < 64; e += 4) {
+        const f32x4 qv = *reinterpret_cast<const f32x4*>(&qs[g * D + h0 + e]);
+        dot = fmaf(qv[0], kf[e], fmaf(qv[1], kf[e + 1], fmaf(qv[2], kf[e + 2], fmaf(qv[3], kf[e + 3], dot))));
+      }
+      float* dst = &sp[g * kPaNT + tid];
+      if (h0 + 64 < D) *dst = (h0 == 0 ? 0.f : *dst) + dot;
+      else *dst = valid ? ((h0 == 0 ? 0.f : *dst) + dot) * p.sm_scale : kNegInf;
+    }
+  }
+
+  // ---- softmax statistics per head over the split: thread (g = tid / 16, part = tid % 16)
+  // reduces 16 of head g's 256 scores from LDS, then the 16 parts by DPP within a row
+  __syncthreads();
+  const int hg = tid >> 4, part = tid & 15;
+  if (hg < G) {
+    float m = kNegInf;
+#pragma unroll
+    for (int e = 0; e < 16; e += 4) {
+      const f32x4 v = *reinterpret_cast<const f32x4*>(&sp[hg * kPaNT + part * 16 + e]);
+      m = fmaxf(fmaxf(m, fmaxf(v[0], v[1])), fmaxf(v[2], v[3]));
+    }
+    m = row16_max(m);
+    if (part == 0) stat[hg] = m;
+  }
+  __syncthreads();
+  for (int g = 0; g < G; ++g) {
+    const float sv = sp[g * kPaNT + tid];
+    sp[g * kPaNT + tid] = sv == kNegInf ? 0.f : __expf(sv - stat[g]);  // all masked: m = -inf
+  }
+  __syncthreads();
+  if (hg < G) {
+    float l = 0.f;
+#pragma unroll
+    for (int e = 0; e < 16; e += 4) {
+      const f32x4 v = *reinterpret_cast<const f32x4*>(&sp[hg * kPaNT + part * 16 + e]);
+      l += (v[0] + v[1]) + (v[2] + v[3]);
+    }
+    l = row16_sum(l);
+    if (part == 0) stat[kPaMaxG + hg] = l;
+  }
+
+  // ---- p * v: wave w takes tokens [64 w, 64 w + 64), lane d (then d + 64) one dimension;
+  // the 64 values of the lane's dimension come from the transposed tile, 16 bytes a read
+  const int tw = wid * 64;
+#pragma unroll
+  for (int j = 0; j < D / 64; ++j) {
+    const int d = lane + 64 * j;
+    float vv[64];
+#pragma unroll
+    for (int c = 0; c < 64 * ESZ / 16; ++c) {
+      const u32x4 w = *reinterpret_cast<const u32x4*>(&tile[(d * kVtLd + tw) * ESZ + c * 16]);
+#pragma unroll
+      for (int e = 0; e < 16 / ESZ; ++e) {
+        const int tt = c * (16 / ESZ) + e;
+        float v;
+        if constexpr (I8) {
+          const int qv = static_cast<int8_t>(w[e >> 2] >> (8 * (e & 3)));
+          v = Act<DT>::round(opaque(static_cast<float>(qv) * vsc[tw + tt]));
+        } else if constexpr (DT == LSQ_F32) {
+          v = __uint_as_float(w[e]);  // (fp32 caches are staged 4 bytes an element)
+        } else {
+          v = Act<DT>::to_f32(static_cast<uint16_t>(w[e >> 1] >> (16 * (e & 1))));
+        }
+        vv[tt] = vsc[tw + tt] == 0.f ? 0.f : v;  // masked token: its row may hold anything
+      }
+    }
+    for (int g = 0; g < G; ++g) {
+      float a = 0.f;
+#pragma unroll
+      for (int e = 0; e < 64; e += 4) {
+        const f32x4 pg = *reinterpret_cast<const f32x4*>(&sp[g * kPaNT + tw + e]);
+        a = fmaf(pg[0], vv[e], fmaf(pg[1], vv[e + 1], fmaf(pg[2], vv[e + 2], fmaf(pg[3], vv[e + 3], a))));
+      }
+      accs[(wid * kPaMaxG + g) * D + d] = a;
+    }
+  }
+  __syncthreads();
+
+  for (int i = tid; i < G * D; i += kPaNT) {
+    const int g = i / D, d = i - (i / D) * D;
+    const float a = (accs[(0 * kPaMaxG + g) * D + d] + accs[(1 * kPaMaxG + g) * D + d]) +
+                    (accs[(2 * kPaMaxG + g) * D + d] + accs[(3 * kPaMaxG + g) * D + d]);
+    const float m = stat[g], l = stat[kPaMaxG + g];
+    const int64_t oh = static_cast<int64_t>(b) * p.H + head(g);
+    if (p.nsplit == 1) {
+      static_cast<S*>(p.out)[oh * D + d] = Act<DT>::from_f32(opaque(a / l));
+    } else {
+      float* w = p.ws + (oh * p.nsplit + split) * (D + 2);
+      if (d == 0) { w[0] = m; w[1] = l; }
+      w[2 + d] = a;
+    }
+  }
+}
+
+// One workgroup of D threads per (sequence, head): out = sum_s e^(m_s - M) acc_s /
+// sum_s e^(m_s - M) l_s over the splits. (A ticket in the split kernel would save this
+// launch, but the device-scope release / acquire it needs writes back and invalidates
+// each XCD's L2 per workgroup, which measured 3.5 x slower.)
+template <int DT, int D>
+__global__ void __launch_bounds__(D) paged_attn_combine_kernel(PagedArgs p) {
+  using S = typename Act<DT>::storage;
+  const int64_t oh = blockIdx.x;
+  const int d = threadIdx.x;
+  const float* w = p.ws + oh * p.nsplit * (D + 2);
+  constexpr float kNegInf = -__builtin_huge_valf();
+  float M = kNegInf;
+  for (int s = 0; s < p.nsplit; ++s) M = fmaxf(M, w[s * (D + 2)]);
+  float a = 0.f, l = 0.f;
+  for (int s = 0; s < p.nsplit; ++s) {
+    const float ms = w[s * (D + 2)];
+    const float f = ms == kNegInf ? 0.f : __expf(ms - M);
+    l = fmaf(f, w[s * (D + 2) + 1], l);
+    a = fmaf(f, w[s * (D + 2) + 2 + d], a);
+  }
+  static_cast<S*>(p.out)[oh * D + d] = Act<DT>::from_f32(opaque(a / l));
+}
+
+template <int DT, bool I8, int D>
+int launch_paged(const PagedArgs& a, hipStream_t s) {
+  const dim3 grid(static_cast<unsigned>(a.nsplit), static_cast<unsigned>(a.Hkv), static_cast<unsigned>(a.B));
+  paged_attn_split_kernel<DT, I8, D><<<grid, dim3(kPaNT), 0, s>>>(a);
+  if (a.nsplit > 1)
+    paged_attn_combine_kernel<DT, D><<<dim3(static_cast<unsigned>(a.B * a.H)), dim3(D), 0, s>>>(a);
+  return static_cast<int>(hipGetLastError());
+}
+
+template <int DT>
+int launch_paged_dt(const PagedArgs& a, bool i8, int D, hipStream_t s) {
+  if (D == 64) return i8 ? launch_paged<DT, true, 64>(a, s) : launch_paged<DT, false, 64>(a, s);
+  if constexpr (DT == LSQ_F32) {  // an fp32 value tile of 256 x 128 does not fit in LDS
+    if (!i8) return LSQ_E_SHAPE;
+    return launch_paged<DT, true, 128>(a, s);
+  } else {
+    return i8 ? launch_paged<DT, true, 128>(a, s) : launch_paged<DT, false, 128>(a, s);
+  }
+}
+
+}  // namespace
+}  // namespace lsq
+
+using namespace lsq;
+
+extern "C" int64_t lsq_paged_attention_workspace_bytes(int64_t B, int64_t H, int64_t D, int64_t max_seq_len) {
+  if (B <= 0 || H <= 0 || D <= 0 || max_seq_len <= 0) return 0;
+  const int64_t nsplit = (max_seq_len + kPaNT - 1) / kPaNT;
+  return nsplit > 1 ? B * H * nsplit * (D + 2) * static_cast<int64_t>(sizeof(float)) : 0;
+}
+
+extern "C" int lsq_paged_attention_decode(
+    const void* query, const void* k_pool, const void* v_pool, int kv_dtype, const void* k_scales,
+    const void* v_scales, int scale_dtype, const int64_t* block_tables, int64_t bt_stride,
+    const int64_t* seq_lens, const uint8_t* mask, int64_t mask_stride, int64_t mask_rows_per_b,
+    void* out, int dtype, int64_t B, int64_t H, int64_t Hkv, int64_t D, int64_t block_size,
+    int64_t max_seq_len, int head_mapping, void* workspace, int64_t workspace_bytes, void* stream) {
+  const bool dt_ok = dtype == LSQ_F32 || dtype == LSQ_F16 || dtype == LSQ_BF16;
+  const bool i8 = kv_dtype == LSQ_I8;
+  if (!dt_ok || (!i8 && kv_dtype != dtype)) return LSQ_E_DTYPE;
+  if (i8 && scale_dtype != LSQ_F32 && scale_dtype != LSQ_F16 && scale_dtype != LSQ_BF16) return LSQ_E_DTYPE;
+  if (B < 0 || H < 1 || Hkv < 1 || H % Hkv != 0 || H / Hkv > kPaMaxG || (D != 64 && D != 128) ||
+      block_size < 1 || max_seq_len < 0 || bt_stride < (max_seq_len + block_size - 1) / block_size)
+    return LSQ_E_SHAPE;
+  if (mask && (mask_rows_per_b != 1 && mask_rows_per_b != Hkv)) return LSQ_E_SHAPE;
+  if (mask && mask_stride < max_seq_len) return LSQ_E_SHAPE;
+  if (B == 0) return LSQ_OK;
+  if (!query || !k_pool || !v_pool || !block_tables || !seq_lens || !out) return LSQ_E_NULL;
+  if (i8 && (!k_scales || !v_scales)) return LSQ_E_NULL;
+  if ((reinterpret_cast<uintptr_t>(k_pool) & 15) || (reinterpret_cast<uintptr_t>(v_pool) & 15))
+    return LSQ_E_ALIGN;
+  if (B > 65535 || Hkv > 65535 || B * H > INT32_MAX) return LSQ_E_SHAPE;
+  const int64_t nsplit = max_seq_len > 0 ? (max_seq_len + kPaNT - 1) / kPaNT : 1;
+  if (nsplit > 1 && (!workspace || workspace_bytes < lsq_paged_attention_workspace_bytes(B, H, D, max_seq_len)))
+    return LSQ_E_NULL;
+  PagedArgs a{};
+  a.q = query; a.kp = k_pool; a.vp = v_pool; a.ks = k_scales; a.vs = v_scales;
+  a.scale_dt = scale_dtype; a.bt = block_tables; a.ldbt = bt_stride; a.sl = seq_lens;
+  a.mask = mask; a.ldm = mask_stride; a.mask_rows_per_b = static_cast<int>(mask_rows_per_b);
+  a.out = out; a.ws = static_cast<float*>(workspace);
+  a.B = static_cast<int>(B); a.H = static_cast<int>(H); a.Hkv = static_cast<int>(Hkv);
+  a.G = static_cast<int>(H / Hkv); a.BS = static_cast<int>(block_size);
+  a.nsplit = static_cast<int>(nsplit); a.max_sl = static_cast<int>(max_seq_len);
+  a.interleaved = head_mapping != 0;
+  a.sm_scale = 1.0f / std::sqrt(static_cast<float>(D));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case LSQ_F32: return launch_paged_dt<LSQ_F32>(a, i8, static_cast<int>(D), s);
+    case LSQ_F16: return launch_paged_dt<LSQ_F16>(a, i8, static_cast<int>(D), s);
+    default: return launch_paged_dt<LSQ_BF16>(a, i8, static_cast<int>(D), s);
+  }
+}

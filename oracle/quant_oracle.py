@@ -22,6 +22,9 @@ reference's behaviour (no code copied):
   w8a8_linear         quantization.py:404-447 Int8GEMMLinear's native path: int32 GEMM,
                       fp32 rescale, bias, one rounding to T (bit-exact target)
   silu_mul            modeling_qwen2.py:48 F.silu(gate) * up on T-valued layer outputs
+  paged_attention     paged_attention.py:33-173 decode attention over a paged (INT8) KV
+                      cache: gather by block table, keys.to(T) * scales, GQA mapping,
+                      SDPA (float64 here), one rounding to T
 
 How each part is pinned (tests/test_oracle.py):
   * round_bf16 / round_f16 against torch's dtype casts on every bf16 boundary case,
@@ -38,7 +41,11 @@ How each part is pinned (tests/test_oracle.py):
     device evaluation order (product with fp32 1/127) against torch on the GPU over every
     bf16 / fp16 value and random fp32 (tests/test_gpu_w8a8.py);
   * silu_mul against torch's CPU F.silu and product, and closed forms (silu(0) = 0,
-    large |g|).
+    large |g|);
+  * paged_attention against torch's CPU scaled_dot_product_attention on the gathered,
+    dequantized tensors (the reference's own ground truth, paged_attention.py:23-30,
+    :196-225), closed forms (equal keys -> mean of the values; one dominant key -> its
+    value) and the interleaved / contiguous head mappings.
 """
 
 from __future__ import annotations
@@ -279,3 +286,47 @@ def silu_mul(g, u, dt: str) -> np.ndarray:
     with np.errstate(over="ignore"):
         sg = round_to((g32 / (np.float32(1.0) + np.exp(-g32))).astype(np.float32), dt)
     return round_to((sg * np.asarray(u, dtype=np.float32)).astype(np.float32), dt)
+
+
+# ----------------------------------------------------------------------------- paged attention
+
+
+def paged_attention(q, k_pool, v_pool, block_tables, seq_lens, block_size, dt: str,
+                    k_scales=None, v_scales=None, head_mapping: str = "contiguous",
+                    mask=None, max_sl=None) -> np.ndarray:
+    """Decode attention of paged_attention_decode (paged_attention.py:33-173) as fp32
+    values of T, [B, H, D]. q [B, H, D] (T values); pools [NB, BS, Hkv, D] (int8 with
+    scales [NB, BS, Hkv] as fp32 values of their dtype, or T values); block_tables
+    [B, nblk]; token t of sequence b attends when t < max_sl and (mask[b or b*Hkv+kvh, t]
+    if a mask [rows, max_sl] is given, else t < seq_lens[b]). Keys / values are
+    round_T(k * s) for an INT8 cache; scores (q . k) / sqrt(D), softmax and the value
+    sum in float64, then one rounding to T."""
+    q = np.asarray(q, dtype=np.float64)
+    b_, h_, d_ = q.shape
+    hkv = k_pool.shape[2]
+    g_ = h_ // hkv
+    if max_sl is None:
+        max_sl = int(np.max(seq_lens))
+    out = np.zeros((b_, h_, d_), dtype=np.float64)
+    for b in range(b_):
+        ts = np.arange(max_sl)
+        rows = (np.asarray(block_tables[b])[ts // block_size], ts % block_size)
+        for kvh in range(hkv):
+            k = np.asarray(k_pool[rows[0], rows[1], kvh, :], dtype=np.float32)
+            v = np.asarray(v_pool[rows[0], rows[1], kvh, :], dtype=np.float32)
+            if k_scales is not None:
+                k = round_to(k * np.asarray(k_scales[rows[0], rows[1], kvh], np.float32)[:, None], dt)
+                v = round_to(v * np.asarray(v_scales[rows[0], rows[1], kvh], np.float32)[:, None], dt)
+            if mask is not None:
+                mrow = b * hkv + kvh if mask.shape[0] == b_ * hkv and hkv > 1 else b
+                valid = np.asarray(mask[mrow][:max_sl], dtype=bool)
+            else:
+                valid = ts < int(seq_lens[b])
+            for g in range(g_):
+                h = kvh * g_ + g if head_mapping == "contiguous" else g * hkv + kvh
+                sc = (k.astype(np.float64) @ q[b, h]) / np.sqrt(d_)
+                sc = np.where(valid, sc, -np.inf)
+                with np.errstate(invalid="ignore"):
+                    p = np.exp(sc - np.max(sc))
+                    out[b, h] = (p @ v.astype(np.float64)) / np.sum(p)
+    return round_to(out.astype(np.float32), dt)

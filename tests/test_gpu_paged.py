@@ -1,0 +1,124 @@
+"""GPU parity of the paged attention decode kernel (paged_attention_decode,
+src/kernels/paged_attention.py:33-173) against the oracle (float64 attention on the same
+T-valued, dequantized keys and values), to the 1e-2 relative bar; plus the reference's
+own ground truth (gather + SDPA in torch) on one case."""
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from localstrm_amd import paged_attention_decode
+from oracle import quant_oracle as qo
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda:0")
+TDT = {"f16": torch.float16, "bf16": torch.bfloat16, "f32": torch.float32}
+
+
+def _case(seed, b, h, hkv, d, bs, seqs, int8, dt, spare=5):
+    rng = np.random.default_rng(seed)
+    nblk = max(-(-max(seqs) // bs), 1)
+    nb = b * nblk + spare
+    bt = rng.permutation(nb)[: b * nblk].reshape(b, nblk).astype(np.int64)
+    if int8:
+        kp = rng.integers(-128, 128, size=(nb, bs, hkv, d)).astype(np.int8)
+        vp = rng.integers(-128, 128, size=(nb, bs, hkv, d)).astype(np.int8)
+        ks = qo.round_f16(rng.uniform(0.002, 0.03, size=(nb, bs, hkv)).astype(np.float32))
+        vs = qo.round_f16(rng.uniform(0.002, 0.03, size=(nb, bs, hkv)).astype(np.float32))
+    else:
+        kp = qo.round_to(rng.standard_normal((nb, bs, hkv, d)).astype(np.float32), dt)
+        vp = qo.round_to(rng.standard_normal((nb, bs, hkv, d)).astype(np.float32), dt)
+        ks = vs = None
+    q = qo.round_to(rng.standard_normal((b, h, d)).astype(np.float32), dt)
+    return q, kp, vp, ks, vs, bt, np.array(seqs, dtype=np.int64)
+
+
+def _run(q, kp, vp, ks, vs, bt, seqs, bs, dt, mapping="contiguous", mask=None, max_sl=None):
+    t = TDT[dt]
+    kv_t = torch.int8 if kp.dtype == np.int8 else t
+    args = dict(
+        query=torch.from_numpy(q).to(t).unsqueeze(2).to(DEV),
+        k_cache_pool=torch.from_numpy(kp).to(kv_t).to(DEV),
+        v_cache_pool=torch.from_numpy(vp).to(kv_t).to(DEV),
+        block_tables=torch.from_numpy(bt).to(DEV), seq_lens=torch.from_numpy(seqs).to(DEV),
+        block_size=bs, head_mapping=mapping, max_sl=max_sl,
+        attn_mask=None if mask is None else torch.from_numpy(mask).to(DEV),
+    )
+    if ks is not None:
+        args["k_scales"] = torch.from_numpy(ks).half().unsqueeze(-1).to(DEV)
+        args["v_scales"] = torch.from_numpy(vs).half().unsqueeze(-1).to(DEV)
+    out = paged_attention_decode(**args)
+    torch.cuda.synchronize()
+    return out[:, :, 0, :].float().cpu().numpy()
+
+
+CASES = [
+    # (b, h, hkv, d, bs, seqs, int8, dt, mapping)
+    (4, 14, 2, 64, 16, [1, 17, 300, 1000], True, "f16", "contiguous"),
+    (3, 28, 4, 128, 16, [256, 257, 2048], True, "bf16", "contiguous"),
+    (2, 4, 4, 64, 16, [5, 513], False, "f16", "contiguous"),
+    (3, 8, 2, 64, 32, [100, 64, 700], True, "f16", "interleaved"),
+    (2, 16, 1, 128, 8, [33, 260], False, "bf16", "contiguous"),
+    (2, 6, 2, 64, 16, [40, 9], False, "f32", "contiguous"),
+]
+
+
+@pytest.mark.parametrize("b,h,hkv,d,bs,seqs,int8,dt,mapping", CASES)
+def test_paged_attention_matches_oracle(b, h, hkv, d, bs, seqs, int8, dt, mapping):
+    print(f"paged B={b} H={h} Hkv={hkv} D={d} BS={bs} seqs={seqs} int8={int8} {dt} {mapping}", flush=True)
+    q, kp, vp, ks, vs, bt, sl = _case(b + h + d, b, h, hkv, d, bs, seqs, int8, dt)
+    got = _run(q, kp, vp, ks, vs, bt, sl, bs, dt, mapping)
+    ref = qo.paged_attention(q, kp, vp, bt, sl, bs, dt, ks, vs, mapping)
+    err = qo.rel_err(got, ref)
+    print(f"  rel_err={err:.2e}", flush=True)
+    assert err <= 1e-2
+
+
+def test_paged_attention_engine_mask_and_reference_ground_truth():
+    # the engine passes a repeat_interleave'd [B * Hkv, 1, 1, max_sl] mask
+    # (model_runner.py:138-143); and the reference's ground truth (gather, dequantize,
+    # SDPA) on the GPU with torch
+    b, h, hkv, d, bs = 3, 14, 2, 64, 16
+    seqs = [70, 5, 200]
+    q, kp, vp, ks, vs, bt, sl = _case(11, b, h, hkv, d, bs, seqs, True, "f16")
+    max_sl = max(seqs)
+    m = (np.arange(max_sl)[None, :] < sl[:, None]).reshape(b, 1, 1, max_sl)
+    mask = np.repeat(m, hkv, axis=0)
+    got = _run(q, kp, vp, ks, vs, bt, sl, bs, "f16", mask=mask, max_sl=max_sl)
+    plain = _run(q, kp, vp, ks, vs, bt, sl, bs, "f16")
+    assert np.array_equal(got, plain)
+    kt = torch.from_numpy(kp).to(DEV)
+    vt = torch.from_numpy(vp).to(DEV)
+    kst = torch.from_numpy(ks).half().to(DEV)
+    vst = torch.from_numpy(vs).half().to(DEV)
+    g = h // hkv
+    for bb in range(b):
+        n = seqs[bb]
+        tok = torch.arange(n, device=DEV)
+        blk = torch.from_numpy(bt[bb]).to(DEV)[tok // bs]
+        off = tok % bs
+        k = kt[blk, off].half() * kst[blk, off][..., None]
+        v = vt[blk, off].half() * vst[blk, off][..., None]
+        qq = torch.from_numpy(q[bb]).half().to(DEV).view(hkv, g, 1, d)
+        kk = k.permute(1, 0, 2).float().contiguous().view(hkv, 1, n, d).expand(hkv, g, n, d)
+        vv = v.permute(1, 0, 2).float().contiguous().view(hkv, 1, n, d).expand(hkv, g, n, d)
+        ref = F.scaled_dot_product_attention(qq.float(), kk, vv).half().float().view(h, d).cpu().numpy()
+        assert qo.rel_err(got[bb], ref) <= 1e-2
+
+
+def test_paged_attention_validation():
+    q = torch.zeros(2, 4, 1, 64, device=DEV, dtype=torch.float16)
+    kp = torch.zeros(4, 16, 2, 64, device=DEV, dtype=torch.int8)
+    bt = torch.zeros(2, 2, dtype=torch.int64, device=DEV)
+    sl = torch.ones(2, dtype=torch.int64, device=DEV)
+    with pytest.raises(ValueError, match="requires both k_scales and v_scales"):
+        paged_attention_decode(q, kp, kp, bt, sl)
+    with pytest.raises(ValueError, match="Unsupported head_mapping"):
+        paged_attention_decode(q, kp, kp, bt, sl, head_mapping="strided")
+    with pytest.raises(ValueError, match="must be divisible"):
+        paged_attention_decode(torch.zeros(2, 3, 1, 64, device=DEV), kp, kp, bt, sl)
+    with pytest.raises(NotImplementedError):
+        paged_attention_decode(torch.zeros(2, 4, 2, 64, device=DEV, dtype=torch.float16),
+                               kp.half(), kp.half(), bt, sl)

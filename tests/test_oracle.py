@@ -378,3 +378,69 @@ def test_silu_mul_matches_torch_ops(dt):
     assert qo.silu_mul(np.float32([0.0]), np.float32([3.0]), dt)[0] == 0.0
     assert qo.silu_mul(np.float32([60.0]), np.float32([0.5]), dt)[0] == 30.0
     assert qo.silu_mul(np.float32([-200.0]), np.float32([1.0]), dt)[0] == 0.0
+
+
+# ----------------------------------------------------------------------------- paged attention
+
+
+def _paged_case(rng, b, h, hkv, d, bs, nblk, seqs, int8):
+    nb = b * nblk + 3
+    perm = rng.permutation(nb)[: b * nblk].reshape(b, nblk)  # scattered physical blocks
+    if int8:
+        kp = rng.integers(-128, 128, size=(nb, bs, hkv, d)).astype(np.int8)
+        vp = rng.integers(-128, 128, size=(nb, bs, hkv, d)).astype(np.int8)
+        ks = qo.round_f16(rng.uniform(0.002, 0.02, size=(nb, bs, hkv)).astype(np.float32))
+        vs = qo.round_f16(rng.uniform(0.002, 0.02, size=(nb, bs, hkv)).astype(np.float32))
+    else:
+        kp = qo.round_f16(rng.standard_normal((nb, bs, hkv, d)).astype(np.float32))
+        vp = qo.round_f16(rng.standard_normal((nb, bs, hkv, d)).astype(np.float32))
+        ks = vs = None
+    q = qo.round_f16(rng.standard_normal((b, h, d)).astype(np.float32))
+    return q, kp, vp, ks, vs, perm, np.array(seqs, dtype=np.int64)
+
+
+@pytest.mark.parametrize("int8", [False, True])
+@pytest.mark.parametrize("mapping", ["contiguous", "interleaved"])
+def test_paged_attention_matches_torch_sdpa_on_gathered_tensors(int8, mapping):
+    # the reference's ground truth: gather the blocks, dequantize, expand heads, SDPA
+    rng = np.random.default_rng(4)
+    b, h, hkv, d, bs = 3, 6, 2, 64, 16
+    q, kp, vp, ks, vs, bt, seqs = _paged_case(rng, b, h, hkv, d, bs, 5, [38, 80, 1], int8)
+    ours = qo.paged_attention(q, kp, vp, bt, seqs, bs, "f16", ks, vs, mapping)
+    g = h // hkv
+    for bb in range(b):
+        n = int(seqs[bb])
+        blk, off = bt[bb][np.arange(n) // bs], np.arange(n) % bs
+        k = torch.from_numpy(kp[blk, off].astype(np.float32))
+        v = torch.from_numpy(vp[blk, off].astype(np.float32))
+        if int8:
+            k = (k.half() * torch.from_numpy(ks[blk, off])[..., None].half()).float()
+            v = (v.half() * torch.from_numpy(vs[blk, off])[..., None].half()).float()
+        for hh in range(h):
+            kvh = hh // g if mapping == "contiguous" else hh % hkv
+            qq = torch.from_numpy(q[bb, hh]).view(1, 1, 1, d)
+            ref = F.scaled_dot_product_attention(qq, k[:, kvh].view(1, 1, n, d), v[:, kvh].view(1, 1, n, d))
+            ref = ref.half().float().view(d).numpy()
+            assert np.max(np.abs(ours[bb, hh] - ref)) <= 2e-3 * max(1.0, np.max(np.abs(ref)))
+
+
+def test_paged_attention_closed_forms():
+    rng = np.random.default_rng(5)
+    b, h, hkv, d, bs = 1, 2, 1, 64, 4
+    q, kp, vp, _, _, bt, _ = _paged_case(rng, b, h, hkv, d, bs, 3, [10], False)
+    kp[:] = qo.round_f16(np.float32(0.25))  # equal scores: output = mean of the values
+    out = qo.paged_attention(q, kp, vp, bt, np.array([10]), bs, "f32")
+    ts = np.arange(10)
+    vals = vp[bt[0][ts // bs], ts % bs, 0].astype(np.float64)
+    np.testing.assert_allclose(out[0, 0], vals.mean(axis=0), rtol=1e-5, atol=1e-6)
+    # one key aligned with q and large: the output is that token's value
+    kp[:] = 0
+    kp[bt[0][1], 3, 0] = q[0, 1] * 50
+    out = qo.paged_attention(q, kp, vp, bt, np.array([10]), bs, "f32")
+    np.testing.assert_allclose(out[0, 1], vp[bt[0][1], 3, 0], rtol=1e-4, atol=1e-5)
+    # a mask that hides everything past token 4 equals seq_len 5
+    mask = np.zeros((1, 10), dtype=bool)
+    mask[0, :5] = True
+    a = qo.paged_attention(q, kp, vp, bt, np.array([10]), bs, "f32", mask=mask, max_sl=10)
+    bb = qo.paged_attention(q, kp, vp, bt, np.array([5]), bs, "f32", max_sl=5)
+    np.testing.assert_array_equal(a, bb)
