@@ -283,14 +283,35 @@ __global__ void __launch_bounds__(D) paged_attn_combine_kernel(PagedArgs p) {
   const int d = threadIdx.x;
   const float* w = p.ws + oh * p.nsplit * (D + 2);
   constexpr float kNegInf = -__builtin_huge_valf();
-  float M = kNegInf;
-  for (int s = 0; s < p.nsplit; ++s) M = fmaxf(M, w[s * (D + 2)]);
-  float a = 0.f, l = 0.f;
-  for (int s = 0; s < p.nsplit; ++s) {
-    const float ms = w[s * (D + 2)];
-    const float f = ms == kNegInf ? 0.f : __expf(ms - M);
-    l = fmaf(f, w[s * (D + 2) + 1], l);
-    a = fmaf(f, w[s * (D + 2) + 2 + d], a);
+  // splits in batches of 8 whose loads are all in flight before any is used
+  constexpr int kB = 8;
+  float M = kNegInf, a = 0.f, l = 0.f;
+  for (int s0 = 0; s0 < p.nsplit; s0 += kB) {
+    float ms[kB], ls[kB], as[kB];
+#pragma unroll
+    for (int u = 0; u < kB; ++u) {
+      const int sp_ = s0 + u < p.nsplit ? s0 + u : s0;  // past the end: a repeat, skipped
+      ms[u] = w[sp_ * (D + 2)];
+      ls[u] = w[sp_ * (D + 2) + 1];
+      as[u] = w[sp_ * (D + 2) + 2 + d];
+    }
+    float Mb = M;
+#pragma unroll
+    for (int u = 0; u < kB; ++u)
+      if (s0 + u < p.nsplit) Mb = fmaxf(Mb, ms[u]);
+    // rescale what was summed so far to the new running max
+    const float r = (M == kNegInf || Mb == kNegInf) ? 0.f : __expf(M - Mb);
+    a *= r;
+    l *= r;
+#pragma unroll
+    for (int u = 0; u < kB; ++u) {
+      if (s0 + u < p.nsplit) {
+        const float f = ms[u] == kNegInf ? 0.f : __expf(ms[u] - Mb);
+        l = fmaf(f, ls[u], l);
+        a = fmaf(f, as[u], a);
+      }
+    }
+    M = Mb;
   }
   static_cast<S*>(p.out)[oh * D + d] = Act<DT>::from_f32(opaque(a / l));
 }
