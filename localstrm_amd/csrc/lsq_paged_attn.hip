@@ -22,9 +22,12 @@
 // dequantized entries, as the reference feeds them to SDPA.
 
 #include "lsq_common.h"
+#include "lsq_mfma16.h"
 
 #include <cmath>
 #include <cstdint>
+#include <cstdlib>
+#include <type_traits>
 
 namespace lsq {
 namespace {
@@ -272,6 +275,229 @@ __global__ void __launch_bounds__(kPaNT) paged_attn_split_kernel(PagedArgs p) {
   }
 }
 
+
+// fp16 / bf16 queries: the same split on v_mfma_f32_16x16x32 (the G heads padded to the 16
+// rows of the MFMA). Scores: A = q (row = head), B = the dequantized keys of 16 tokens
+// (column = token); lane l of wave w owns token 64 w + 16 tt + (l & 15) of the split for
+// tt = 0..3 and dims 32 j + 8 (l >> 4) .. +7 of it, which it loads, dequantizes to T and
+// packs as the B operand, and whose value bytes it writes into the transposed tile. Value
+// sum: A = the probabilities rounded to T (as flash-attention kernels feed P to the second
+// product), B = 8 consecutive tokens' values of one dim from the transposed tile.
+template <int DT, bool I8, int D>
+__global__ void __launch_bounds__(kPaNT) paged_attn_mfma_kernel(PagedArgs p) {
+  using S = typename Act<DT>::storage;
+  constexpr int ESZ = I8 ? 1 : 2;
+  constexpr int kQLd = D + 8;        // q rows (T elements), padded against bank conflicts
+  constexpr int kSpLd = kPaNT + 4;   // score / probability rows (floats)
+  constexpr int kVtLd = kPaNT + 16 / ESZ;  // transposed value rows (elements)
+  __shared__ __align__(16) uint16_t qs[16 * kQLd];
+  __shared__ __align__(16) float sp[16 * kSpLd];
+  __shared__ float stat[2 * kPaMaxG];
+  __shared__ __align__(16) float vsc[kPaNT];
+  __shared__ __align__(16) unsigned char tile[D * kVtLd * ESZ];
+  __shared__ __align__(16) float accs[4 * kPaMaxG * D];
+
+  const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int r16 = lane & 15, q4 = lane >> 4;
+  const int G = p.G;
+  auto head = [&](int g) { return p.interleaved ? g * p.Hkv + kvh : kvh * G + g; };
+  const S* q = static_cast<const S*>(p.q);
+  for (int i = tid; i < 16 * D; i += kPaNT) {
+    const int g = i / D, d = i - (i / D) * D;
+    qs[g * kQLd + d] = g < G ? q[(static_cast<int64_t>(b) * p.H + head(g)) * D + d] : uint16_t(0);
+  }
+  const int seq = static_cast<int>(p.sl[b]);
+  auto valid_tok = [&](int t) -> bool {
+    if (t >= p.max_sl) return false;
+    if (p.mask) {
+      const int row = b * p.mask_rows_per_b + (p.mask_rows_per_b > 1 ? kvh : 0);
+      return p.mask[static_cast<int64_t>(row) * p.ldm + t] != 0;
+    }
+    return t < seq;
+  };
+
+  // ---- loads of the lane's 4 tokens: rows, scales, key and value slices (all in flight)
+  const int t0 = split * kPaNT;
+  int rowv[4];
+  bool val[4];
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt) {
+    const int t = t0 + wid * 64 + tt * 16 + r16;
+    val[tt] = valid_tok(t);
+    rowv[tt] = 0;  // masked: row 0 is read and its results discarded
+    if (val[tt]) {
+      const int64_t blk = p.bt[static_cast<int64_t>(b) * p.ldbt + t / p.BS];
+      rowv[tt] = static_cast<int>((blk * p.BS + t % p.BS) * p.Hkv + kvh);
+    }
+  }
+  float ksc[4], vscl[4];
+  using Chunk = typename std::conditional<I8, uint2, u32x4>::type;  // 8 elements
+  Chunk kc[4][D / 32], vc[4][D / 32];
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt) {
+    ksc[tt] = I8 ? load_as_f32(p.ks, p.scale_dt, rowv[tt]) : 1.f;
+    vscl[tt] = I8 ? load_as_f32(p.vs, p.scale_dt, rowv[tt]) : 1.f;
+    const unsigned char* kr = static_cast<const unsigned char*>(p.kp) + static_cast<int64_t>(rowv[tt]) * D * ESZ;
+    const unsigned char* vr = static_cast<const unsigned char*>(p.vp) + static_cast<int64_t>(rowv[tt]) * D * ESZ;
+#pragma unroll
+    for (int j = 0; j < D / 32; ++j) {
+      kc[tt][j] = *reinterpret_cast<const Chunk*>(kr + (32 * j + 8 * q4) * ESZ);
+      vc[tt][j] = *reinterpret_cast<const Chunk*>(vr + (32 * j + 8 * q4) * ESZ);
+    }
+  }
+  // values -> transposed tile (a masked token's values as 0), scales
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt) {
+    const int tl = wid * 64 + tt * 16 + r16;
+#pragma unroll
+    for (int j = 0; j < D / 32; ++j)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int d = 32 * j + 8 * q4 + e;
+        if constexpr (I8) {
+          const uint32_t w = e < 4 ? vc[tt][j].x : vc[tt][j].y;
+          tile[d * kVtLd + tl] = val[tt] ? static_cast<unsigned char>(w >> (8 * (e & 3))) : 0;
+        } else {
+          const uint32_t w = vc[tt][j][e >> 1];
+          reinterpret_cast<uint16_t*>(tile)[d * kVtLd + tl] = val[tt] ? static_cast<uint16_t>(w >> (16 * (e & 1))) : 0;
+        }
+      }
+    if (q4 == 0) vsc[tl] = val[tt] ? vscl[tt] : 0.f;
+  }
+  __syncthreads();
+
+  // ---- scores on the MFMA: A = q rows (head r16, dims 32 j + 8 q4 ..), B = keys
+  constexpr float kNegInf = -__builtin_huge_valf();
+  u32x4 qa[D / 32];
+#pragma unroll
+  for (int j = 0; j < D / 32; ++j) qa[j] = *reinterpret_cast<const u32x4*>(&qs[r16 * kQLd + 32 * j + 8 * q4]);
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt) {
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < D / 32; ++j) {
+      u32x4 kb;
+      if constexpr (I8) {
+        float kf[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const uint32_t w = e < 4 ? kc[tt][j].x : kc[tt][j].y;
+          kf[e] = Act<DT>::round(opaque(static_cast<float>(static_cast<int8_t>(w >> (8 * (e & 3)))) * ksc[tt]));
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) kb[e] = Mma<DT>::pack2(kf[2 * e], kf[2 * e + 1]);
+      } else {
+        kb = kc[tt][j];
+      }
+      acc = Mma<DT>::mma(qa[j], kb, acc);
+    }
+    const int tl = wid * 64 + tt * 16 + r16;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int g = 4 * q4 + e;
+      if (g < G) sp[g * kSpLd + tl] = val[tt] ? acc[e] * p.sm_scale : kNegInf;
+    }
+  }
+  __syncthreads();
+
+  // ---- softmax statistics per head (16 threads a head, DPP row reductions), exp
+  const int hg = tid >> 4, part = tid & 15;
+  if (hg < G) {
+    float m = kNegInf;
+#pragma unroll
+    for (int e = 0; e < 16; e += 4) {
+      const f32x4 v = *reinterpret_cast<const f32x4*>(&sp[hg * kSpLd + part * 16 + e]);
+      m = fmaxf(fmaxf(m, fmaxf(v[0], v[1])), fmaxf(v[2], v[3]));
+    }
+    m = row16_max(m);
+    if (part == 0) stat[hg] = m;
+  }
+  __syncthreads();
+  for (int g = 0; g < G; ++g) {
+    const float sv = sp[g * kSpLd + tid];
+    sp[g * kSpLd + tid] = sv == kNegInf ? 0.f : __expf(sv - stat[g]);
+  }
+  __syncthreads();
+  if (hg < G) {
+    float l = 0.f;
+#pragma unroll
+    for (int e = 0; e < 16; e += 4) {
+      const f32x4 v = *reinterpret_cast<const f32x4*>(&sp[hg * kSpLd + part * 16 + e]);
+      l += (v[0] + v[1]) + (v[2] + v[3]);
+    }
+    l = row16_sum(l);
+    if (part == 0) stat[kPaMaxG + hg] = l;
+  }
+
+  // ---- value sum on the MFMA: wave w over its 64 tokens in 2 steps of 32
+  f32x4 oacc[D / 16];
+#pragma unroll
+  for (int dt = 0; dt < D / 16; ++dt) oacc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int st = 0; st < 2; ++st) {
+    const int tb = wid * 64 + st * 32 + 8 * q4;  // the lane's 8 tokens
+    u32x4 pa;
+    {
+      const f32x4 p0 = *reinterpret_cast<const f32x4*>(&sp[r16 * kSpLd + tb]);
+      const f32x4 p1 = *reinterpret_cast<const f32x4*>(&sp[r16 * kSpLd + tb + 4]);
+      pa[0] = Mma<DT>::pack2(p0[0], p0[1]);
+      pa[1] = Mma<DT>::pack2(p0[2], p0[3]);
+      pa[2] = Mma<DT>::pack2(p1[0], p1[1]);
+      pa[3] = Mma<DT>::pack2(p1[2], p1[3]);
+    }
+    float sc8[8];
+    if constexpr (I8) {
+      const f32x4 s0 = *reinterpret_cast<const f32x4*>(&vsc[tb]);
+      const f32x4 s1 = *reinterpret_cast<const f32x4*>(&vsc[tb + 4]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) { sc8[e] = s0[e]; sc8[4 + e] = s1[e]; }
+    }
+#pragma unroll
+    for (int dt = 0; dt < D / 16; ++dt) {
+      const int d = 16 * dt + r16;
+      u32x4 vb;
+      if constexpr (I8) {
+        const uint2 w = *reinterpret_cast<const uint2*>(&tile[d * kVtLd + tb]);
+        float vf[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const uint32_t ww = e < 4 ? w.x : w.y;
+          vf[e] = Act<DT>::round(opaque(static_cast<float>(static_cast<int8_t>(ww >> (8 * (e & 3)))) * sc8[e]));
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) vb[e] = Mma<DT>::pack2(vf[2 * e], vf[2 * e + 1]);
+      } else {
+        vb = *reinterpret_cast<const u32x4*>(&reinterpret_cast<const uint16_t*>(tile)[d * kVtLd + tb]);
+      }
+      oacc[dt] = Mma<DT>::mma(pa, vb, oacc[dt]);
+    }
+  }
+#pragma unroll
+  for (int dt = 0; dt < D / 16; ++dt)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int g = 4 * q4 + e;
+      if (g < G) accs[(wid * kPaMaxG + g) * D + 16 * dt + r16] = oacc[dt][e];
+    }
+  __syncthreads();
+
+  for (int i = tid; i < G * D; i += kPaNT) {
+    const int g = i / D, d = i - (i / D) * D;
+    const float a = (accs[(0 * kPaMaxG + g) * D + d] + accs[(1 * kPaMaxG + g) * D + d]) +
+                    (accs[(2 * kPaMaxG + g) * D + d] + accs[(3 * kPaMaxG + g) * D + d]);
+    const float m = stat[g], l = stat[kPaMaxG + g];
+    const int64_t oh = static_cast<int64_t>(b) * p.H + head(g);
+    if (p.nsplit == 1) {
+      static_cast<S*>(p.out)[oh * D + d] = Act<DT>::from_f32(opaque(a / l));
+    } else {
+      float* w = p.ws + (oh * p.nsplit + split) * (D + 2);
+      if (d == 0) { w[0] = m; w[1] = l; }
+      w[2 + d] = a;
+    }
+  }
+}
+
 // One workgroup of D threads per (sequence, head): out = sum_s e^(m_s - M) acc_s /
 // sum_s e^(m_s - M) l_s over the splits. (A ticket in the split kernel would save this
 // launch, but the device-scope release / acquire it needs writes back and invalidates
@@ -316,10 +542,21 @@ __global__ void __launch_bounds__(D) paged_attn_combine_kernel(PagedArgs p) {
   static_cast<S*>(p.out)[oh * D + d] = Act<DT>::from_f32(opaque(a / l));
 }
 
+// LSQ_PAGED_KERNEL=valu runs the VALU split kernel for fp16 / bf16 too (comparisons).
+bool paged_valu() {
+  const char* e = std::getenv("LSQ_PAGED_KERNEL");
+  return e && e[0] == 'v';
+}
+
 template <int DT, bool I8, int D>
 int launch_paged(const PagedArgs& a, hipStream_t s) {
   const dim3 grid(static_cast<unsigned>(a.nsplit), static_cast<unsigned>(a.Hkv), static_cast<unsigned>(a.B));
-  paged_attn_split_kernel<DT, I8, D><<<grid, dim3(kPaNT), 0, s>>>(a);
+  if constexpr (DT != LSQ_F32) {
+    if (!paged_valu()) paged_attn_mfma_kernel<DT, I8, D><<<grid, dim3(kPaNT), 0, s>>>(a);
+    else paged_attn_split_kernel<DT, I8, D><<<grid, dim3(kPaNT), 0, s>>>(a);
+  } else {
+    paged_attn_split_kernel<DT, I8, D><<<grid, dim3(kPaNT), 0, s>>>(a);
+  }
   if (a.nsplit > 1)
     paged_attn_combine_kernel<DT, D><<<dim3(static_cast<unsigned>(a.B * a.H)), dim3(D), 0, s>>>(a);
   return static_cast<int>(hipGetLastError());

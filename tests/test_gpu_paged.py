@@ -65,9 +65,14 @@ CASES = [
 ]
 
 
+@pytest.mark.parametrize("kernel", ["mfma", "valu"])
 @pytest.mark.parametrize("b,h,hkv,d,bs,seqs,int8,dt,mapping", CASES)
-def test_paged_attention_matches_oracle(b, h, hkv, d, bs, seqs, int8, dt, mapping):
-    print(f"paged B={b} H={h} Hkv={hkv} D={d} BS={bs} seqs={seqs} int8={int8} {dt} {mapping}", flush=True)
+def test_paged_attention_matches_oracle(monkeypatch, kernel, b, h, hkv, d, bs, seqs, int8, dt, mapping):
+    # fp16 / bf16 queries run the MFMA kernel by default; LSQ_PAGED_KERNEL=valu the VALU one
+    # (the only one for fp32)
+    if kernel == "valu":
+        monkeypatch.setenv("LSQ_PAGED_KERNEL", "valu")
+    print(f"paged {kernel} B={b} H={h} Hkv={hkv} D={d} BS={bs} seqs={seqs} int8={int8} {dt} {mapping}", flush=True)
     q, kp, vp, ks, vs, bt, sl = _case(b + h + d, b, h, hkv, d, bs, seqs, int8, dt)
     got = _run(q, kp, vp, ks, vs, bt, sl, bs, dt, mapping)
     ref = qo.paged_attention(q, kp, vp, bt, sl, bs, dt, ks, vs, mapping)
