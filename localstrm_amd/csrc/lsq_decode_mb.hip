@@ -1,7 +1,7 @@
 // Decode-shaped weight-only GEMM for small batches, 16 < M <= 64 tokens (gfx950).
 //
 // GPU form of QuantizedLinear.forward (src/kernels/quantization.py:129-141) for batched
-// decode steps. Same weight stream and in-register unpack as lsq_decode.hip: each wave
+// decode steps. Same weight stream and in-register unpack as lsq_decode_impl.h: each wave
 // owns one 16-row tile of W and one of KS K slices, streams its tiles once from HBM
 // through a ring of kD k-tile steps in registers, and turns them into the B operands of
 // v_mfma_f32_16x16x32. What changes is the activation side: 17..64 tokens of a layer
@@ -19,7 +19,7 @@
 // activation loads of a chunk are issued one (INT8) or two (INT4) chunks before they are
 // needed, and the weight loads issued after them stay in flight across the wait.
 //
-// Numerics as in lsq_decode.hip: weight products are exact in the fp32 accumulators; the
+// Numerics as in lsq_decode_impl.h: weight products are exact in the fp32 accumulators; the
 // INT4 nibble bias (and the magic exponent) is removed per 128-column tile with the
 // activation sums, group scales are applied per tile in fp32, per-channel scales and
 // the bias at the end, then one rounding to T.

@@ -4,7 +4,7 @@
 // reference materializes W = dequantize(x.dtype) and then calls F.linear. This file holds
 // the C entry points and the dispatch between the kernels; none materializes W in HBM:
 //
-//  * decode (lsq_decode.hip): M <= 64, fp16/bf16, K % 128 == 0, all activations staged in
+//  * decode (lsq_decode_impl.h): M <= 64, fp16/bf16, K % 128 == 0, all activations staged in
 //    LDS once (the common decode case; up to 64 tokens when x fits in LDS);
 //  * chunked decode (lsq_decode_mb.hip): 16 < M <= 64 when x does not fit, activations
 //    streamed through LDS;

@@ -5,7 +5,7 @@
 // chain of elementwise kernels (:411-414), pads M to a multiple of 32 (:416-422), calls
 // torch._int_mm (:425) and rescales in fp32 (:431-440). Here:
 //
-//  * the decode kernel's W8A8 modes (lsq_decode.hip) for M <= 64: int8 weights streamed
+//  * the decode kernel's W8A8 modes (lsq_decode_impl.h) for M <= 64: int8 weights streamed
 //    once from the tiled layout straight into v_mfma_i32_16x16x64_i8, no conversion;
 //    for small x (M * K <= 16384) every workgroup quantizes x itself while staging it,
 //    so the layer is one launch;
