@@ -82,6 +82,9 @@ __global__ void __launch_bounds__(64 * RG * KS) decode_mb_kernel(LinearArgs p) {
   const int ng = static_cast<int>(p.ngroups);
   const int ngs = GROUPED ? ng : 1;
   const int gtiles = static_cast<int>(p.group / kTileK);
+  // k tile -> group without a divide (a branch) in the loop: floor(kt / gtiles) =
+  // mulhi(kt, ceil(2^32 / gtiles)), exact for kt, gtiles < 2^16
+  const uint32_t gmagic = gtiles > 1 ? static_cast<uint32_t>((0x100000000ull + gtiles - 1) / gtiles) : 0u;
   // K slices: slice s owns k tiles [s * nkt / KS, (s + 1) * nkt / KS); every slice runs
   // the same number of chunks (that of the longest one), so all waves meet at the same
   // barriers.
@@ -191,8 +194,10 @@ __global__ void __launch_bounds__(64 * RG * KS) decode_mb_kernel(LinearArgs p) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) sum += Mma<DT>::lo(v[e]) + Mma<DT>::hi(v[e]);
         // the 16 pieces of one (slice, token, k tile) sit in one 16-lane row
+        // (every lane of the row stores the same value: a store from one lane in 16 would
+        // be a divergent branch, at which the compiler drains all global loads in flight)
         sum = row16_sum(sum);
-        if ((lane & 15) == 0) xsum[((sl * 2 + b) * kCT + pc / 16) * MP + m] = sum;
+        xsum[((sl * 2 + b) * kCT + pc / 16) * MP + m] = sum;
       }
     }
   };
@@ -243,8 +248,10 @@ __global__ void __launch_bounds__(64 * RG * KS) decode_mb_kernel(LinearArgs p) {
           }
         }
       }
-      // Per k tile: LDS reads first (they overlap the wait for the weights), unpack,
-      // refill of the ring slot just freed, then MB interleaved MFMA chains.
+      // Per k tile: unpack the ring slot and refill it, both unconditionally (a ring
+      // register written on only some paths makes the compiler load into a temporary and
+      // copy it over after draining every load in flight), then the LDS reads and MB
+      // interleaved MFMA chains.
       const bool live = st < my_nt;  // uniform
       const int kBuf = (s / kCT) & 1;  // (b * kD + s) / kCT has the parity of s / kCT
       const uint16_t* xb = xs + (ks * 2 + kBuf) * MP * ldxs + (s % kCT) * kTileK;
@@ -253,6 +260,11 @@ __global__ void __launch_bounds__(64 * RG * KS) decode_mb_kernel(LinearArgs p) {
       f32x4 xo[MB];
       float sc = 1.f;
       u32x4 bb[4];
+#pragma unroll
+      for (int d = 0; d < 4; ++d)
+        bb[d] = W4 ? unpack_w4(wbuf[s][0][d], nib_mask, magic)
+                   : convert_w8<DT>(wbuf[s][d >> 1][2 * (d & 1)], wbuf[s][d >> 1][2 * (d & 1) + 1]);
+      issue(wbuf[s], st + kD);
       if (live) {
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb)
@@ -264,16 +276,9 @@ __global__ void __launch_bounds__(64 * RG * KS) decode_mb_kernel(LinearArgs p) {
           for (int mb = 0; mb < MB; ++mb) xo[mb] = *reinterpret_cast<const f32x4*>(xsb + 16 * mb + 4 * q);
         }
         if (GROUPED) {
-          const int kt = my_lo + st;
-          sc = srow[gtiles == 1 ? kt : kt / gtiles];
+          const uint32_t kt = static_cast<uint32_t>(my_lo + st);
+          sc = srow[gtiles == 1 ? kt : __umulhi(kt, gmagic)];
         }
-#pragma unroll
-        for (int d = 0; d < 4; ++d)
-          bb[d] = W4 ? unpack_w4(wbuf[s][0][d], nib_mask, magic)
-                     : convert_w8<DT>(wbuf[s][d >> 1][2 * (d & 1)], wbuf[s][d >> 1][2 * (d & 1) + 1]);
-      }
-      issue(wbuf[s], st + kD);
-      if (live) {
         if (W4) {
           f32x4 dacc[MB];
 #pragma unroll

@@ -285,10 +285,12 @@ def test_batched_decode_edges(layout, kind, group, monkeypatch):
     _check_layer(kind, 80, 128, 33, group=128, bias=True, seed=3)
 
 
-@pytest.mark.parametrize("kind,group", [("int8", None), ("int4", 128), ("int4", 4864)])
+@pytest.mark.parametrize("kind,group", [("int8", None), ("int4", 128), ("int4", 256), ("int4", 384),
+                                        ("int4", 4864)])
 def test_chunked_decode_large_k(kind, group):
     """17..64 tokens with activations too large for LDS (K = 4864, the Qwen2.5-0.5B down
-    projection): the chunked decode kernel, partial last workgroup, bias, both dtypes."""
+    projection): the chunked decode kernel, partial last workgroup, bias, both dtypes;
+    groups of 1, 2 and 3 k tiles (384: the last group is partial) and per-channel."""
     g = group if group is not None else 128
     for m in (17, 48):
         for dtype in (torch.bfloat16, torch.float16):
