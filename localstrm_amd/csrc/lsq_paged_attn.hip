@@ -6,7 +6,12 @@
 // block into a contiguous copy, dequantizes it (keys.to(T) * scales), expands the GQA
 // heads and calls F.scaled_dot_product_attention. Here nothing is copied:
 //
-//  * paged_attn_split_kernel: one workgroup per (sequence, KV head, split of 256 tokens);
+//  * paged_attn_mfma_kernel (fp16 / bf16 queries): one workgroup per (sequence, KV head,
+//    split of one or more 256-token chunks), scores and P x V on the MFMA, an online
+//    softmax across the split's chunks, each chunk's loads issued while the previous one
+//    finishes; described at the kernel;
+//  * paged_attn_split_kernel (fp32, or LSQ_PAGED_KERNEL=valu): one workgroup per
+//    (sequence, KV head, split of 256 tokens);
 //    thread t takes token t of the split: it walks the block table to the token's row,
 //    dequantizes its key (round_T(k * scale)) and forms the scores of all G query heads
 //    that share this KV head (q of the G heads in LDS); softmax statistics per head over
@@ -15,7 +20,8 @@
 //    LDS. One split writes the normalized output; several write (max, sum, partial
 //    output) to the caller's workspace;
 //  * paged_attn_combine_kernel: rescales and adds the splits of each (sequence, head).
-// HBM-bound: every key / value byte (plus its scale) is read once per step.
+// Every key / value byte (plus its scale) is read once per step; at decode sizes the time
+// is set by each workgroup's chain of dependent loads and barriers more than by bandwidth.
 //
 // Numerics: scores and softmax in fp32 with the SDPA default scale 1 / sqrt(D), the
 // value sum in fp32, one rounding to T at the end; keys and values are the T-valued
@@ -24,6 +30,7 @@
 #include "lsq_common.h"
 #include "lsq_mfma16.h"
 
+#include <algorithm>
 #include <cmath>
 #include <cstdint>
 #include <cstdlib>
@@ -51,6 +58,7 @@ struct PagedArgs {
   void* out;              // [B, H, D] (dtype DT)
   float* ws;              // [B, H, nsplit, D + 2] partials when nsplit > 1
   int B, H, Hkv, G, BS, nsplit, max_sl, interleaved;
+  int cps;                // chunks of kPaNT tokens per split (MFMA kernel; the VALU kernel: 1)
   float sm_scale;
 };
 
@@ -66,6 +74,16 @@ __device__ __forceinline__ float kv_elem(u32x4 v, int e, float s) {
     return Act<DT>::to_f32(static_cast<uint16_t>(v[e >> 1] >> (16 * (e & 1))));
   }
 }
+
+// The aligned dword holding scale i (fp32, or 16-bit f16 / bf16) of a per-row scale
+// array, loaded without branching on the dtype so that several such loads are in flight
+// together (a load inside a dtype branch is waited for before the branch ends); convert
+// with dword_elem(w, scale_half(dt, i), dt). A 16-bit element's dword never crosses a page.
+__device__ __forceinline__ uint32_t load_scale_word(const void* p, int dt, int64_t i) {
+  const int64_t off = dt == LSQ_F32 ? 4 * i : 2 * i;
+  return *reinterpret_cast<const uint32_t*>(static_cast<const unsigned char*>(p) + (off & ~int64_t(3)));
+}
+__device__ __forceinline__ int scale_half(int dt, int64_t i) { return dt == LSQ_F32 ? 0 : static_cast<int>(i & 1); }
 
 // Max / sum of a float over each row of 16 lanes, in every lane of the row (DPP).
 __device__ __forceinline__ float dpp_f(float v, int ctrl) {
@@ -124,15 +142,16 @@ __global__ void __launch_bounds__(kPaNT) paged_attn_split_kernel(PagedArgs p) {
   // are all in flight together.
   const int t0 = split * kPaNT;
   const int t = t0 + tid;
+  // The block table entry is read for every token below max_seq_len (the table holds
+  // ceil(max_seq_len / block_size) entries per sequence), so its load does not wait for
+  // the sequence length; only valid tokens use it.
+  const int64_t blk = t < p.max_sl ? p.bt[static_cast<int64_t>(b) * p.ldbt + t / p.BS] : 0;
   const bool valid = valid_tok(t);
   int my_row = -1;
-  if (valid) {
-    const int64_t blk = p.bt[static_cast<int64_t>(b) * p.ldbt + t / p.BS];
-    my_row = static_cast<int>((blk * p.BS + t % p.BS) * p.Hkv + kvh);
-  }
+  if (valid) my_row = static_cast<int>((blk * p.BS + t % p.BS) * p.Hkv + kvh);
   const int64_t lrow = my_row < 0 ? 0 : my_row;
-  const float ks = I8 ? load_as_f32(p.ks, p.scale_dt, lrow) : 1.f;
-  const float vs = I8 ? load_as_f32(p.vs, p.scale_dt, lrow) : 1.f;
+  const uint32_t ksw = I8 ? load_scale_word(p.ks, p.scale_dt, lrow) : 0u;
+  const uint32_t vsw = I8 ? load_scale_word(p.vs, p.scale_dt, lrow) : 0u;
   u32x4 kraw[D / EPC], vraw[D / EPC];
   {
     const unsigned char* kr = static_cast<const unsigned char*>(p.kp) + lrow * D * ESZ;
@@ -142,6 +161,8 @@ __global__ void __launch_bounds__(kPaNT) paged_attn_split_kernel(PagedArgs p) {
 #pragma unroll
     for (int c = 0; c < D / EPC; ++c) vraw[c] = *reinterpret_cast<const u32x4*>(vr + c * 16);
   }
+  const float ks = I8 ? dword_elem(ksw, scale_half(p.scale_dt, lrow), p.scale_dt) : 1.f;
+  const float vs = I8 ? dword_elem(vsw, scale_half(p.scale_dt, lrow), p.scale_dt) : 1.f;
   // value row -> transposed tile (elements as stored), scale (0 for a masked token)
 #pragma unroll
   for (int c = 0; c < D / EPC; ++c)
@@ -276,13 +297,16 @@ __global__ void __launch_bounds__(kPaNT) paged_attn_split_kernel(PagedArgs p) {
 }
 
 
-// fp16 / bf16 queries: the same split on v_mfma_f32_16x16x32 (the G heads padded to the 16
-// rows of the MFMA). Scores: A = q (row = head), B = the dequantized keys of 16 tokens
-// (column = token); lane l of wave w owns token 64 w + 16 tt + (l & 15) of the split for
-// tt = 0..3 and dims 32 j + 8 (l >> 4) .. +7 of it, which it loads, dequantizes to T and
-// packs as the B operand, and whose value bytes it writes into the transposed tile. Value
-// sum: A = the probabilities rounded to T (as flash-attention kernels feed P to the second
-// product), B = 8 consecutive tokens' values of one dim from the transposed tile.
+// fp16 / bf16 queries on v_mfma_f32_16x16x32 (the G heads padded to the 16 rows of the
+// MFMA). A workgroup takes p.cps consecutive chunks of 256 tokens. Per chunk, scores:
+// A = q (row = head), B = the dequantized keys of 16 tokens (column = token); lane l of
+// wave w owns token 64 w + 16 tt + (l & 15) of the chunk for tt = 0..3 and dims
+// 32 j + 8 (l >> 4) .. +7 of it, which it loads, dequantizes to T and packs as the B
+// operand, and whose value bytes it writes into the transposed tile. Value sum: A = the
+// probabilities rounded to T (as flash-attention kernels feed P to the second product),
+// B = 8 consecutive tokens' values of one dim from the transposed tile, accumulated in
+// registers across chunks with the running max / sum of an online softmax (the partial
+// sums rescaled by e^(m_old - m_new) per head).
 template <int DT, bool I8, int D>
 __global__ void __launch_bounds__(kPaNT) paged_attn_mfma_kernel(PagedArgs p) {
   using S = typename Act<DT>::storage;
@@ -292,7 +316,7 @@ __global__ void __launch_bounds__(kPaNT) paged_attn_mfma_kernel(PagedArgs p) {
   constexpr int kVtLd = kPaNT + 16 / ESZ;  // transposed value rows (elements)
   __shared__ __align__(16) uint16_t qs[16 * kQLd];
   __shared__ __align__(16) float sp[16 * kSpLd];
-  __shared__ float stat[2 * kPaMaxG];
+  __shared__ float stat[3 * 16];     // per head: running max, running sum, rescale factor
   __shared__ __align__(16) float vsc[kPaNT];
   __shared__ __align__(16) unsigned char tile[D * kVtLd * ESZ];
   __shared__ __align__(16) float accs[4 * kPaMaxG * D];
@@ -307,6 +331,11 @@ __global__ void __launch_bounds__(kPaNT) paged_attn_mfma_kernel(PagedArgs p) {
     const int g = i / D, d = i - (i / D) * D;
     qs[g * kQLd + d] = g < G ? q[(static_cast<int64_t>(b) * p.H + head(g)) * D + d] : uint16_t(0);
   }
+  if (tid < 16) {
+    stat[tid] = -__builtin_huge_valf();
+    stat[16 + tid] = 0.f;
+    stat[32 + tid] = 0.f;
+  }
   const int seq = static_cast<int>(p.sl[b]);
   auto valid_tok = [&](int t) -> bool {
     if (t >= p.max_sl) return false;
@@ -317,162 +346,234 @@ __global__ void __launch_bounds__(kPaNT) paged_attn_mfma_kernel(PagedArgs p) {
     return t < seq;
   };
 
-  // ---- loads of the lane's 4 tokens: rows, scales, key and value slices (all in flight)
-  const int t0 = split * kPaNT;
-  int rowv[4];
-  bool val[4];
+  // This workgroup's chunks of kPaNT tokens: [c_lo, c_hi). Each chunk is loaded while the
+  // previous one finishes: its block-table entries one chunk ahead, its keys, values and
+  // scales as soon as the previous chunk's are consumed (after its scores and value
+  // tile), so the softmax and value sum of a chunk overlap the next chunk's loads.
+  const int nchunk = (p.max_sl + kPaNT - 1) / kPaNT;
+  const int c_lo = split * p.cps;
+  const int c_hi = min(c_lo + p.cps, nchunk);
+  auto tok = [&](int c, int tt) { return c * kPaNT + wid * 64 + tt * 16 + r16; };
+  // Block-table entries are read for every token below max_seq_len (the table holds
+  // ceil(max_seq_len / block_size) entries per sequence): these loads do not wait for
+  // the sequence length, and only valid tokens use them.
+  // The loads are unconditional (tokens past max_seq_len read the last column, and are
+  // masked later): a load under a per-lane condition makes the compiler wait for it at
+  // the end of the condition. Block indices are below 2^31 (pool rows are), so the low
+  // dword of each entry is enough.
+  const int32_t* btw = reinterpret_cast<const int32_t*>(p.bt);
+  auto load_bt = [&](int c, int (&blk)[4]) {
+    if (c < c_hi) {  // uniform; then max_seq_len > 0
 #pragma unroll
-  for (int tt = 0; tt < 4; ++tt) {
-    const int t = t0 + wid * 64 + tt * 16 + r16;
-    val[tt] = valid_tok(t);
-    rowv[tt] = 0;  // masked: row 0 is read and its results discarded
-    if (val[tt]) {
-      const int64_t blk = p.bt[static_cast<int64_t>(b) * p.ldbt + t / p.BS];
-      rowv[tt] = static_cast<int>((blk * p.BS + t % p.BS) * p.Hkv + kvh);
+      for (int tt = 0; tt < 4; ++tt) {
+        const int t = min(tok(c, tt), p.max_sl - 1);
+        blk[tt] = btw[2 * (static_cast<int64_t>(b) * p.ldbt + t / p.BS)];
+      }
     }
-  }
-  float ksc[4], vscl[4];
+  };
   using Chunk = typename std::conditional<I8, uint2, u32x4>::type;  // 8 elements
   Chunk kc[4][D / 32], vc[4][D / 32];
+  uint32_t ksw[4], vsw[4];  // raw scale words, converted when the chunk is used
+  int shalf[4];
+  bool val[4];
+  // Keys, values and scales of the lane's 4 tokens of chunk c (a masked token, or a chunk
+  // past the last, reads row 0 and its results are discarded).
+  // No load here sits inside a data-dependent branch, so all of them are in flight
+  // together (mask bytes first, then rows, scales, keys and values).
+  auto load_kv = [&](int c, const int (&blk)[4]) {
+    const bool live = c < c_hi;
+    unsigned char mk[4] = {1, 1, 1, 1};
+    if (p.mask && live) {  // uniform; a mask row holds max_seq_len entries
+      const int64_t mrow = static_cast<int64_t>(b * p.mask_rows_per_b + (p.mask_rows_per_b > 1 ? kvh : 0)) * p.ldm;
 #pragma unroll
-  for (int tt = 0; tt < 4; ++tt) {
-    ksc[tt] = I8 ? load_as_f32(p.ks, p.scale_dt, rowv[tt]) : 1.f;
-    vscl[tt] = I8 ? load_as_f32(p.vs, p.scale_dt, rowv[tt]) : 1.f;
-    const unsigned char* kr = static_cast<const unsigned char*>(p.kp) + static_cast<int64_t>(rowv[tt]) * D * ESZ;
-    const unsigned char* vr = static_cast<const unsigned char*>(p.vp) + static_cast<int64_t>(rowv[tt]) * D * ESZ;
-#pragma unroll
-    for (int j = 0; j < D / 32; ++j) {
-      kc[tt][j] = *reinterpret_cast<const Chunk*>(kr + (32 * j + 8 * q4) * ESZ);
-      vc[tt][j] = *reinterpret_cast<const Chunk*>(vr + (32 * j + 8 * q4) * ESZ);
+      for (int tt = 0; tt < 4; ++tt) mk[tt] = p.mask[mrow + min(tok(c, tt), p.max_sl - 1)];
     }
-  }
-  // values -> transposed tile (a masked token's values as 0), scales
+    int row[4];
 #pragma unroll
-  for (int tt = 0; tt < 4; ++tt) {
-    const int tl = wid * 64 + tt * 16 + r16;
+    for (int tt = 0; tt < 4; ++tt) {
+      const int t = tok(c, tt);
+      val[tt] = live && t < p.max_sl && (p.mask ? mk[tt] != 0 : t < seq);
+      row[tt] = val[tt] ? (blk[tt] * p.BS + t % p.BS) * p.Hkv + kvh : 0;
+    }
+    if constexpr (I8) {
 #pragma unroll
-    for (int j = 0; j < D / 32; ++j)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int d = 32 * j + 8 * q4 + e;
-        if constexpr (I8) {
-          const uint32_t w = e < 4 ? vc[tt][j].x : vc[tt][j].y;
-          tile[d * kVtLd + tl] = val[tt] ? static_cast<unsigned char>(w >> (8 * (e & 3))) : 0;
-        } else {
-          const uint32_t w = vc[tt][j][e >> 1];
-          reinterpret_cast<uint16_t*>(tile)[d * kVtLd + tl] = val[tt] ? static_cast<uint16_t>(w >> (16 * (e & 1))) : 0;
-        }
+      for (int tt = 0; tt < 4; ++tt) {
+        ksw[tt] = load_scale_word(p.ks, p.scale_dt, row[tt]);
+        vsw[tt] = load_scale_word(p.vs, p.scale_dt, row[tt]);
+        shalf[tt] = scale_half(p.scale_dt, row[tt]);
       }
-    if (q4 == 0) vsc[tl] = val[tt] ? vscl[tt] : 0.f;
-  }
-  __syncthreads();
+    }
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) {
+      const unsigned char* kr = static_cast<const unsigned char*>(p.kp) + static_cast<int64_t>(row[tt]) * D * ESZ;
+      const unsigned char* vr = static_cast<const unsigned char*>(p.vp) + static_cast<int64_t>(row[tt]) * D * ESZ;
+#pragma unroll
+      for (int j = 0; j < D / 32; ++j) {
+        kc[tt][j] = *reinterpret_cast<const Chunk*>(kr + (32 * j + 8 * q4) * ESZ);
+        vc[tt][j] = *reinterpret_cast<const Chunk*>(vr + (32 * j + 8 * q4) * ESZ);
+      }
+    }
+  };
+  int blk_next[4] = {0, 0, 0, 0};
+  load_bt(c_lo, blk_next);
+  load_kv(c_lo, blk_next);
+  load_bt(c_lo + 1, blk_next);
 
-  // ---- scores on the MFMA: A = q rows (head r16, dims 32 j + 8 q4 ..), B = keys
   constexpr float kNegInf = -__builtin_huge_valf();
-  u32x4 qa[D / 32];
-#pragma unroll
-  for (int j = 0; j < D / 32; ++j) qa[j] = *reinterpret_cast<const u32x4*>(&qs[r16 * kQLd + 32 * j + 8 * q4]);
-#pragma unroll
-  for (int tt = 0; tt < 4; ++tt) {
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int j = 0; j < D / 32; ++j) {
-      u32x4 kb;
-      if constexpr (I8) {
-        float kf[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const uint32_t w = e < 4 ? kc[tt][j].x : kc[tt][j].y;
-          kf[e] = Act<DT>::round(opaque(static_cast<float>(static_cast<int8_t>(w >> (8 * (e & 3)))) * ksc[tt]));
-        }
-#pragma unroll
-        for (int e = 0; e < 4; ++e) kb[e] = Mma<DT>::pack2(kf[2 * e], kf[2 * e + 1]);
-      } else {
-        kb = kc[tt][j];
-      }
-      acc = Mma<DT>::mma(qa[j], kb, acc);
-    }
-    const int tl = wid * 64 + tt * 16 + r16;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int g = 4 * q4 + e;
-      if (g < G) sp[g * kSpLd + tl] = val[tt] ? acc[e] * p.sm_scale : kNegInf;
-    }
-  }
-  __syncthreads();
-
-  // ---- softmax statistics per head (16 threads a head, DPP row reductions), exp
-  const int hg = tid >> 4, part = tid & 15;
-  if (hg < G) {
-    float m = kNegInf;
-#pragma unroll
-    for (int e = 0; e < 16; e += 4) {
-      const f32x4 v = *reinterpret_cast<const f32x4*>(&sp[hg * kSpLd + part * 16 + e]);
-      m = fmaxf(fmaxf(m, fmaxf(v[0], v[1])), fmaxf(v[2], v[3]));
-    }
-    m = row16_max(m);
-    if (part == 0) stat[hg] = m;
-  }
-  __syncthreads();
-  for (int g = 0; g < G; ++g) {
-    const float sv = sp[g * kSpLd + tid];
-    sp[g * kSpLd + tid] = sv == kNegInf ? 0.f : __expf(sv - stat[g]);
-  }
-  __syncthreads();
-  if (hg < G) {
-    float l = 0.f;
-#pragma unroll
-    for (int e = 0; e < 16; e += 4) {
-      const f32x4 v = *reinterpret_cast<const f32x4*>(&sp[hg * kSpLd + part * 16 + e]);
-      l += (v[0] + v[1]) + (v[2] + v[3]);
-    }
-    l = row16_sum(l);
-    if (part == 0) stat[kPaMaxG + hg] = l;
-  }
-
-  // ---- value sum on the MFMA: wave w over its 64 tokens in 2 steps of 32
   f32x4 oacc[D / 16];
 #pragma unroll
   for (int dt = 0; dt < D / 16; ++dt) oacc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  __syncthreads();  // q rows and the running statistics are in LDS
+  u32x4 qa[D / 32];
 #pragma unroll
-  for (int st = 0; st < 2; ++st) {
-    const int tb = wid * 64 + st * 32 + 8 * q4;  // the lane's 8 tokens
-    u32x4 pa;
-    {
-      const f32x4 p0 = *reinterpret_cast<const f32x4*>(&sp[r16 * kSpLd + tb]);
-      const f32x4 p1 = *reinterpret_cast<const f32x4*>(&sp[r16 * kSpLd + tb + 4]);
-      pa[0] = Mma<DT>::pack2(p0[0], p0[1]);
-      pa[1] = Mma<DT>::pack2(p0[2], p0[3]);
-      pa[2] = Mma<DT>::pack2(p1[0], p1[1]);
-      pa[3] = Mma<DT>::pack2(p1[2], p1[3]);
+  for (int j = 0; j < D / 32; ++j) qa[j] = *reinterpret_cast<const u32x4*>(&qs[r16 * kQLd + 32 * j + 8 * q4]);
+  const int hg = tid >> 4, part = tid & 15;
+
+  for (int c = c_lo; c < c_hi; ++c) {
+    float ksc[4], vscl[4];
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) {
+      ksc[tt] = I8 ? dword_elem(ksw[tt], shalf[tt], p.scale_dt) : 1.f;
+      vscl[tt] = I8 ? dword_elem(vsw[tt], shalf[tt], p.scale_dt) : 1.f;
     }
-    float sc8[8];
-    if constexpr (I8) {
-      const f32x4 s0 = *reinterpret_cast<const f32x4*>(&vsc[tb]);
-      const f32x4 s1 = *reinterpret_cast<const f32x4*>(&vsc[tb + 4]);
+    // ---- values -> transposed tile (a masked token's values as 0), scales
 #pragma unroll
-      for (int e = 0; e < 4; ++e) { sc8[e] = s0[e]; sc8[4 + e] = s1[e]; }
-    }
+    for (int tt = 0; tt < 4; ++tt) {
+      const int tl = wid * 64 + tt * 16 + r16;
 #pragma unroll
-    for (int dt = 0; dt < D / 16; ++dt) {
-      const int d = 16 * dt + r16;
-      u32x4 vb;
-      if constexpr (I8) {
-        const uint2 w = *reinterpret_cast<const uint2*>(&tile[d * kVtLd + tb]);
-        float vf[8];
+      for (int j = 0; j < D / 32; ++j)
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          const uint32_t ww = e < 4 ? w.x : w.y;
-          vf[e] = Act<DT>::round(opaque(static_cast<float>(static_cast<int8_t>(ww >> (8 * (e & 3)))) * sc8[e]));
+          const int d = 32 * j + 8 * q4 + e;
+          if constexpr (I8) {
+            const uint32_t w = e < 4 ? vc[tt][j].x : vc[tt][j].y;
+            tile[d * kVtLd + tl] = val[tt] ? static_cast<unsigned char>(w >> (8 * (e & 3))) : 0;
+          } else {
+            const uint32_t w = vc[tt][j][e >> 1];
+            reinterpret_cast<uint16_t*>(tile)[d * kVtLd + tl] = val[tt] ? static_cast<uint16_t>(w >> (16 * (e & 1))) : 0;
+          }
         }
-#pragma unroll
-        for (int e = 0; e < 4; ++e) vb[e] = Mma<DT>::pack2(vf[2 * e], vf[2 * e + 1]);
-      } else {
-        vb = *reinterpret_cast<const u32x4*>(&reinterpret_cast<const uint16_t*>(tile)[d * kVtLd + tb]);
-      }
-      oacc[dt] = Mma<DT>::mma(pa, vb, oacc[dt]);
+      if (q4 == 0) vsc[tl] = val[tt] ? vscl[tt] : 0.f;
     }
+    // ---- scores on the MFMA: A = q rows (head r16, dims 32 j + 8 q4 ..), B = keys
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) {
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < D / 32; ++j) {
+        u32x4 kb;
+        if constexpr (I8) {
+          float kf[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const uint32_t w = e < 4 ? kc[tt][j].x : kc[tt][j].y;
+            kf[e] = Act<DT>::round(opaque(static_cast<float>(static_cast<int8_t>(w >> (8 * (e & 3)))) * ksc[tt]));
+          }
+#pragma unroll
+          for (int e = 0; e < 4; ++e) kb[e] = Mma<DT>::pack2(kf[2 * e], kf[2 * e + 1]);
+        } else {
+          kb = kc[tt][j];
+        }
+        acc = Mma<DT>::mma(qa[j], kb, acc);
+      }
+      const int tl = wid * 64 + tt * 16 + r16;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int g = 4 * q4 + e;
+        if (g < G) sp[g * kSpLd + tl] = val[tt] ? acc[e] * p.sm_scale : kNegInf;
+      }
+    }
+    // ---- the next chunk's loads (registers free now), then its table entries' refill
+    if (c + 1 < c_hi) {  // uniform
+      load_kv(c + 1, blk_next);
+      load_bt(c + 2, blk_next);  // (the loads above already hold their row offsets)
+    }
+    __syncthreads();
+
+    // ---- online softmax per head (16 threads a head, DPP row reductions): new running
+    // max, factor rescaling what was summed so far, exp, running sum
+    if (hg < G) {
+      float m = kNegInf;
+#pragma unroll
+      for (int e = 0; e < 16; e += 4) {
+        const f32x4 v = *reinterpret_cast<const f32x4*>(&sp[hg * kSpLd + part * 16 + e]);
+        m = fmaxf(fmaxf(m, fmaxf(v[0], v[1])), fmaxf(v[2], v[3]));
+      }
+      m = row16_max(m);
+      if (part == 0) {
+        const float mo = stat[hg];
+        const float mn = fmaxf(mo, m);
+        stat[32 + hg] = mo == kNegInf ? 0.f : __expf(mo - mn);
+        stat[hg] = mn;
+      }
+    }
+    __syncthreads();
+    for (int g = 0; g < G; ++g) {
+      const float sv = sp[g * kSpLd + tid];
+      sp[g * kSpLd + tid] = sv == kNegInf ? 0.f : __expf(sv - stat[g]);
+    }
+    __syncthreads();
+    if (hg < G) {
+      float l = 0.f;
+#pragma unroll
+      for (int e = 0; e < 16; e += 4) {
+        const f32x4 v = *reinterpret_cast<const f32x4*>(&sp[hg * kSpLd + part * 16 + e]);
+        l += (v[0] + v[1]) + (v[2] + v[3]);
+      }
+      l = row16_sum(l);
+      if (part == 0) stat[16 + hg] = fmaf(stat[16 + hg], stat[32 + hg], l);
+    }
+
+    // ---- value sum on the MFMA: wave w over its 64 tokens in 2 steps of 32, into the
+    // running sums rescaled to the new max (rows g >= G hold nothing used)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float f = stat[32 + ((4 * q4 + e) & 15)];
+#pragma unroll
+      for (int dt = 0; dt < D / 16; ++dt) oacc[dt][e] *= f;
+    }
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
+      const int tb = wid * 64 + st * 32 + 8 * q4;  // the lane's 8 tokens
+      u32x4 pa;
+      {
+        const f32x4 p0 = *reinterpret_cast<const f32x4*>(&sp[r16 * kSpLd + tb]);
+        const f32x4 p1 = *reinterpret_cast<const f32x4*>(&sp[r16 * kSpLd + tb + 4]);
+        pa[0] = Mma<DT>::pack2(p0[0], p0[1]);
+        pa[1] = Mma<DT>::pack2(p0[2], p0[3]);
+        pa[2] = Mma<DT>::pack2(p1[0], p1[1]);
+        pa[3] = Mma<DT>::pack2(p1[2], p1[3]);
+      }
+      float sc8[8];
+      if constexpr (I8) {
+        const f32x4 s0 = *reinterpret_cast<const f32x4*>(&vsc[tb]);
+        const f32x4 s1 = *reinterpret_cast<const f32x4*>(&vsc[tb + 4]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) { sc8[e] = s0[e]; sc8[4 + e] = s1[e]; }
+      }
+#pragma unroll
+      for (int dt = 0; dt < D / 16; ++dt) {
+        const int d = 16 * dt + r16;
+        u32x4 vb;
+        if constexpr (I8) {
+          const uint2 w = *reinterpret_cast<const uint2*>(&tile[d * kVtLd + tb]);
+          float vf[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const uint32_t ww = e < 4 ? w.x : w.y;
+            vf[e] = Act<DT>::round(opaque(static_cast<float>(static_cast<int8_t>(ww >> (8 * (e & 3)))) * sc8[e]));
+          }
+#pragma unroll
+          for (int e = 0; e < 4; ++e) vb[e] = Mma<DT>::pack2(vf[2 * e], vf[2 * e + 1]);
+        } else {
+          vb = *reinterpret_cast<const u32x4*>(&reinterpret_cast<const uint16_t*>(tile)[d * kVtLd + tb]);
+        }
+        oacc[dt] = Mma<DT>::mma(pa, vb, oacc[dt]);
+      }
+    }
+    __syncthreads();  // the tile, scales and probabilities are free for the next chunk
   }
+
 #pragma unroll
   for (int dt = 0; dt < D / 16; ++dt)
 #pragma unroll
@@ -486,7 +587,7 @@ __global__ void __launch_bounds__(kPaNT) paged_attn_mfma_kernel(PagedArgs p) {
     const int g = i / D, d = i - (i / D) * D;
     const float a = (accs[(0 * kPaMaxG + g) * D + d] + accs[(1 * kPaMaxG + g) * D + d]) +
                     (accs[(2 * kPaMaxG + g) * D + d] + accs[(3 * kPaMaxG + g) * D + d]);
-    const float m = stat[g], l = stat[kPaMaxG + g];
+    const float m = stat[g], l = stat[16 + g];
     const int64_t oh = static_cast<int64_t>(b) * p.H + head(g);
     if (p.nsplit == 1) {
       static_cast<S*>(p.out)[oh * D + d] = Act<DT>::from_f32(opaque(a / l));
@@ -548,11 +649,33 @@ bool paged_valu() {
   return e && e[0] == 'v';
 }
 
+// Chunks of kPaNT tokens per workgroup of the MFMA kernel (each split loops over its
+// chunks with the next chunk's loads in flight). Measured on the Qwen2.5-0.5B attention
+// shapes: one chunk per workgroup is fastest up to ~768 (sequence, KV head, chunk)
+// triples, since the per-workgroup chain of dependent loads and barriers is what takes
+// the time; beyond that, or past 16 splits per sequence (the merge kernel then walks many
+// partials), two or more. LSQ_PAGED_CHUNKS=n forces n chunks per split (tuning).
+int paged_chunks_per_split(int64_t pairs, int nchunk) {
+  const char* e = std::getenv("LSQ_PAGED_CHUNKS");
+  const int forced = e ? std::atoi(e) : 0;
+  int64_t cps = forced > 0 ? forced : 1;
+  if (forced <= 0) {
+    const int64_t work = pairs * nchunk;
+    cps = std::max<int64_t>((work + 767) / 768, (nchunk + 15) / 16);
+  }
+  return static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(cps, nchunk)));
+}
+
 template <int DT, bool I8, int D>
-int launch_paged(const PagedArgs& a, hipStream_t s) {
+int launch_paged(const PagedArgs& a0, hipStream_t s) {
+  PagedArgs a = a0;
+  const int nchunk = a.max_sl > 0 ? (a.max_sl + kPaNT - 1) / kPaNT : 1;
+  const bool mfma = DT != LSQ_F32 && !paged_valu();
+  a.cps = mfma ? paged_chunks_per_split(int64_t(a.B) * a.Hkv, nchunk) : 1;
+  a.nsplit = (nchunk + a.cps - 1) / a.cps;
   const dim3 grid(static_cast<unsigned>(a.nsplit), static_cast<unsigned>(a.Hkv), static_cast<unsigned>(a.B));
   if constexpr (DT != LSQ_F32) {
-    if (!paged_valu()) paged_attn_mfma_kernel<DT, I8, D><<<grid, dim3(kPaNT), 0, s>>>(a);
+    if (mfma) paged_attn_mfma_kernel<DT, I8, D><<<grid, dim3(kPaNT), 0, s>>>(a);
     else paged_attn_split_kernel<DT, I8, D><<<grid, dim3(kPaNT), 0, s>>>(a);
   } else {
     paged_attn_split_kernel<DT, I8, D><<<grid, dim3(kPaNT), 0, s>>>(a);

@@ -77,6 +77,11 @@ def paged_attention_decode(
     if max_sl is None:
         max_sl = int(seq_lens.max().item())  # the reference's host read (:97-98)
     tables = sub_tables if sub_tables is not None else block_tables
+    if tables.ndim != 2 or tables.shape[0] < batch_size or tables.shape[1] * block_size < max_sl:
+        # the reference gathers ceil(max_sl / block_size) table entries per sequence
+        raise ValueError(
+            f"paged_attention_decode: block tables of shape {list(tables.shape)} do not cover "
+            f"{batch_size} sequences of max_sl={max_sl} tokens in blocks of {block_size}")
     if tables.dtype != torch.int64:
         tables = tables.to(torch.int64)
     if tables.stride(-1) != 1:

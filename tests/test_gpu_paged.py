@@ -81,6 +81,39 @@ def test_paged_attention_matches_oracle(monkeypatch, kernel, b, h, hkv, d, bs, s
     assert err <= 1e-2
 
 
+@pytest.mark.parametrize("chunks", ["2", "3", "8"])
+@pytest.mark.parametrize("b,h,hkv,d,bs,seqs,int8,dt,mapping", [c for c in CASES if c[7] != "f32"])
+def test_paged_attention_multi_chunk_splits(monkeypatch, chunks, b, h, hkv, d, bs, seqs, int8, dt, mapping):
+    # workgroups that loop over several 256-token chunks (online softmax across chunks,
+    # next chunk's loads in flight), forced for every MFMA case; a split count that does not
+    # divide the chunks leaves a short last split, and 8 chunks puts whole sequences in one
+    print(f"paged chunks={chunks} B={b} H={h} Hkv={hkv} D={d} seqs={seqs} int8={int8} {dt} {mapping}", flush=True)
+    monkeypatch.setenv("LSQ_PAGED_CHUNKS", chunks)
+    q, kp, vp, ks, vs, bt, sl = _case(b + h + d + 1, b, h, hkv, d, bs, seqs, int8, dt)
+    got = _run(q, kp, vp, ks, vs, bt, sl, bs, dt, mapping)
+    ref = qo.paged_attention(q, kp, vp, bt, sl, bs, dt, ks, vs, mapping)
+    err = qo.rel_err(got, ref)
+    print(f"  rel_err={err:.2e}", flush=True)
+    assert err <= 1e-2
+
+
+def test_paged_attention_multi_chunk_mask(monkeypatch):
+    # the engine's mask with two chunks per workgroup: a sequence whose second chunk is
+    # fully masked, and one masked from the start of a chunk
+    monkeypatch.setenv("LSQ_PAGED_CHUNKS", "2")
+    b, h, hkv, d, bs = 3, 14, 2, 64, 16
+    seqs = [300, 256, 1100]
+    q, kp, vp, ks, vs, bt, sl = _case(12, b, h, hkv, d, bs, seqs, True, "bf16")
+    max_sl = max(seqs)
+    m = (np.arange(max_sl)[None, :] < sl[:, None]).reshape(b, 1, 1, max_sl)
+    mask = np.repeat(m, hkv, axis=0)
+    got = _run(q, kp, vp, ks, vs, bt, sl, bs, "bf16", mask=mask, max_sl=max_sl)
+    ref = qo.paged_attention(q, kp, vp, bt, sl, bs, "bf16", ks, vs, "contiguous")
+    assert qo.rel_err(got, ref) <= 1e-2
+    plain = _run(q, kp, vp, ks, vs, bt, sl, bs, "bf16")
+    assert np.array_equal(got, plain)
+
+
 def test_paged_attention_engine_mask_and_reference_ground_truth():
     # the engine passes a repeat_interleave'd [B * Hkv, 1, 1, max_sl] mask
     # (model_runner.py:138-143); and the reference's ground truth (gather, dequantize,
@@ -127,3 +160,5 @@ def test_paged_attention_validation():
     with pytest.raises(NotImplementedError):
         paged_attention_decode(torch.zeros(2, 4, 2, 64, device=DEV, dtype=torch.float16),
                                kp.half(), kp.half(), bt, sl)
+    with pytest.raises(ValueError, match="do not cover"):  # 2 blocks of 16 < 40 tokens
+        paged_attention_decode(q, kp.half(), kp.half(), bt, sl, max_sl=40)
