@@ -398,22 +398,27 @@ __global__ void __launch_bounds__(NT) gemm_kernel(LinearArgs p) {
 }
 
 // ---------------------------------------------------------------------------------------
-// Register-weight variant. A workgroup of 4 waves computes a 128 x 256 tile; two such
-// workgroups share a CU (one wave of each per SIMD), each with its own barrier, so one
-// workgroup's barrier and LDS latency bubbles are filled by the other's MFMAs. Wave w
-// owns columns [64 w, 64 w + 64) for all 128 rows (4 x 2 blocks of 32 x 32). Only the
+// Register-weight variant. A workgroup of 4 waves computes a 128 x 128 tile (128 x 256
+// selectable, half the workgroups); two such workgroups share a CU (one wave of
+// each per SIMD), each with its own barrier, so one workgroup's barrier and LDS latency
+// bubbles are filled by the other's MFMAs. Wave w owns columns [64 w, 64 w + 64) (or
+// [32 w, 32 w + 32)) for all 128 rows (4 x 2 or 4 x 1 blocks of 32 x 32). Only the
 // activations go through LDS (two 16 KB stages, DMA one step ahead); each wave loads its
-// own 64 weight rows straight into registers in MFMA operand order (three steps in
-// flight) and dequantizes them right before use, so weight tiles never touch LDS.
+// own weight rows straight into registers in MFMA operand order (three steps in flight)
+// and dequantizes them right before use, so weight tiles never touch LDS.
 // K order inside a step: lane l at 16-column sub-step kk multiplies columns
 // 32 (l >> 5) + 8 kk .. +7 (the same permutation on both operands), which makes each
 // lane's weights one contiguous 32-column chunk per step.
-constexpr int RBM = 128, RBN = 256, RNT = 256;
-constexpr int RFM = RBM / 32, RFN = 2;
+constexpr int RBM = 128, RNT = 256;
+constexpr int RFM = RBM / 32;
 constexpr int kRLdsBytes = 2 * RBM * BK * 2;
 
-template <int DT, int KIND, bool GROUPED>
+// RFN_ 32-column blocks per wave: 2 (128 x 256 tiles) or 1 (128 x 128 tiles, twice the
+// workgroups, for layers whose 128 x 256 tiles would leave CUs idle).
+template <int DT, int KIND, bool GROUPED, int RFN_>
 __global__ void __launch_bounds__(RNT, 2) gemm_rw_kernel(LinearArgs p) {
+  constexpr int RFN = RFN_;
+  constexpr int RBN = 4 * 32 * RFN;
   constexpr bool W4 = KIND == kW4Tiled || KIND == kW4Canon;
   constexpr bool TILED = KIND == kW4Tiled || KIND == kW8Tiled;
   constexpr int WLB = W4 ? 1 : 2;  // 16-byte loads per lane per 32-row block per step
@@ -494,7 +499,7 @@ __global__ void __launch_bounds__(RNT, 2) gemm_rw_kernel(LinearArgs p) {
   int lr[RFN];
 #pragma unroll
   for (int j = 0; j < RFN; ++j) {
-    lr[j] = 64 * wid + 32 * j + (lane & 31);
+    lr[j] = 32 * RFN * wid + 32 * j + (lane & 31);
     woff[j] = TILED ? static_cast<uint32_t>((lr[j] >> 4) * nkt * tb + ((lr[j] & 15) + 16 * h) * 16)
                     : static_cast<uint32_t>(lr[j] * (W4 ? K / 2 : K) + (W4 ? 16 : 32) * h);
   }
@@ -634,8 +639,18 @@ __global__ void __launch_bounds__(RNT, 2) gemm_rw_kernel(LinearArgs p) {
 
 template <int DT, int KIND, bool GROUPED>
 int launch_rw(const LinearArgs& a, hipStream_t s) {
-  const int64_t tiles = ((a.M + RBM - 1) / RBM) * ((a.N + RBN - 1) / RBN);
-  gemm_rw_kernel<DT, KIND, GROUPED><<<dim3(static_cast<unsigned>(tiles)), dim3(RNT), kRLdsBytes, s>>>(a);
+  const int64_t mt = (a.M + RBM - 1) / RBM;
+  const int64_t wide = mt * ((a.N + 255) / 256);
+  // 128-column tiles measured faster at every size this kernel serves (14336 x 4096:
+  // M=256 77 -> 55 us, M=768 136 -> 130 us); LSQ_GEMM_RW_N=2 forces 256 (tests, tuning).
+  const char* e = std::getenv("LSQ_GEMM_RW_N");
+  const bool narrow = !(e && e[0] == '2');
+  if (narrow) {
+    const int64_t tiles = mt * ((a.N + 127) / 128);
+    gemm_rw_kernel<DT, KIND, GROUPED, 1><<<dim3(static_cast<unsigned>(tiles)), dim3(RNT), kRLdsBytes, s>>>(a);
+  } else {
+    gemm_rw_kernel<DT, KIND, GROUPED, 2><<<dim3(static_cast<unsigned>(wide)), dim3(RNT), kRLdsBytes, s>>>(a);
+  }
   return static_cast<int>(hipGetLastError());
 }
 
