@@ -639,7 +639,8 @@ struct Cfg {
   X(1, 2, 4, 8)               \
   X(1, 1, 4, 8)               \
   X(1, 4, 4, 4)               \
-  X(1, 8, 1, 6)
+  X(1, 8, 1, 6)               \
+  X(1, 6, 2, 4)
 
 int g_max_lds = -1;
 
@@ -669,10 +670,9 @@ bool env_cfg(Cfg* out) {
   return state == 2;
 }
 
-// Every wave streams one row tile over one K slice. Large layers: one slice per row
-// tile, 8 row tiles per workgroup (1184 waves at N = 18944 already keep enough bytes in
-// flight). Small layers: split K so that there are at least ~1024 waves, each with at
-// least a few k tiles.
+// Every wave streams one row tile over one K slice. Large layers: at most one workgroup
+// per CU, 2 K slices per row tile where that still fits (see below). Small layers: split K
+// so that there are at least ~1024 waves, each with at least a few k tiles.
 Cfg pick_cfg(int kind, int64_t M, int64_t N, int64_t K) {
   Cfg c;
   if (env_cfg(&c)) return c;
@@ -681,7 +681,14 @@ Cfg pick_cfg(int kind, int64_t M, int64_t N, int64_t K) {
   const int64_t nkt = K / kTileK;
   // INT8 moves twice the bytes per tile and keeps a 6-step ring busy (measured 3-7 %
   // faster than 4 at 18944 x 3584); INT4 is fastest with 4.
-  if (nrt >= 1024) return (kind == kW8 || kind == kW8Tiled) ? Cfg{1, 8, 1, 6} : Cfg{1, 8, 1, 4};
+  // Large N: up to 1536 row tiles (N <= 24576), 6 row tiles x 2 K slices per workgroup
+  // keep every workgroup on its own CU (198 at N = 18944, 12 waves each); measured 9-14 %
+  // faster than 8 row tiles of unsplit K (148 workgroups, 108 CUs idle) at 18944 x 3584,
+  // INT8 and INT4, M = 1 to 16. Beyond that, 8 row tiles of unsplit K.
+  if (nrt >= 1024) {
+    if (nrt <= 6 * 256 && nkt >= 8) return Cfg{1, 6, 2, 4};
+    return (kind == kW8 || kind == kW8Tiled) ? Cfg{1, 8, 1, 6} : Cfg{1, 8, 1, 4};
+  }
   // Fewer than 8 k tiles (K < 1024, e.g. hidden 896): split K 4 ways over pairs of row
   // tiles (N up to ~8K), 2 ways over 4 row tiles above; measured 20-26 % faster than 8 row
   // tiles of unsplit K at 896 x 896 and 4864 x 896 (M = 1 and 32), which launch 7-38
