@@ -40,7 +40,7 @@ constexpr int kD = 8;   // weight ring depth in k tiles; a multiple of 2 * kCT
 // workgroup's scales and bias as fp32 rounded to the activation type; the cross-slice
 // partial sums.
 struct MbLds {
-  int64_t xs, xsum, ss, sb, red, total;
+  int64_t xs, xsum, ss, sb, red, dummy, total;
   int ldxs;
 };
 
@@ -52,7 +52,8 @@ __host__ __device__ inline MbLds mb_lds(int mp, int rows, int64_t ngs, int ks, i
   l.ss = l.xsum + int64_t(ks) * 2 * kCT * mp * 4;
   l.sb = l.ss + align16(rows * ngs * 4);
   l.red = l.sb + align16(rows * 4);
-  l.total = l.red + int64_t(red_floats) * 4;
+  l.dummy = l.red + int64_t(red_floats) * 4;  // 16-byte sink for stores of padding threads
+  l.total = l.dummy + 32;
   return l;
 }
 
@@ -69,9 +70,8 @@ __global__ void __launch_bounds__(64 * RG * KS) decode_mb_kernel(LinearArgs p) {
   constexpr int ROWS = RG * kTileN;
   constexpr int PIECES = kCT * kTileK / 8;    // 16-byte pieces per chunk row
   constexpr int SP = MP * PIECES;             // pieces per slice per chunk
-  constexpr int XL = KS * SP / NT;            // activation loads per thread per chunk
+  constexpr int XL = (KS * SP + NT - 1) / NT;  // activation loads per thread per chunk
   constexpr int RED = KS > 1 ? (KS - 1) * RG * MB * 4 * 64 : 0;
-  static_assert(KS * SP % NT == 0, "chunk pieces must split evenly over the threads");
   static_assert(kD % (2 * kCT) == 0, "the ring block must hold whole pairs of chunks");
   extern __shared__ __align__(16) unsigned char smem[];
   using S = typename Act<DT>::storage;
@@ -166,7 +166,7 @@ __global__ void __launch_bounds__(64 * RG * KS) decode_mb_kernel(LinearArgs p) {
       const int j = i - sl * SP;
       const int m = j / PIECES;
       const int k = (kt_lo(sl) + c * kCT) * kTileK + (j - m * PIECES) * 8;
-      xr[set][u] = bload16<0>(rx, (m < M && k < kt_lo(sl + 1) * kTileK && c < nchunks)
+      xr[set][u] = bload16<0>(rx, (i < KS * SP && m < M && k < kt_lo(sl + 1) * kTileK && c < nchunks)
                                        ? static_cast<uint32_t>((m * p.ldx + k) * 2) : kOOB);
     }
   };
@@ -187,8 +187,10 @@ __global__ void __launch_bounds__(64 * RG * KS) decode_mb_kernel(LinearArgs p) {
       const int m = j / PIECES;
       const int pc = j - m * PIECES;
       const u32x4 v = xr[set][u];
+      const bool ok = i < KS * SP;  // padding threads store into the sink (no branch)
       uint16_t* xb = xs + ((sl * 2 + b) * MP + m) * ldxs;
-      *reinterpret_cast<u32x4*>(xb + pc * 8) = KIND == kW4Canon ? permute_canon(v) : v;
+      u32x4* dst = ok ? reinterpret_cast<u32x4*>(xb + pc * 8) : reinterpret_cast<u32x4*>(smem + L.dummy);
+      *dst = KIND == kW4Canon ? permute_canon(v) : v;
       if (W4) {
         float sum = 0.f;
 #pragma unroll
@@ -197,7 +199,7 @@ __global__ void __launch_bounds__(64 * RG * KS) decode_mb_kernel(LinearArgs p) {
         // (every lane of the row stores the same value: a store from one lane in 16 would
         // be a divergent branch, at which the compiler drains all global loads in flight)
         sum = row16_sum(sum);
-        xsum[((sl * 2 + b) * kCT + pc / 16) * MP + m] = sum;
+        *(ok ? &xsum[((sl * 2 + b) * kCT + pc / 16) * MP + m] : reinterpret_cast<float*>(smem + L.dummy)) = sum;
       }
     }
   };
@@ -374,6 +376,10 @@ MbCfg pick_mb(int64_t N, int mb) {
   }
   if (env == 4 || env == 8) return MbCfg{env, 1};
   const int64_t nrt = (N + kTileN - 1) / kTileN;
+  // up to 32 tokens and 1536 row tiles: 6 row tiles x 2 K slices, one workgroup per CU
+  // (198 at N = 18944; measured 9-17 % faster than 148 of 8 x 1 at 32 tokens; 64 tokens
+  // would need more registers than 12 waves per CU leave)
+  if (mb == 2 && nrt >= 8 * 128 && nrt <= 6 * 256) return MbCfg{6, 2};
   if (nrt >= 8 * 128) return MbCfg{8, 1};
   if (nrt >= 256) return MbCfg{4, 1};
   return MbCfg{2, mb == 2 ? 4 : 2};
@@ -404,6 +410,7 @@ template <int DT, int KIND, bool GROUPED>
 int launch_kind(const LinearArgs& a, hipStream_t s) {
   if (a.M <= 32) {
     const MbCfg c = pick_mb(a.N, 2);
+    if (c.rg == 6) return launch_one<DT, KIND, 2, 6, 2, GROUPED>(a, s);
     if (c.ks == 4) return launch_one<DT, KIND, 2, 2, 4, GROUPED>(a, s);
     return c.rg == 8 ? launch_one<DT, KIND, 2, 8, 1, GROUPED>(a, s) : launch_one<DT, KIND, 2, 4, 1, GROUPED>(a, s);
   }

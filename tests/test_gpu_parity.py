@@ -193,10 +193,11 @@ def test_int8_decode_config_shape(m, layout, monkeypatch):
     _check_layer("int8", 18944, 3584, m, rows=rows)
 
 
-@pytest.mark.parametrize("m", [1, 16, 64])
+@pytest.mark.parametrize("m", [1, 16, 17, 32, 64])
 @pytest.mark.parametrize("layout", ["tiled", "canonical"])
 def test_int4_g128_decode_config_shape(m, layout, monkeypatch):
-    """INT4 group-128 decode at 18944x3584, M in {1, 16, 64}, both weight layouts."""
+    """INT4 group-128 decode at 18944x3584, M in {1, 16, 64} and the chunked kernel's
+    6 x 2 workgroups at 17 and 32 tokens, both weight layouts."""
     monkeypatch.setenv("LSQ_WEIGHT_LAYOUT", layout)
     rows = np.sort(np.random.default_rng(m).choice(18944, 512, replace=False))
     _check_layer("int4", 18944, 3584, m, rows=rows)
