@@ -337,14 +337,6 @@ __global__ void __launch_bounds__(kPaNT) paged_attn_mfma_kernel(PagedArgs p) {
     stat[32 + tid] = 0.f;
   }
   const int seq = static_cast<int>(p.sl[b]);
-  auto valid_tok = [&](int t) -> bool {
-    if (t >= p.max_sl) return false;
-    if (p.mask) {
-      const int row = b * p.mask_rows_per_b + (p.mask_rows_per_b > 1 ? kvh : 0);
-      return p.mask[static_cast<int64_t>(row) * p.ldm + t] != 0;
-    }
-    return t < seq;
-  };
 
   // This workgroup's chunks of kPaNT tokens: [c_lo, c_hi). Each chunk is loaded while the
   // previous one finishes: its block-table entries one chunk ahead, its keys, values and
