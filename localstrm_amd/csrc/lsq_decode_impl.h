@@ -743,6 +743,7 @@ int launch_kind(const LinearArgs& a, hipStream_t s) {
     LSQ_TRY_MB(1, 4, 2, 8)
     LSQ_TRY_MB(1, 2, 4, 4)
     LSQ_TRY_MB(1, 1, 8, 4)
+    LSQ_TRY_MB(1, 6, 2, 4)
 #undef LSQ_TRY_MB
     return a.M <= 32 ? launch_one<DT, KIND, 1, 8, 1, 4, GROUPED, 2, A8>(a, s)
                      : launch_one<DT, KIND, 1, 8, 1, 4, GROUPED, 4, A8>(a, s);

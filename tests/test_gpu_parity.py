@@ -203,6 +203,15 @@ def test_int4_g128_decode_config_shape(m, layout, monkeypatch):
     _check_layer("int4", 18944, 3584, m, rows=rows)
 
 
+@pytest.mark.parametrize("m", [17, 33, 64])
+@pytest.mark.parametrize("kind", ["int8", "int4"])
+def test_decode_large_n_small_k_token_blocks(kind, m):
+    """18944 x 1024: 1184 row tiles over 8 k tiles take the 6 x 2 workgroups, here with
+    the 17..64-token blocks (activations resident in LDS); oracle on 512 rows."""
+    rows = np.sort(np.random.default_rng(100 + m).choice(18944, 512, replace=False))
+    _check_layer(kind, 18944, 1024, m, rows=rows, bias=(m % 2 == 1))
+
+
 @pytest.mark.parametrize("m", [256, 2048])
 @pytest.mark.parametrize("layout", ["tiled", "canonical"])
 def test_int4_g128_prefill_config_shape(m, layout, monkeypatch):

@@ -225,6 +225,21 @@ def test_w8a8_linear_bit_exact(dt, m, n, k):
     assert mism == 0, f"{mism} of {got.size} outputs differ"
 
 
+@pytest.mark.parametrize("m", [1, 8, 17, 33, 64])
+def test_w8a8_linear_bit_exact_large_n(m):
+    # N = 18944 (1184 row tiles) at K = 1024: the 6 x 2 workgroups of the decode kernel,
+    # with the 17..64-token blocks
+    n, k = 18944, 1024
+    _say(f"w8a8 large N bf16 M={m} N={n} K={k}")
+    x, wq, sw, bias = _lin_inputs("bf16", m, n, k)
+    y, _, _ = _linear(x.to(DEV), wq, sw, bias)
+    ref = qo.w8a8_linear(x.float().numpy(), wq.numpy(), sw.numpy(),
+                         None if bias is None else bias.float().numpy(), "bf16")
+    got = y.float().cpu().numpy()
+    mism = np.count_nonzero(_bits(got) != _bits(ref))
+    assert mism == 0, f"{mism} of {got.size} outputs differ"
+
+
 @pytest.mark.parametrize("dt", ["bf16", "f16", "f32"])
 @pytest.mark.parametrize("m,n,k", [(1, 272, 896), (5, 1000, 896), (16, 272, 2048), (64, 272, 896)])
 def test_w8a8_unfused_decode_bit_exact(monkeypatch, dt, m, n, k):
