@@ -1,12 +1,13 @@
-// Decode-shaped weight-only GEMM for small batches, 16 < M <= 64 tokens (gfx950).
+// Decode-shaped weight-only GEMM for small batches whose activations do not fit in LDS,
+// M <= 64 tokens (gfx950).
 //
 // GPU form of QuantizedLinear.forward (src/kernels/quantization.py:129-141) for batched
 // decode steps. Same weight stream and in-register unpack as lsq_decode_impl.h: each wave
 // owns one 16-row tile of W and one of KS K slices, streams its tiles once from HBM
 // through a ring of kD k-tile steps in registers, and turns them into the B operands of
-// v_mfma_f32_16x16x32. What changes is the activation side: 17..64 tokens of a layer
-// with large K no longer fit in LDS at once, so the workgroup streams x through LDS in
-// chunks of kCT k tiles per slice, double-buffered, with one barrier per chunk. Every
+// v_mfma_f32_16x16x32. What changes is the activation side: the tokens of a layer with
+// large K no longer fit in LDS at once (17 at K = 3584, 4 at K = 18944), so the workgroup
+// streams x (padded to 32 or 64 rows) through LDS in chunks of kCT k tiles per slice, double-buffered, with one barrier per chunk. Every
 // token block of 16 (MB of them) reuses each unpacked weight operand, so the unpack cost
 // per weight is shared by up to 64 tokens. Small-N layers split K into KS slices so that
 // more waves stream; the slices' partial sums are added through LDS in slice order.
@@ -37,8 +38,9 @@ constexpr int kD = 8;   // weight ring depth in k tiles; a multiple of 2 * kCT
 
 // LDS layout shared by kernel and host: per K slice, two activation chunk buffers (mp rows
 // of kCT * 128 columns, row stride ldxs elements) and their per-(k tile, token) sums; the
-// workgroup's scales and bias as fp32 rounded to the activation type; the cross-slice
-// partial sums.
+// workgroup's scales as T (round_T(s) is a T value, so 16 bits hold it exactly; at
+// K = 18944 that leaves room for 4 K slices) and its bias as round_T fp32; the
+// cross-slice partial sums.
 struct MbLds {
   int64_t xs, xsum, ss, sb, red, dummy, total;
   int ldxs;
@@ -50,7 +52,7 @@ __host__ __device__ inline MbLds mb_lds(int mp, int rows, int64_t ngs, int ks, i
   l.xs = 0;
   l.xsum = align16(int64_t(ks) * 2 * mp * l.ldxs * 2);
   l.ss = l.xsum + int64_t(ks) * 2 * kCT * mp * 4;
-  l.sb = l.ss + align16(rows * ngs * 4);
+  l.sb = l.ss + align16(rows * ngs * 2);
   l.red = l.sb + align16(rows * 4);
   l.dummy = l.red + int64_t(red_floats) * 4;  // 16-byte sink for stores of padding threads
   l.total = l.dummy + 32;
@@ -96,7 +98,7 @@ __global__ void __launch_bounds__(64 * RG * KS) decode_mb_kernel(LinearArgs p) {
   const int ldxs = L.ldxs;
   uint16_t* xs = reinterpret_cast<uint16_t*>(smem + L.xs);
   float* xsum = reinterpret_cast<float*>(smem + L.xsum);
-  float* ss = reinterpret_cast<float*>(smem + L.ss);
+  S* ss = reinterpret_cast<S*>(smem + L.ss);
   float* sb = reinterpret_cast<float*>(smem + L.sb);
   float* red = reinterpret_cast<float*>(smem + L.red);
 
@@ -137,10 +139,10 @@ __global__ void __launch_bounds__(64 * RG * KS) decode_mb_kernel(LinearArgs p) {
                                      : static_cast<const uint8_t*>(p.scale),
                               p.bias ? static_cast<uint32_t>((rows_valid * es_b + 3) & ~3) : 0u);
 
-  // ---- scales and bias of the workgroup's rows -> LDS, as round_T fp32
+  // ---- scales (as T) and bias (round_T fp32) of the workgroup's rows -> LDS
   for (int t = tid; t < nsc; t += NT) {
     const uint32_t eb = static_cast<uint32_t>(t * es_s);
-    ss[t] = Act<DT>::round(dword_elem(bload4(rs, eb & ~3u), (eb >> 1) & 1, p.scale_dt));
+    ss[t] = Act<DT>::from_f32(Act<DT>::round(dword_elem(bload4(rs, eb & ~3u), (eb >> 1) & 1, p.scale_dt)));
   }
   if (p.bias) {
     for (int t = tid; t < rows_valid; t += NT) {
@@ -231,7 +233,7 @@ __global__ void __launch_bounds__(64 * RG * KS) decode_mb_kernel(LinearArgs p) {
   uint32_t nib_mask, magic;  // INT4 unpack constants in registers (VOP3 takes no literal)
   asm volatile("v_mov_b32 %0, 0x000f000f" : "=v"(nib_mask));
   asm volatile("v_mov_b32 %0, %1" : "=v"(magic) : "i"(Mma<DT>::kMagic));
-  const float* srow = ss + (rg * kTileN + r) * ngs;
+  const S* srow = ss + (rg * kTileN + r) * ngs;
 
   const int nblocks = (nchunks * kCT + kD - 1) / kD;
   for (int b = 0; b < nblocks; ++b) {
@@ -279,7 +281,7 @@ __global__ void __launch_bounds__(64 * RG * KS) decode_mb_kernel(LinearArgs p) {
         }
         if (GROUPED) {
           const uint32_t kt = static_cast<uint32_t>(my_lo + st);
-          sc = srow[gtiles == 1 ? kt : __umulhi(kt, gmagic)];
+          sc = Act<DT>::to_f32(srow[gtiles == 1 ? kt : __umulhi(kt, gmagic)]);
         }
         if (W4) {
           f32x4 dacc[MB];
@@ -331,7 +333,7 @@ __global__ void __launch_bounds__(64 * RG * KS) decode_mb_kernel(LinearArgs p) {
   const int rl = rg * kTileN + r;
   const int n = row0 + rl;
   if (n < N) {
-    const float sc = GROUPED ? 1.f : ss[rl];
+    const float sc = GROUPED ? 1.f : Act<DT>::to_f32(ss[rl]);
     const float bias = p.bias ? sb[rl] : 0.f;
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb)
@@ -368,7 +370,7 @@ struct MbCfg {
   int rg, ks;
 };
 
-MbCfg pick_mb(int64_t N, int mb) {
+MbCfg pick_mb(int64_t N, int64_t K, int mb) {
   static int env = -1;
   if (env < 0) {
     const char* e = std::getenv("LSQ_DECODE_MB_RG");
@@ -381,7 +383,11 @@ MbCfg pick_mb(int64_t N, int mb) {
   // would need more registers than 12 waves per CU leave)
   if (mb == 2 && nrt >= 8 * 128 && nrt <= 6 * 256) return MbCfg{6, 2};
   if (nrt >= 8 * 128) return MbCfg{8, 1};
-  if (nrt >= 256) return MbCfg{4, 1};
+  // 4 row tiles of unsplit K while that still makes ~200 workgroups or K is short (under
+  // 32 k tiles); otherwise split K: INT4 4096 x 14336 at 4-32 tokens 65-68 -> 32-34 us
+  // with 128 workgroups of 2 x 4 instead of 64 of 4 x 1
+  const int64_t nkt = K / kTileK;
+  if (nrt >= 256 && (nkt < 32 || nrt >= 800)) return MbCfg{4, 1};
   return MbCfg{2, mb == 2 ? 4 : 2};
 }
 
@@ -406,17 +412,26 @@ int launch_one(const LinearArgs& a, hipStream_t s) {
   return static_cast<int>(hipGetLastError());
 }
 
+// The staged group scales grow with K (rows x K / group floats), so at large K a split
+// configuration can exceed LDS: then fewer K slices (2, then 1 with 4 row tiles) are
+// tried before the caller falls back to the prefill GEMM.
 template <int DT, int KIND, bool GROUPED>
 int launch_kind(const LinearArgs& a, hipStream_t s) {
+  int rc = LSQ_E_LAYOUT;
   if (a.M <= 32) {
-    const MbCfg c = pick_mb(a.N, 2);
-    if (c.rg == 6) return launch_one<DT, KIND, 2, 6, 2, GROUPED>(a, s);
-    if (c.ks == 4) return launch_one<DT, KIND, 2, 2, 4, GROUPED>(a, s);
-    return c.rg == 8 ? launch_one<DT, KIND, 2, 8, 1, GROUPED>(a, s) : launch_one<DT, KIND, 2, 4, 1, GROUPED>(a, s);
+    const MbCfg c = pick_mb(a.N, a.K, 2);
+    if (c.rg == 6) rc = launch_one<DT, KIND, 2, 6, 2, GROUPED>(a, s);
+    else if (c.ks == 4) rc = launch_one<DT, KIND, 2, 2, 4, GROUPED>(a, s);
+    else rc = c.rg == 8 ? launch_one<DT, KIND, 2, 8, 1, GROUPED>(a, s) : launch_one<DT, KIND, 2, 4, 1, GROUPED>(a, s);
+    if (rc == LSQ_E_LAYOUT && c.ks == 4) rc = launch_one<DT, KIND, 2, 2, 2, GROUPED>(a, s);
+    if (rc == LSQ_E_LAYOUT && c.ks > 1) rc = launch_one<DT, KIND, 2, 4, 1, GROUPED>(a, s);
+    return rc;
   }
-  const MbCfg c = pick_mb(a.N, 4);
-  if (c.ks == 2) return launch_one<DT, KIND, 4, 2, 2, GROUPED>(a, s);
-  return c.rg == 8 ? launch_one<DT, KIND, 4, 8, 1, GROUPED>(a, s) : launch_one<DT, KIND, 4, 4, 1, GROUPED>(a, s);
+  const MbCfg c = pick_mb(a.N, a.K, 4);
+  if (c.ks == 2) rc = launch_one<DT, KIND, 4, 2, 2, GROUPED>(a, s);
+  else rc = c.rg == 8 ? launch_one<DT, KIND, 4, 8, 1, GROUPED>(a, s) : launch_one<DT, KIND, 4, 4, 1, GROUPED>(a, s);
+  if (rc == LSQ_E_LAYOUT && c.ks > 1) rc = launch_one<DT, KIND, 4, 4, 1, GROUPED>(a, s);
+  return rc;
 }
 
 }  // namespace

@@ -6,8 +6,8 @@
 //
 //  * decode (lsq_decode_impl.h): M <= 64, fp16/bf16, K % 128 == 0, all activations staged in
 //    LDS once (the common decode case; up to 64 tokens when x fits in LDS);
-//  * chunked decode (lsq_decode_mb.hip): 16 < M <= 64 when x does not fit, activations
-//    streamed through LDS;
+//  * chunked decode (lsq_decode_mb.hip): M <= 64 when x does not fit (large K, e.g. 4
+//    tokens at K = 18944 or 17 at K = 3584), activations streamed through LDS;
 //  * prefill GEMM (lsq_gemm.hip): M > 64 (and the shapes above that fit neither decode),
 //    two MFMA kernels chosen by M;
 //  * generic kernel (below): any dtype / shape / group size, exact per-element dequant and
@@ -125,11 +125,11 @@ static int dispatch(bool w4, const void* x, int64_t ldx, const uint8_t* w, const
       LinearArgs a{x, ldx, tiled ? tiled : w, scale, scale_dt, bias, bias_dt, y, ldy,
                    M, N, K, group, ng};
       const int kind = w4 ? (tiled ? kW4Tiled : kW4Canon) : (tiled ? kW8Tiled : kW8);
-      // decode with all activations in LDS; else (more than 16 tokens) the chunked decode;
-      // else the prefill GEMM
+      // decode with all activations in LDS; else (x too large for LDS, e.g. 4 tokens at
+      // K = 18944) the chunked decode; else the prefill GEMM
       int rc = LSQ_E_LAYOUT;
       if (M <= 64) rc = launch_decode<DT>(kind, a, s);
-      if (rc == LSQ_E_LAYOUT && M > 16 && M <= 64) rc = launch_decode_mb<DT>(kind, a, s);
+      if (rc == LSQ_E_LAYOUT && M <= 64) rc = launch_decode_mb<DT>(kind, a, s);
       if (rc == LSQ_E_LAYOUT && M > 16) rc = launch_gemm<DT>(kind, a, s);
       if (rc != LSQ_E_LAYOUT) return rc;
     }

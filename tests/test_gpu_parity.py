@@ -212,6 +212,22 @@ def test_decode_large_n_small_k_token_blocks(kind, m):
     _check_layer(kind, 18944, 1024, m, rows=rows, bias=(m % 2 == 1))
 
 
+@pytest.mark.parametrize("m", [2, 4, 8, 16, 24, 33, 64])
+@pytest.mark.parametrize("kind", ["int8", "int4"])
+def test_decode_large_k_small_n(kind, m):
+    """Down-projection shape 3584 x 18944: x of 4+ tokens exceeds LDS, so the chunked decode
+    serves every M here (with fewer K slices when the staged group scales need the room);
+    oracle on 256 rows."""
+    rows = np.sort(np.random.default_rng(200 + m).choice(3584, 256, replace=False))
+    _check_layer(kind, 3584, 18944, m, rows=rows, bias=(m % 2 == 0), seed=m)
+
+
+@pytest.mark.parametrize("m", [9, 16])
+def test_decode_qwen05b_down_proj_16_tokens(m):
+    """896 x 4864 (Qwen2.5-0.5B down_proj) at 9 and 16 tokens: chunked decode."""
+    _check_layer("int4", 896, 4864, m, bias=True, seed=m)
+
+
 @pytest.mark.parametrize("m", [256, 2048])
 @pytest.mark.parametrize("layout", ["tiled", "canonical"])
 def test_int4_g128_prefill_config_shape(m, layout, monkeypatch):
