@@ -379,8 +379,9 @@ constexpr int64_t kFusedMaxElems = 16384;
 
 // M <= 64: the decode kernel quantizing x itself when x is small (above) and fits its
 // first load batch; otherwise x is quantized by act_quant_kernel and the decode kernel
-// streams x_q while it fits in LDS, else runs in blocks of 32 or 16 tokens (the weights
-// are streamed once per block). M > 64, or no block fits: the GEMM on x_q.
+// streams x_q while it fits in LDS, else runs in blocks of 32, 16, 8, 4 or 2 tokens (the
+// weights are streamed once per block, at most 8 blocks). M > 64, or no block fits: the
+// GEMM on x_q.
 template <int DT>
 int run_w8a8(const LinearArgs& ax, const LinearArgs& a, hipStream_t s) {
   const bool gemm = path_is("gemm");
@@ -398,8 +399,11 @@ int run_w8a8(const LinearArgs& ax, const LinearArgs& a, hipStream_t s) {
     rc = launch_decode_a8<DT>(a, false, s);
     if (rc != LSQ_E_LAYOUT) return rc;
     using Sy = typename Act<DT>::storage;
-    for (int64_t blk : {int64_t(32), int64_t(16)}) {
-      if (blk >= a.M) continue;
+    // At most 8 passes over W: at small N the GEMM launches few workgroups (14 at
+    // N = 3584), and 8 passes of the decode kernel still beat it (3584 x 18944, 8 tokens
+    // in 2 blocks of 4: 263 -> ~52 us).
+    for (int64_t blk : {int64_t(32), int64_t(16), int64_t(8), int64_t(4), int64_t(2)}) {
+      if (blk >= a.M || (a.M + blk - 1) / blk > 8) continue;
       LinearArgs b = a;
       b.M = blk;
       rc = launch_decode_a8<DT>(b, false, s);  // block 0; LSQ_E_LAYOUT: does not fit, nothing ran
