@@ -7,7 +7,7 @@
 // through a ring of kD k-tile steps in registers, and turns them into the B operands of
 // v_mfma_f32_16x16x32. What changes is the activation side: the tokens of a layer with
 // large K no longer fit in LDS at once (17 at K = 3584, 4 at K = 18944), so the workgroup
-// streams x (padded to 32 or 64 rows) through LDS in chunks of kCT k tiles per slice, double-buffered, with one barrier per chunk. Every
+// streams x (padded to 16, 32 or 64 rows) through LDS in chunks of kCT k tiles per slice, double-buffered, with one barrier per chunk. Every
 // token block of 16 (MB of them) reuses each unpacked weight operand, so the unpack cost
 // per weight is shared by up to 64 tokens. Small-N layers split K into KS slices so that
 // more waves stream; the slices' partial sums are added through LDS in slice order.
@@ -365,7 +365,7 @@ int mb_max_lds() {
 // Workgroup shape (row tiles RG x K slices KS): 8 row tiles when that still leaves
 // enough workgroups (one pass over x serves 128 rows), 4 for mid-size N; small N (fewer
 // than 256 row tiles) splits K so that more waves stream the weights (4 slices of 2 row
-// tiles for 32 tokens, 2 for 64, within LDS). LSQ_DECODE_MB_RG=4|8 forces RG (tuning).
+// tiles up to 32 tokens, 2 for 64, within LDS). LSQ_DECODE_MB_RG=4|8 forces RG (tuning).
 struct MbCfg {
   int rg, ks;
 };
@@ -418,6 +418,15 @@ int launch_one(const LinearArgs& a, hipStream_t s) {
 template <int DT, int KIND, bool GROUPED>
 int launch_kind(const LinearArgs& a, hipStream_t s) {
   int rc = LSQ_E_LAYOUT;
+  if (a.M <= 16) {  // one block of 16 tokens (3584 x 18944, INT4: 41 -> 27 us against two)
+    const MbCfg c = pick_mb(a.N, a.K, 2);
+    if (c.rg == 6) rc = launch_one<DT, KIND, 1, 6, 2, GROUPED>(a, s);
+    else if (c.ks == 4) rc = launch_one<DT, KIND, 1, 2, 4, GROUPED>(a, s);
+    else rc = c.rg == 8 ? launch_one<DT, KIND, 1, 8, 1, GROUPED>(a, s) : launch_one<DT, KIND, 1, 4, 1, GROUPED>(a, s);
+    if (rc == LSQ_E_LAYOUT && c.ks == 4) rc = launch_one<DT, KIND, 1, 2, 2, GROUPED>(a, s);
+    if (rc == LSQ_E_LAYOUT && c.ks > 1) rc = launch_one<DT, KIND, 1, 4, 1, GROUPED>(a, s);
+    return rc;
+  }
   if (a.M <= 32) {
     const MbCfg c = pick_mb(a.N, a.K, 2);
     if (c.rg == 6) rc = launch_one<DT, KIND, 2, 6, 2, GROUPED>(a, s);
