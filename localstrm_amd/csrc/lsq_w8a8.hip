@@ -374,8 +374,14 @@ bool path_is(const char* want) {
 
 // Every workgroup of the fused decode quantizes all of x again, which costs more than
 // the separate quantization launch once a workgroup's share passes ~16K activations
-// (measured: 18944 x 3584 gains 3.5 us at M = 1, loses 2.4 us at M = 8).
+// (measured: 18944 x 3584 gains 3.5 us at M = 1, loses 2.4 us at M = 8). One or two
+// long rows still gain (3584 x 18944: M = 1 24.0 -> 18.4 us, M = 2 25.6 -> 23.5 us;
+// 4096 x 14336 at M = 4 loses 6 us).
 constexpr int64_t kFusedMaxElems = 16384;
+constexpr int64_t kFusedMaxElemsTwoRows = 40960;
+bool fuse_quant(int64_t M, int64_t K) {
+  return M * K <= kFusedMaxElems || (M <= 2 && M * K <= kFusedMaxElemsTwoRows);
+}
 
 // M <= 64: the decode kernel quantizing x itself when x is small (above) and fits its
 // first load batch; otherwise x is quantized by act_quant_kernel and the decode kernel
@@ -385,7 +391,7 @@ constexpr int64_t kFusedMaxElems = 16384;
 template <int DT>
 int run_w8a8(const LinearArgs& ax, const LinearArgs& a, hipStream_t s) {
   const bool gemm = path_is("gemm");
-  const bool fused = path_is("fused") || (ax.M * ax.K <= kFusedMaxElems && !path_is("unfused"));
+  const bool fused = path_is("fused") || (fuse_quant(ax.M, ax.K) && !path_is("unfused"));
   if (a.M <= 64 && !gemm && fused) {
     const int rc = launch_decode_a8<DT>(ax, true, s);
     if (rc != LSQ_E_LAYOUT) return rc;

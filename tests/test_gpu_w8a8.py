@@ -240,11 +240,13 @@ def test_w8a8_linear_bit_exact_large_n(m):
     assert mism == 0, f"{mism} of {got.size} outputs differ"
 
 
-@pytest.mark.parametrize("m,n,k", [(3, 3584, 18944), (8, 3584, 18944), (13, 3584, 18944),
+@pytest.mark.parametrize("m,n,k", [(1, 3584, 18944), (2, 3584, 18944), (3, 3584, 18944),
+                                   (8, 3584, 18944), (13, 3584, 18944),
                                    (16, 4096, 14336), (64, 4096, 14336)])
 def test_w8a8_large_k_token_blocks(m, n, k):
-    # x_q of 8+ tokens at K = 18944 exceeds LDS: blocks of 4 (2 passes at M = 8, 4 at
-    # M = 13 with a ragged last block), of 8 at K = 14336
+    # 1-2 long rows: quantized inside the decode kernel; x_q of 8+ tokens at K = 18944
+    # exceeds LDS: blocks of 4 (2 passes at M = 8, 4 at M = 13 with a ragged last
+    # block), of 8 at K = 14336
     _say(f"w8a8 large K blocks bf16 M={m} N={n} K={k}")
     x, wq, sw, bias = _lin_inputs("bf16", m, n, k)
     y, _, _ = _linear(x.to(DEV), wq, sw, bias)
