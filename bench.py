@@ -18,7 +18,8 @@ copy, see --calibrate-copy) and recorded in profiles/decode_int8_m1_18944x3584.t
 
 `sweep` reports the other shapes of the same metric (INT8 M in {8,32,64}, INT4 group-128
 decode M in {1,16,64} at 18944x3584, INT4 group-128 prefill M in {256,2048,8192} at
-14336x4096 in TFLOP/s, the single INT8 layer 4864x896 at M=1, and one batch-32 decode step
+14336x4096 in TFLOP/s, the single INT8 layer 4864x896 at M=1, INT4 group-128 decode M in
+{1,16} at the transposed 3584x18944 shape, W8A8 layers, and one batch-32 decode step
 through the 168 INT4 projections of a Qwen2.5-0.5B-architecture stack); `cpu_baseline`
 times the reference's CPU path (dequantize, then F.linear, on the host cores) on the
 headline shape.
@@ -505,6 +506,9 @@ def main() -> int:
             sweep.append(bench_decode("int4", 14336, 4096, m, max(10, args.steps // 20),
                                       max(2, args.warmup // 4), device))
         sweep.append(bench_decode("int8", 4864, 896, 1, args.steps, args.warmup, device))
+        # the transposed (down-projection) shape, whose activations exceed LDS from 4 tokens
+        for m in (1, 16):
+            sweep.append(bench_decode("int4", K, N, m, args.steps, args.warmup, device))
         for m in (1, 64):
             sweep.append(bench_decode("w8a8", N, K, m, args.steps, args.warmup, device))
         sweep.append(bench_decode("w8a8", 14336, 4096, 2048, max(10, args.steps // 20),
