@@ -49,6 +49,13 @@ int launch_decode(int kind, const LinearArgs& a, hipStream_t s);
 template <int DT>
 int launch_decode_a8(const LinearArgs& a, bool fused, hipStream_t s);
 
+// Decode GEMV for 1..16 tokens on the tiled INT4 / INT8 layouts (lsq_gemv.hip): whole row
+// tiles per workgroup, balanced over the grid. Returns LSQ_E_LAYOUT without launching
+// anything for shapes, layouts or modes it does not cover (canonical layouts, the SiLU.mul
+// epilogue, W8A8, activations too large for LDS).
+template <int DT>
+int launch_gemv(int kind, const LinearArgs& a, hipStream_t s);
+
 // Batched decode, 16 < M <= 64 tokens (activations streamed through LDS in chunks).
 // Same contract as launch_decode.
 template <int DT>

@@ -4,6 +4,8 @@
 // reference materializes W = dequantize(x.dtype) and then calls F.linear. This file holds
 // the C entry points and the dispatch between the kernels; none materializes W in HBM:
 //
+//  * decode GEMV (lsq_gemv.hip): M <= 16 on the tiled layouts, whole row tiles per
+//    workgroup balanced over the grid;
 //  * decode (lsq_decode_impl.h): M <= 64, fp16/bf16, K % 128 == 0, all activations staged in
 //    LDS once (the common decode case; up to 64 tokens when x fits in LDS);
 //  * chunked decode (lsq_decode_mb.hip): M <= 64 when x does not fit (large K, e.g. 4
@@ -128,7 +130,8 @@ static int dispatch(bool w4, const void* x, int64_t ldx, const uint8_t* w, const
       // decode with all activations in LDS; else (x too large for LDS, e.g. 4 tokens at
       // K = 18944) the chunked decode; else the prefill GEMM
       int rc = LSQ_E_LAYOUT;
-      if (M <= 64) rc = launch_decode<DT>(kind, a, s);
+      if (M <= 16) rc = launch_gemv<DT>(kind, a, s);
+      if (rc == LSQ_E_LAYOUT && M <= 64) rc = launch_decode<DT>(kind, a, s);
       if (rc == LSQ_E_LAYOUT && M <= 64) rc = launch_decode_mb<DT>(kind, a, s);
       if (rc == LSQ_E_LAYOUT && M > 16) rc = launch_gemm<DT>(kind, a, s);
       if (rc != LSQ_E_LAYOUT) return rc;
