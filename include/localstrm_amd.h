@@ -108,7 +108,8 @@ int lsq_w8_untile(const int8_t* tiled, int8_t* weight_q, int64_t N, int64_t K, v
  * (src/kernels/quantization.py:129-141). x and y have dtype `dtype`, row strides ldx and
  * ldy (elements); bias is NULL or [N] of bias_dtype (rounded to `dtype` first, as
  * quantization.py:135-140 casts it). `tiled` is NULL or the output of lsq_w8_retile for
- * the same weights; when given, the decode kernels stream it instead of weight_q. */
+ * the same weights; when given, every kernel reads it instead of weight_q, and weight_q
+ * may be NULL (a module on a GPU keeps only the tiled copy). */
 int lsq_w8_linear(const void* x, int64_t ldx, const int8_t* weight_q, const int8_t* tiled,
                   const void* scale, int scale_dtype, const void* bias, int bias_dtype, void* y,
                   int64_t ldy, int dtype, int64_t M, int64_t N, int64_t K, void* stream);
@@ -116,8 +117,9 @@ int lsq_w8_linear(const void* x, int64_t ldx, const int8_t* weight_q, const int8
 /* y[M, N] = x[M, K] @ dequant(W4)^T + round_T(bias).
  * Replaces QuantizedLinear.forward for quant_type "int4"
  * (src/kernels/quantization.py:129-141), extended with group-wise scales.
- * `tiled` is NULL or the output of lsq_w4_retile for the same weights; when given, the
- * decode kernels stream it instead of weight_packed. */
+ * `tiled` is NULL or the output of lsq_w4_retile for the same weights; when given, every
+ * kernel reads it instead of weight_packed, and weight_packed may be NULL (a module on a
+ * GPU keeps only the tiled copy). */
 int lsq_w4_linear(const void* x, int64_t ldx, const uint8_t* weight_packed,
                   const uint8_t* tiled, const void* scale, int scale_dtype,
                   int64_t group_size, const void* bias, int bias_dtype, void* y, int64_t ldy,
@@ -197,8 +199,11 @@ int lsq_w8a8_linear(const void* x, int64_t ldx, const int8_t* tiled, const void*
  * [num_blocks, block_size, Hkv, D] of kv_dtype (LSQ_I8 with k_scales / v_scales
  * [num_blocks, block_size, Hkv] of scale_dtype, or the query's dtype with NULL scales),
  * block_tables int64 [B, >= ceil(max_seq_len / block_size)] (row stride bt_stride),
- * seq_lens int64 [B]. A token t of sequence b attends when t < max_seq_len and, without a
- * mask, t < seq_lens[b]; with a mask (bool bytes, row stride mask_stride, one row per
+ * seq_lens int64 [B]. A table entry e < 0 stands for block e + num_blocks (Python
+ * indexing, as the reference's gather k_cache_pool[sub_tables]); an entry outside
+ * [-num_blocks, num_blocks) masks its token (the reference's gather would raise
+ * IndexError there). A token t of sequence b attends when its entry is in range,
+ * t < max_seq_len and, without a mask, t < seq_lens[b]; with a mask (bool bytes, row stride mask_stride, one row per
  * sequence or, mask_rows_per_b = Hkv, one per (sequence, KV head) as the reference's
  * repeat_interleave'd mask), when mask[row][t]. head_mapping 0: query head h uses KV head
  * h / (H / Hkv) ("contiguous"); 1: h % Hkv ("interleaved"). Keys / values are dequantized
@@ -214,8 +219,8 @@ int lsq_paged_attention_decode(const void* query, const void* k_pool, const void
                                const int64_t* seq_lens, const uint8_t* mask, int64_t mask_stride,
                                int64_t mask_rows_per_b, void* out, int dtype, int64_t B,
                                int64_t H, int64_t Hkv, int64_t D, int64_t block_size,
-                               int64_t max_seq_len, int head_mapping, void* workspace,
-                               int64_t workspace_bytes, void* stream);
+                               int64_t num_blocks, int64_t max_seq_len, int head_mapping,
+                               void* workspace, int64_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

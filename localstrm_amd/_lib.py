@@ -58,7 +58,7 @@ SIGNATURES = {
     "lsq_paged_attention_decode": (
         _int,
         [_vp, _vp, _vp, _int, _vp, _vp, _int, _vp, _i64, _vp, _vp, _i64, _i64, _vp, _int, _i64,
-         _i64, _i64, _i64, _i64, _i64, _int, _vp, _i64, _vp],
+         _i64, _i64, _i64, _i64, _i64, _i64, _int, _vp, _i64, _vp],
     ),
     "lsq_w8a8_tiled_bytes": (_i64, [_i64, _i64]),
     "lsq_w8a8_retile": (_int, [_vp, _vp, _i64, _i64, _vp]),

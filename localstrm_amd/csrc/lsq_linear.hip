@@ -29,12 +29,30 @@ namespace lsq {
 
 constexpr int kGenMB = 8;  // activation rows per wavefront
 
+// Byte offset of weight (n, k) in the tiled layouts (lsq_internal.h), and for INT4 which
+// nibble of that byte (1 = high) holds it.
+__device__ __forceinline__ int64_t tiled_w4_byte(int64_t n, int64_t k, int64_t nkt, int* hi) {
+  const int c = static_cast<int>(k & (kTileK - 1));
+  const int e = c & 7;
+  const int p = (e & 1) ? 4 + (e >> 1) : (e >> 1);  // nibble position with tiled_nibble_k(p) == e
+  const int lane = (c >> 5) * 16 + static_cast<int>(n & (kTileN - 1));
+  *hi = p & 1;
+  return ((n / kTileN) * nkt + k / kTileK) * kTileBytes + lane * 16 + ((c >> 3) & 3) * 4 + (p >> 1);
+}
+
+__device__ __forceinline__ int64_t tiled_w8_byte(int64_t n, int64_t k, int64_t nkt) {
+  const int c = static_cast<int>(k & (kTileK - 1));
+  const int lane = (c >> 5) * 16 + static_cast<int>(n & (kTileN - 1));
+  return ((n / kTileN) * nkt + k / kTileK) * kTileBytes8 + ((c >> 4) & 1) * 1024 + lane * 16 + (c & 15);
+}
+
+// `tiled` (optional): the weights in the tiled layout, read instead of `w` when given.
 template <int DT, bool W4>
 __global__ void __launch_bounds__(256) linear_generic_kernel(
     const typename Act<DT>::storage* __restrict__ x, int64_t ldx, const void* __restrict__ w,
-    const void* __restrict__ scale, int scale_dt, int64_t group, const void* __restrict__ bias,
-    int bias_dt, typename Act<DT>::storage* __restrict__ y, int64_t ldy, int64_t M, int64_t N,
-    int64_t K) {
+    const uint8_t* __restrict__ tiled, const void* __restrict__ scale, int scale_dt, int64_t group,
+    const void* __restrict__ bias, int bias_dt, typename Act<DT>::storage* __restrict__ y,
+    int64_t ldy, int64_t M, int64_t N, int64_t K) {
   const int lane = threadIdx.x & 63;
   const int64_t n = blockIdx.x * 4 + (threadIdx.x >> 6);
   const int64_t m0 = blockIdx.y * (int64_t)kGenMB;
@@ -43,15 +61,18 @@ __global__ void __launch_bounds__(256) linear_generic_kernel(
   float acc[kGenMB];
 #pragma unroll
   for (int i = 0; i < kGenMB; ++i) acc[i] = 0.f;
+  const int64_t nkt = K / kTileK;
   for (int64_t k = lane; k < K; k += 64) {
     int q;
     float s;
     if (W4) {
-      const uint8_t byte = static_cast<const uint8_t*>(w)[n * ((K + 1) / 2) + (k >> 1)];
-      q = static_cast<int>((k & 1) ? (byte >> 4) : (byte & 0xF)) - 8;
+      int hi = static_cast<int>(k & 1);
+      const uint8_t byte = tiled ? tiled[tiled_w4_byte(n, k, nkt, &hi)]
+                                 : static_cast<const uint8_t*>(w)[n * ((K + 1) / 2) + (k >> 1)];
+      q = static_cast<int>(hi ? (byte >> 4) : (byte & 0xF)) - 8;
       s = load_as_f32(scale, scale_dt, n * ng + k / group);
     } else {
-      q = static_cast<const int8_t*>(w)[n * K + k];
+      q = tiled ? static_cast<int8_t>(tiled[tiled_w8_byte(n, k, nkt)]) : static_cast<const int8_t*>(w)[n * K + k];
       s = load_as_f32(scale, scale_dt, n);
     }
     const float wv = dequant_elem<DT>(q, Act<DT>::round(s));
@@ -71,29 +92,30 @@ __global__ void __launch_bounds__(256) linear_generic_kernel(
 // ------------------------------------------------------------ generic launch
 
 template <int DT>
-static int launch_generic(bool w4, const void* x, int64_t ldx, const void* w, const void* scale,
-                          int scale_dt, int64_t group, const void* bias, int bias_dt, void* y,
-                          int64_t ldy, int64_t M, int64_t N, int64_t K, hipStream_t s) {
+static int launch_generic(bool w4, const void* x, int64_t ldx, const void* w, const uint8_t* tiled,
+                          const void* scale, int scale_dt, int64_t group, const void* bias, int bias_dt,
+                          void* y, int64_t ldy, int64_t M, int64_t N, int64_t K, hipStream_t s) {
   using S = typename Act<DT>::storage;
   const dim3 grid(static_cast<unsigned>((N + 3) / 4), static_cast<unsigned>((M + kGenMB - 1) / kGenMB));
   if (grid.y > 65535u) return LSQ_E_SHAPE;
   if (w4)
-    linear_generic_kernel<DT, true><<<grid, 256, 0, s>>>(static_cast<const S*>(x), ldx, w, scale,
+    linear_generic_kernel<DT, true><<<grid, 256, 0, s>>>(static_cast<const S*>(x), ldx, w, tiled, scale,
                                                          scale_dt, group, bias, bias_dt,
                                                          static_cast<S*>(y), ldy, M, N, K);
   else
-    linear_generic_kernel<DT, false><<<grid, 256, 0, s>>>(static_cast<const S*>(x), ldx, w, scale,
+    linear_generic_kernel<DT, false><<<grid, 256, 0, s>>>(static_cast<const S*>(x), ldx, w, tiled, scale,
                                                           scale_dt, group, bias, bias_dt,
                                                           static_cast<S*>(y), ldy, M, N, K);
   return static_cast<int>(hipGetLastError());
 }
 
-static int check_common(const void* x, int64_t ldx, const void* w, const void* scale, void* y,
-                        int64_t ldy, int dtype, int bias_dt, const void* bias, int64_t M,
+static int check_common(const void* x, int64_t ldx, const void* w, const void* tiled, const void* scale,
+                        void* y, int64_t ldy, int dtype, int bias_dt, const void* bias, int64_t M,
                         int64_t N, int64_t K) {
   // An empty x or y (M, N or K zero) may come with a NULL data pointer, as torch gives
-  // for zero-element tensors; such a pointer is never dereferenced.
-  if (!w || !scale) return LSQ_E_NULL;
+  // for zero-element tensors; such a pointer is never dereferenced. The canonical weights
+  // may be NULL when the tiled copy is given.
+  if ((!w && !tiled) || !scale) return LSQ_E_NULL;
   if ((!x && M > 0 && K > 0) || (!y && M > 0 && N > 0)) return LSQ_E_NULL;
   if (M < 0 || N < 0 || K < 0 || ldx < K || ldy < N) return LSQ_E_SHAPE;
   if (N > INT32_MAX / 2 || K > INT32_MAX / 2 || M > INT32_MAX / 2) return LSQ_E_SHAPE;
@@ -114,8 +136,8 @@ static int dispatch(bool w4, const void* x, int64_t ldx, const uint8_t* w, const
                     int act = LSQ_ACT_NONE) {
   const int64_t ng = (K + group - 1) / group;
   if constexpr (DT != LSQ_F32) {
-    const bool mfma_ok = K % kTileK == 0 && x_aligned16(x, ldx) &&
-                         (reinterpret_cast<uintptr_t>(w) & 15) == 0;
+    const void* wf = tiled ? static_cast<const void*>(tiled) : static_cast<const void*>(w);
+    const bool mfma_ok = K % kTileK == 0 && x_aligned16(x, ldx) && (reinterpret_cast<uintptr_t>(wf) & 15) == 0;
     if (act != LSQ_ACT_NONE) {  // the fused epilogue exists in the decode kernel only
       if (!mfma_ok || M > 64) return LSQ_E_LAYOUT;
       LinearArgs a{x, ldx, tiled ? tiled : w, scale, scale_dt, bias, bias_dt, y, ldy,
@@ -138,8 +160,8 @@ static int dispatch(bool w4, const void* x, int64_t ldx, const uint8_t* w, const
     }
   }
   if (act != LSQ_ACT_NONE) return LSQ_E_LAYOUT;
-  return launch_generic<DT>(w4, x, ldx, w, scale, scale_dt, group, bias, bias_dt, y, ldy, M, N, K,
-                            s);
+  return launch_generic<DT>(w4, x, ldx, w, tiled, scale, scale_dt, group, bias, bias_dt, y, ldy, M, N,
+                            K, s);
 }
 
 // ============================================================ SiLU.mul over interleaved rows
@@ -197,7 +219,7 @@ static int w8_linear(const void* x, int64_t ldx, const int8_t* weight_q, const i
                      const void* scale, int scale_dtype, const void* bias, int bias_dtype, void* y,
                      int64_t ldy, int dtype, int64_t M, int64_t N, int64_t K, void* stream, int act) {
   const int64_t ny = act == LSQ_ACT_SILU_MUL ? N / 2 : N;  // output columns
-  const int rc = check_common(x, ldx, weight_q, scale, y, ldy, dtype, bias_dtype, bias, M, ny, K);
+  const int rc = check_common(x, ldx, weight_q, tiled, scale, y, ldy, dtype, bias_dtype, bias, M, ny, K);
   if (rc != LSQ_OK) return rc;
   if (act != LSQ_ACT_NONE && (act != LSQ_ACT_SILU_MUL || N % 32 != 0)) return LSQ_E_LAYOUT;
   if (scale_dtype != LSQ_F32 && scale_dtype != LSQ_F16 && scale_dtype != LSQ_BF16) return LSQ_E_DTYPE;
@@ -236,7 +258,7 @@ static int w4_linear(const void* x, int64_t ldx, const uint8_t* weight_packed, c
                      int bias_dtype, void* y, int64_t ldy, int dtype, int64_t M, int64_t N, int64_t K,
                      void* stream, int act) {
   const int64_t ny = act == LSQ_ACT_SILU_MUL ? N / 2 : N;  // output columns
-  const int rc = check_common(x, ldx, weight_packed, scale, y, ldy, dtype, bias_dtype, bias, M, ny, K);
+  const int rc = check_common(x, ldx, weight_packed, tiled, scale, y, ldy, dtype, bias_dtype, bias, M, ny, K);
   if (rc != LSQ_OK) return rc;
   if (act != LSQ_ACT_NONE && (act != LSQ_ACT_SILU_MUL || N % 32 != 0)) return LSQ_E_LAYOUT;
   if (group_size < 1) return LSQ_E_GROUP;

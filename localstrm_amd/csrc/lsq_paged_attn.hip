@@ -51,6 +51,7 @@ struct PagedArgs {
   int scale_dt;
   const int64_t* bt;      // block tables, row stride ldbt
   int64_t ldbt;
+  int64_t nb;             // blocks in the pools: a table entry outside [-nb, nb) masks its token
   const int64_t* sl;      // sequence lengths [B]
   const uint8_t* mask;    // optional boolean mask rows (row stride ldm), else sl decides
   int64_t ldm;
@@ -145,8 +146,9 @@ __global__ void __launch_bounds__(kPaNT) paged_attn_split_kernel(PagedArgs p) {
   // The block table entry is read for every token below max_seq_len (the table holds
   // ceil(max_seq_len / block_size) entries per sequence), so its load does not wait for
   // the sequence length; only valid tokens use it.
-  const int64_t blk = t < p.max_sl ? p.bt[static_cast<int64_t>(b) * p.ldbt + t / p.BS] : 0;
-  const bool valid = valid_tok(t);
+  int64_t blk = t < p.max_sl ? p.bt[static_cast<int64_t>(b) * p.ldbt + t / p.BS] : 0;
+  if (blk < 0) blk += p.nb;  // a negative entry counts from the end, as Python indexing does
+  const bool valid = valid_tok(t) && blk >= 0 && blk < p.nb;
   int my_row = -1;
   if (valid) my_row = static_cast<int>((blk * p.BS + t % p.BS) * p.Hkv + kvh);
   const int64_t lrow = my_row < 0 ? 0 : my_row;
@@ -351,17 +353,20 @@ __global__ void __launch_bounds__(kPaNT) paged_attn_mfma_kernel(PagedArgs p) {
   // the sequence length, and only valid tokens use them.
   // The loads are unconditional (tokens past max_seq_len read the last column, and are
   // masked later): a load under a per-lane condition makes the compiler wait for it at
-  // the end of the condition. Block indices are below 2^31 (pool rows are), so the low
-  // dword of each entry is enough.
-  const int32_t* btw = reinterpret_cast<const int32_t*>(p.bt);
-  auto load_bt = [&](int c, int (&blk)[4]) {
+  // the end of the condition. An entry outside [-nb, nb) becomes -1 (its token is masked);
+  // a negative one counts from the end, as Python indexing does.
+  auto load_bt = [&](int c, int64_t (&blk)[4]) {
     if (c < c_hi) {  // uniform; then max_seq_len > 0
 #pragma unroll
       for (int tt = 0; tt < 4; ++tt) {
         const int t = min(tok(c, tt), p.max_sl - 1);
-        blk[tt] = btw[2 * (static_cast<int64_t>(b) * p.ldbt + t / p.BS)];
+        blk[tt] = p.bt[static_cast<int64_t>(b) * p.ldbt + t / p.BS];
       }
     }
+  };
+  auto block_of = [&](int64_t e) -> int {
+    const int64_t i = e < 0 ? e + p.nb : e;
+    return (i >= 0 && i < p.nb) ? static_cast<int>(i) : -1;
   };
   using Chunk = typename std::conditional<I8, uint2, u32x4>::type;  // 8 elements
   Chunk kc[4][D / 32], vc[4][D / 32];
@@ -372,7 +377,7 @@ __global__ void __launch_bounds__(kPaNT) paged_attn_mfma_kernel(PagedArgs p) {
   // past the last, reads row 0 and its results are discarded).
   // No load here sits inside a data-dependent branch, so all of them are in flight
   // together (mask bytes first, then rows, scales, keys and values).
-  auto load_kv = [&](int c, const int (&blk)[4]) {
+  auto load_kv = [&](int c, const int64_t (&blk)[4]) {
     const bool live = c < c_hi;
     unsigned char mk[4] = {1, 1, 1, 1};
     if (p.mask && live) {  // uniform; a mask row holds max_seq_len entries
@@ -384,8 +389,9 @@ __global__ void __launch_bounds__(kPaNT) paged_attn_mfma_kernel(PagedArgs p) {
 #pragma unroll
     for (int tt = 0; tt < 4; ++tt) {
       const int t = tok(c, tt);
-      val[tt] = live && t < p.max_sl && (p.mask ? mk[tt] != 0 : t < seq);
-      row[tt] = val[tt] ? (blk[tt] * p.BS + t % p.BS) * p.Hkv + kvh : 0;
+      const int bi = block_of(blk[tt]);
+      val[tt] = live && t < p.max_sl && (p.mask ? mk[tt] != 0 : t < seq) && bi >= 0;
+      row[tt] = val[tt] ? (bi * p.BS + t % p.BS) * p.Hkv + kvh : 0;
     }
     if constexpr (I8) {
 #pragma unroll
@@ -406,7 +412,7 @@ __global__ void __launch_bounds__(kPaNT) paged_attn_mfma_kernel(PagedArgs p) {
       }
     }
   };
-  int blk_next[4] = {0, 0, 0, 0};
+  int64_t blk_next[4] = {0, 0, 0, 0};
   load_bt(c_lo, blk_next);
   load_kv(c_lo, blk_next);
   load_bt(c_lo + 1, blk_next);
@@ -704,14 +710,18 @@ extern "C" int lsq_paged_attention_decode(
     const void* v_scales, int scale_dtype, const int64_t* block_tables, int64_t bt_stride,
     const int64_t* seq_lens, const uint8_t* mask, int64_t mask_stride, int64_t mask_rows_per_b,
     void* out, int dtype, int64_t B, int64_t H, int64_t Hkv, int64_t D, int64_t block_size,
-    int64_t max_seq_len, int head_mapping, void* workspace, int64_t workspace_bytes, void* stream) {
+    int64_t num_blocks, int64_t max_seq_len, int head_mapping, void* workspace, int64_t workspace_bytes,
+    void* stream) {
   const bool dt_ok = dtype == LSQ_F32 || dtype == LSQ_F16 || dtype == LSQ_BF16;
   const bool i8 = kv_dtype == LSQ_I8;
   if (!dt_ok || (!i8 && kv_dtype != dtype)) return LSQ_E_DTYPE;
   if (i8 && scale_dtype != LSQ_F32 && scale_dtype != LSQ_F16 && scale_dtype != LSQ_BF16) return LSQ_E_DTYPE;
   if (B < 0 || H < 1 || Hkv < 1 || H % Hkv != 0 || H / Hkv > kPaMaxG || (D != 64 && D != 128) ||
-      block_size < 1 || max_seq_len < 0 || bt_stride < (max_seq_len + block_size - 1) / block_size)
+      block_size < 1 || num_blocks < 0 || max_seq_len < 0 ||
+      bt_stride < (max_seq_len + block_size - 1) / block_size)
     return LSQ_E_SHAPE;
+  // pool rows (block, slot, KV head) are addressed with 32 bits
+  if (num_blocks * block_size * Hkv >= (int64_t(1) << 31)) return LSQ_E_SHAPE;
   if (mask && (mask_rows_per_b != 1 && mask_rows_per_b != Hkv)) return LSQ_E_SHAPE;
   if (mask && mask_stride < max_seq_len) return LSQ_E_SHAPE;
   if (B == 0) return LSQ_OK;
@@ -725,7 +735,7 @@ extern "C" int lsq_paged_attention_decode(
     return LSQ_E_NULL;
   PagedArgs a{};
   a.q = query; a.kp = k_pool; a.vp = v_pool; a.ks = k_scales; a.vs = v_scales;
-  a.scale_dt = scale_dtype; a.bt = block_tables; a.ldbt = bt_stride; a.sl = seq_lens;
+  a.scale_dt = scale_dtype; a.bt = block_tables; a.ldbt = bt_stride; a.nb = num_blocks; a.sl = seq_lens;
   a.mask = mask; a.ldm = mask_stride; a.mask_rows_per_b = static_cast<int>(mask_rows_per_b);
   a.out = out; a.ws = static_cast<float*>(workspace);
   a.B = static_cast<int>(B); a.H = static_cast<int>(H); a.Hkv = static_cast<int>(Hkv);

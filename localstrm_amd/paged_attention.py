@@ -6,7 +6,10 @@ contiguous tensors, dequantizes an INT8 cache (keys.to(T) * k_scales), expands t
 heads and calls F.scaled_dot_product_attention; here lsq_paged_attention_decode reads the
 pool through the block table directly (no gather, no dequantized copy). Decode only: one
 query token per sequence (query [B, H, 1, D]), head_dim 64 or 128, at most 16 query heads
-per KV head; on a CPU tensor it raises (no CPU path).
+per KV head; on a CPU tensor it raises (no CPU path). Block-table entries: a negative one
+counts from the end of the pool (Python indexing, as the reference's gather does); one
+outside [-num_blocks, num_blocks) masks its token (it contributes nothing) where the
+reference's gather would raise IndexError, which a kernel cannot do without a host sync.
 """
 
 from __future__ import annotations
@@ -74,6 +77,9 @@ def paged_attention_decode(
     if not int8_kv and (k_cache_pool.dtype != query.dtype or v_cache_pool.dtype != query.dtype):
         raise ValueError("paged_attention_decode: a non-INT8 KV cache must have the query's dtype")
 
+    if seq_lens.numel() < batch_size:
+        raise ValueError(f"paged_attention_decode: seq_lens has {seq_lens.numel()} entries for "
+                         f"{batch_size} sequences")
     if max_sl is None:
         max_sl = int(seq_lens.max().item())  # the reference's host read (:97-98)
     tables = sub_tables if sub_tables is not None else block_tables
@@ -112,7 +118,7 @@ def paged_attention_decode(
             _lib.dtype_code(ks.dtype) if int8_kv else 0, tables.data_ptr(), tables.stride(0),
             lens.data_ptr(), _lib.ptr(mask), mask_ld, mask_rows, out.data_ptr(),
             _lib.dtype_code(query.dtype), batch_size, num_heads, num_kv_heads, head_dim, block_size,
-            max_sl, 0 if head_mapping == "contiguous" else 1, _lib.ptr(ws), wbytes,
+            k_cache_pool.shape[0], max_sl, 0 if head_mapping == "contiguous" else 1, _lib.ptr(ws), wbytes,
             _lib.stream_handle(query.device))
     _lib.check(rc, "lsq_paged_attention_decode")
     return out

@@ -162,3 +162,47 @@ def test_paged_attention_validation():
                                kp.half(), kp.half(), bt, sl)
     with pytest.raises(ValueError, match="do not cover"):  # 2 blocks of 16 < 40 tokens
         paged_attention_decode(q, kp.half(), kp.half(), bt, sl, max_sl=40)
+
+
+@pytest.mark.parametrize("kernel", ["mfma", "valu"])
+def test_paged_attention_out_of_range_block_ids(monkeypatch, kernel):
+    """Block-table entries past each sequence's length may hold anything: -1 pads, ids at
+    or above the pool size, huge values. They are read (the table is read up to max_sl)
+    but must neither fault nor change the result; an in-range negative entry counts from
+    the end of the pool. Inside a sequence, an out-of-range entry masks its tokens."""
+    if kernel == "valu":
+        monkeypatch.setenv("LSQ_PAGED_KERNEL", "valu")
+    b, h, hkv, d, bs = 3, 14, 2, 64, 16
+    seqs = [40, 300, 513]
+    q, kp, vp, ks, vs, bt, sl = _case(77, b, h, hkv, d, bs, seqs, True, "f16")
+    nb = kp.shape[0]
+    ref = qo.paged_attention(q, kp, vp, bt, sl, bs, "f16", ks, vs, "contiguous")
+    bad = bt.copy()
+    junk = [-1, nb, nb + 7, 2 ** 40, -(2 ** 40)]
+    for i, n in enumerate(seqs):
+        used = -(-n // bs)
+        for j in range(used, bad.shape[1]):
+            bad[i, j] = junk[(i + j) % len(junk)]
+    got = _run(q, kp, vp, ks, vs, bad, sl, bs, "f16", max_sl=int(max(seqs)))
+    assert qo.rel_err(got, ref) <= 1e-2
+    # an in-range negative entry names the same block as its positive form
+    neg = bt.copy()
+    neg[1, 2] -= nb
+    got_neg = _run(q, kp, vp, ks, vs, neg, sl, bs, "f16")
+    assert qo.rel_err(got_neg, ref) <= 1e-2
+    # an out-of-range entry inside sequence 2: its 16 tokens are masked
+    hole = bt.copy()
+    hole[2, 3] = nb + 1
+    mask = np.zeros((b, int(max(seqs))), dtype=np.uint8)
+    for i, n in enumerate(seqs):
+        mask[i, :n] = 1
+    mask[2, 3 * bs:4 * bs] = 0
+    ref_hole = qo.paged_attention(q, kp, vp, bt, sl, bs, "f16", ks, vs, "contiguous", mask=mask)
+    got_hole = _run(q, kp, vp, ks, vs, hole, sl, bs, "f16")
+    assert qo.rel_err(got_hole, ref_hole) <= 1e-2
+
+
+def test_paged_attention_rejects_short_seq_lens():
+    q, kp, vp, ks, vs, bt, sl = _case(5, 3, 4, 2, 64, 16, [20, 30, 40], True, "f16")
+    with pytest.raises(ValueError, match="seq_lens"):
+        _run(q, kp, vp, ks, vs, bt, sl[:2], 16, "f16", max_sl=40)

@@ -228,11 +228,12 @@ def test_decode_qwen05b_down_proj_16_tokens(m):
     _check_layer("int4", 896, 4864, m, bias=True, seed=m)
 
 
-@pytest.mark.parametrize("m", [256, 2048])
+@pytest.mark.parametrize("m", [256, 2048, 8192])
 @pytest.mark.parametrize("layout", ["tiled", "canonical"])
 def test_int4_g128_prefill_config_shape(m, layout, monkeypatch):
-    """INT4 group-128 prefill GEMM at the Llama-3-8B MLP shape 14336x4096, M in {256, 2048};
-    oracle on 256 sampled output columns and (for M=2048) 256 sampled rows."""
+    """INT4 group-128 prefill GEMM at the Llama-3-8B MLP shape 14336x4096, M in
+    {256, 2048, 8192}; oracle on 256 sampled output columns and (for M > 256) 256 sampled
+    rows."""
     monkeypatch.setenv("LSQ_WEIGHT_LAYOUT", layout)
     n, k = 14336, 4096
     p, s, x = bench.make_int4(n, k, m, 128, seed=m)

@@ -87,3 +87,35 @@ def test_silu_mul_f32_and_autograd():
     assert xg.grad is not None and xg.grad.shape == xg.shape
     with torch.no_grad():
         assert qo.rel_err(yg.float().cpu().numpy(), fused(xg).float().cpu().numpy()) <= 1e-2
+
+
+@pytest.mark.parametrize("kind,group,n,k,m", [("int4", 128, 4864, 896, 1), ("int4", 128, 4864, 896, 32),
+                                              ("int8", None, 4864, 896, 16), ("int4", 128, 1024, 1024, 200)])
+def test_silu_mul_fused_vs_oracle_chain_from_x(kind, group, n, k, m):
+    """The fused gate / up layer against an oracle chain that starts from x: oracle
+    dequantize, float64 linear rounded to bf16 for gate and up, then the oracle's
+    silu_mul (modeling_qwen2.py:46-48, quantization.py:104-141)."""
+    _say(f"silu_mul oracle chain {kind} g={group} N={n} K={k} M={m}")
+    gate, up = _pair(kind, n, k, group, 3 * n + k + m)
+    fused = fuse_linears([gate, up], act="silu_mul")
+    x = (torch.randn(m, k, generator=torch.Generator().manual_seed(m + 1)) * 0.5).to(torch.bfloat16)
+    with torch.no_grad():
+        y = fused(x.to(DEV)).float().cpu().numpy()
+
+    def chain(layer):
+        if kind == "int8":
+            wd = qo.dequant_int8(layer.weight_q.cpu().numpy(), layer.scale.cpu().numpy(), "bf16")
+        else:
+            wd = qo.dequant_int4(layer.weight_packed.cpu().numpy(), layer.scale.float().cpu().numpy(), k,
+                                 group, "bf16")
+        b = None if layer.bias is None else layer.bias.detach().float().cpu().numpy()
+        return qo.round_to(qo.linear_f64(x.float().numpy(), wd, b, "bf16").astype(np.float32), "bf16")
+
+    ref = qo.silu_mul(chain(gate), chain(up), "bf16")
+    err = qo.rel_err(y, ref)
+    _say(f"  rel_err={err:.2e}")
+    # a 1-ulp bf16 rounding difference in g or u (rare: a near-tie decided by the fp32
+    # summation order) moves the composite by up to ~2.1 % (2 x 2^-7 x 1.1 + 2^-8); the
+    # linear outputs themselves are held to 1e-2 elsewhere
+    mean = float(np.mean(np.abs(y - ref)) / np.max(np.abs(ref)))
+    assert err <= 3e-2 and mean <= 2e-3

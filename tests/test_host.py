@@ -468,3 +468,71 @@ def test_packed_checkpoint_rejects_foreign_files(tmp_path):
     save_packed(model, good)
     with pytest.raises(ValueError, match="no module named"):
         load_packed(nn.Sequential(nn.Linear(4, 4)), good)
+
+
+def _rewrite_packed(src, dst, edit):
+    """Copy a packed file, passing its tensors through edit(dict) (header kept)."""
+    from safetensors import safe_open
+    from safetensors.torch import save_file
+
+    with safe_open(src, framework="pt") as f:
+        meta = f.metadata()
+        tensors = {k: f.get_tensor(k) for k in f.keys()}
+    edit(tensors)
+    save_file(tensors, dst, metadata=meta)
+
+
+@pytest.mark.parametrize("case", ["short_packed", "wide_scale", "wrong_dtype", "missing", "extra",
+                                  "tiled_bytes"])
+def test_packed_checkpoint_rejects_mismatched_tensors(tmp_path, case):
+    """A tensor whose shape, dtype or byte count disagrees with the layer's metadata (a
+    truncated or mixed-up file) raises ValueError before anything is installed; the kernels
+    size their buffer descriptors from N and K, so such a tensor must never reach them."""
+    from safetensors import safe_open
+
+    from localstrm_amd import load_packed, save_packed
+
+    model = seeded_model()
+    apply_optional_quantization(model, quant_type="int4", group_size=32)
+    good = str(tmp_path / "good.safetensors")
+    save_packed(model, good)
+    key = "model.layers.0.mlp.down_proj"
+
+    def edit(t):
+        if case == "short_packed":
+            t[f"{key}.weight_packed"] = t[f"{key}.weight_packed"][:-1].clone()
+        elif case == "wide_scale":
+            s = t[f"{key}.scale"]
+            t[f"{key}.scale"] = torch.cat([s, s[:, :1]], dim=1)
+        elif case == "wrong_dtype":
+            t[f"{key}.weight_packed"] = t[f"{key}.weight_packed"].to(torch.int8)
+        elif case == "missing":
+            del t[f"{key}.scale"]
+        elif case == "extra":
+            t[f"{key}.extra"] = torch.zeros(3)
+        elif case == "tiled_bytes":
+            t[f"{key}.weight_tiled"] = torch.zeros(17, dtype=torch.uint8)
+
+    bad = str(tmp_path / "bad.safetensors")
+    if case in ("extra", "tiled_bytes"):
+        # the header lists the layer's tensors: add the name there too
+        import json
+        from safetensors.torch import save_file
+
+        with safe_open(good, framework="pt") as f:
+            meta = dict(f.metadata())
+            tensors = {k: f.get_tensor(k) for k in f.keys()}
+        layers = json.loads(meta["layers"])
+        layers[key]["tensors"].append("extra" if case == "extra" else "weight_tiled")
+        meta["layers"] = json.dumps(layers)
+        edit(tensors)
+        save_file(tensors, bad, metadata=meta)
+    else:
+        _rewrite_packed(good, bad, edit)
+    fresh = seeded_model(seed=7)
+    before = {k: v.clone() for k, v in fresh.state_dict().items()}
+    with pytest.raises(ValueError, match="load_packed"):
+        load_packed(fresh, bad)
+    if case != "missing":  # layers before the bad one are installed; the bad one never is
+        assert isinstance(fresh.model.layers[0].mlp.down_proj, nn.Linear)
+    assert load_packed(seeded_model(seed=7), good) == 14
