@@ -48,6 +48,7 @@ extern "C" {
 #define LSQ_E_GROUP (-4)       /* group_size < 1 */
 #define LSQ_E_LAYOUT (-5)      /* tiled layouts need K % 128 == 0 */
 #define LSQ_E_ALIGN (-6)       /* pointer or leading dim not aligned as the kernel needs */
+#define LSQ_E_SCRATCH (-7)     /* the call needs more than LSQ_NOALLOC_SCRATCH_BYTES */
 
 /* Library version (major*10000 + minor*100 + patch). No reference counterpart. */
 int lsq_version(void);
@@ -192,6 +193,23 @@ int lsq_w8a8_linear(const void* x, int64_t ldx, const int8_t* tiled, const void*
                     int scale_w_dtype, const void* bias, int bias_dtype, void* y, int64_t ldy,
                     int dtype, int64_t M, int64_t N, int64_t K, int8_t* x_q, float* scale_x,
                     void* stream);
+
+/* Bytes of the fixed device array behind lsq_w8a8_linear_noalloc, one per GPU. */
+#define LSQ_NOALLOC_SCRATCH_BYTES (8 * 1024 * 1024)
+
+/* lsq_w8a8_linear without the x_q / scale_x workspace: the same kernels and the same
+ * result bit for bit, with the quantized activations staged in a fixed device array of
+ * LSQ_NOALLOC_SCRATCH_BYTES that the library holds on each GPU it runs on until the
+ * process ends. No counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc); it calls no hipMalloc / hipFree. The first call on a device resolves that
+ * device's copy of the array (hipGetSymbolAddress; the device is the stream's). Limit:
+ * round_up(M * round_up(K, 128), 256) + 4 * M <= LSQ_NOALLOC_SCRATCH_BYTES (M <= 2046 at
+ * K = 4096), else LSQ_E_SCRATCH before any HIP call. Calls that overlap on one GPU (other
+ * streams, other threads) share the array and race: serialize them. */
+int lsq_w8a8_linear_noalloc(const void* x, int64_t ldx, const int8_t* tiled, const void* scale_w,
+                            int scale_w_dtype, const void* bias, int bias_dtype, void* y,
+                            int64_t ldy, int dtype, int64_t M, int64_t N, int64_t K, void* stream);
 
 /* ---- Paged attention for one decode step (INT8 or T-typed KV cache) ----
  * Replaces paged_attention_decode (src/kernels/paged_attention.py:33-173) for a query of

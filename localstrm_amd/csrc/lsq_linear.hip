@@ -209,6 +209,9 @@ extern "C" const char* lsq_status_string(int status) {
     case LSQ_E_GROUP: return "lsq: group_size must be >= 1";
     case LSQ_E_LAYOUT: return "lsq: the tiled weight layouts need K % 128 == 0";
     case LSQ_E_ALIGN: return "lsq: pointer or leading dimension not aligned as required";
+    case LSQ_E_SCRATCH:
+      return "lsq: the call needs more than the allocation-free entry point's fixed scratch "
+             "(LSQ_NOALLOC_SCRATCH_BYTES); use lsq_w8a8_linear with a workspace";
     default: break;
   }
   if (status > 0) return hipGetErrorString(static_cast<hipError_t>(status));

@@ -36,6 +36,7 @@
 #include <atomic>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 
 namespace lsq {
 namespace {
@@ -511,4 +512,81 @@ extern "C" int lsq_w8a8_linear(const void* x, int64_t ldx, const int8_t* tiled,
     default: rc = run_w8a8<LSQ_BF16>(ax, a, s); break;
   }
   return rc == LSQ_E_LAYOUT ? LSQ_E_SHAPE : rc;
+}
+
+// ---- Allocation-free W8A8 entry point ----
+//
+// `scratch` replaces the caller's x_q / scale_x workspace: x_q [M, round_up(K, 128)] int8
+// at offset 0, scale_x [M] fp32 at the next multiple of 256 bytes. Every GPU the library
+// runs on holds its own copy until the process ends. In host code `scratch` names a
+// host-side stand-in, never device memory: kernels get the address hipGetSymbolAddress
+// returns for the device, resolved once per device (with that device current) and kept in
+// g_scratch. Nothing in it has to start at zero: the activation quantizer writes every
+// x_q byte the GEMM or GEMV reads (the K padding included) and every scale, before they
+// are read, on the caller's stream. Calls that overlap on one GPU share the array and race.
+static __device__ __align__(256) uint8_t scratch[LSQ_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::atomic<uint8_t*> g_scratch[kMaxDevices];
+std::mutex g_scratch_mu;
+
+// This device's address of `scratch`; `dev` is current when called.
+int scratch_on(int dev, uint8_t** out) {
+  if (dev < 0 || dev >= kMaxDevices) return static_cast<int>(hipErrorInvalidDevice);
+  uint8_t* p = g_scratch[dev].load(std::memory_order_acquire);
+  if (!p) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch[dev].load(std::memory_order_relaxed);
+    if (!p) {
+      void* addr = nullptr;
+      const hipError_t e = hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch));
+      if (e != hipSuccess) return static_cast<int>(e);
+      if (!addr) return static_cast<int>(hipErrorInvalidSymbol);
+      p = static_cast<uint8_t*>(addr);
+      g_scratch[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return LSQ_OK;
+}
+
+}  // namespace
+
+extern "C" int lsq_w8a8_linear_noalloc(const void* x, int64_t ldx, const int8_t* tiled,
+                                       const void* scale_w, int scale_w_dtype, const void* bias,
+                                       int bias_dtype, void* y, int64_t ldy, int dtype, int64_t M,
+                                       int64_t N, int64_t K, void* stream) {
+  if (M < 0 || N < 0 || K < 1 || ldx < K || ldy < N) return LSQ_E_SHAPE;
+  if (M > INT32_MAX / 2 || N > INT32_MAX / 2 || K >= 131072) return LSQ_E_SHAPE;
+  // x_q rows, then the scales 256-byte aligned; checked before any HIP call
+  const int64_t xq_bytes = (M * pad_k(K) + 255) / 256 * 256;
+  if (xq_bytes + M * static_cast<int64_t>(sizeof(float)) > LSQ_NOALLOC_SCRATCH_BYTES) return LSQ_E_SCRATCH;
+  if (M == 0 || N == 0) return LSQ_OK;
+  if (!x || !tiled || !scale_w || !y) return LSQ_E_NULL;
+  // the stream's device, which the kernels run on; the scratch address is per device
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  int cur = 0, dev = 0;
+  hipError_t e = hipGetDevice(&cur);
+  if (e != hipSuccess) return static_cast<int>(e);
+  dev = cur;
+  if (s) {
+    e = hipStreamGetDevice(s, &dev);
+    if (e != hipSuccess) return static_cast<int>(e);
+  }
+  uint8_t* base = nullptr;
+  int rc;
+  if (dev == cur) {
+    rc = scratch_on(dev, &base);
+  } else {
+    e = hipSetDevice(dev);
+    if (e != hipSuccess) return static_cast<int>(e);
+    rc = scratch_on(dev, &base);
+    e = hipSetDevice(cur);
+    if (rc == LSQ_OK && e != hipSuccess) rc = static_cast<int>(e);
+  }
+  if (rc != LSQ_OK) return rc;
+  return lsq_w8a8_linear(x, ldx, tiled, scale_w, scale_w_dtype, bias, bias_dtype, y, ldy, dtype, M, N, K,
+                         reinterpret_cast<int8_t*>(base), reinterpret_cast<float*>(base + xq_bytes), stream);
 }
