@@ -4,25 +4,31 @@ python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-sweep] [--no-cpu]
 python bench.py --calibrate-copy   # one 64 MiB device-to-device copy, for PMC calibration
 python bench.py --case int4,14336,4096,2048 --steps 20   # one layer shape only
 
-Headline workload (one JSON line, `value`): INT8 per-output-channel decode GEMV at the
-Qwen2.5-7B MLP shape, W int8 [18944, 3584], x bf16 [1, 3584] -> y bf16 [1, 18944].
-A step is one forward of the layer. `value` is algorithmic GB/s = (W + scales + x + y
-bytes) / time per step, with inputs resident in HBM. The timed region is a HIP graph of
-K back-to-back launches bracketed by events on the launch stream; successive launches
-cycle through enough distinct weight copies (> 256 MB) that every launch streams its
-weights from HBM rather than from the 256 MB Infinity Cache.
+Headline workload (one JSON line, `value`): INT4 group-128 decode GEMV at the
+Qwen2.5-7B MLP shape, W int4 [18944, 3584] (two nibbles per byte, bf16 scales
+[18944, 28]), x bf16 [1, 3584] -> y bf16 [1, 18944]. A step is one forward of the layer.
+`value` is algorithmic GB/s = (W + scales + x + y bytes) / time per step, with inputs
+resident in HBM. The timed region is a HIP graph of K back-to-back launches bracketed by
+events on the launch stream, replayed 7 times; every figure is the median replay.
+Successive launches cycle through enough distinct weight copies (> 256 MB) that every
+launch streams its weights from HBM rather than from the 256 MB Infinity Cache.
+
+`floors` times, the same way in the same run, an empty kernel (the cost of one launch)
+and a bare streaming read of the headline's bytes (lsq_probe_read): the time no kernel
+that must stream those bytes in one launch can beat on this device.
 
 `roofline.traffic` is the HBM bytes one launch of the headline kernel moves, as measured
 by rocprofv3 FETCH_SIZE + WRITE_SIZE (each scaled by what the counter reads for a 64 MiB
-copy, see --calibrate-copy) and recorded in profiles/decode_int8_m1_18944x3584.txt.
+copy, see --calibrate-copy) and recorded in profiles/decode_int4_g128_m1_18944x3584.txt.
 
-`sweep` reports the other shapes of the same metric (INT8 M in {8,32,64}, INT4 group-128
-decode M in {1,16,64} at 18944x3584, INT4 group-128 prefill M in {256,2048,8192} at
-14336x4096 in TFLOP/s, the single INT8 layer 4864x896 at M=1, INT4 group-128 decode M in
-{1,16} at the transposed 3584x18944 shape, W8A8 layers, and one batch-32 decode step
-through the 168 INT4 projections of a Qwen2.5-0.5B-architecture stack); `cpu_baseline`
-times the reference's CPU path (dequantize, then F.linear, on the host cores) on the
-headline shape.
+`sweep` reports the other shapes of the same metric (INT8 per-channel decode M in
+{1,8,32,64} at 18944x3584, INT4 group-128 decode M in {16,64}, INT4 group-128 prefill M in
+{256,2048,8192} at 14336x4096 in TFLOP/s, the single INT8 layer 4864x896 at M=1, INT4
+decode M in {1,16} at the transposed 3584x18944 shape, W8A8 layers, the batch-32 decode
+step through the 168 INT4 projections of a Qwen2.5-0.5B-architecture stack, its MLPs, and
+paged attention). `cpu_baseline` times the reference's CPU path (dequantize, then
+F.linear, on the host cores) on the headline shape; `cpu_baselines_more` on INT8 M=1 and
+on INT4 prefill M=2048.
 """
 
 from __future__ import annotations
@@ -112,36 +118,47 @@ def _layers(kind, w, s, group, copies, device):
     return out
 
 
-def time_layers(layers, x, steps: int, warmup: int) -> float:
-    """Mean ms per forward over `steps` launches replayed from one HIP graph, cycling the
-    weight copies; bracketed by events on the launch stream."""
+REPLAYS = 7  # timed replays of each graph; figures are their median
+
+
+def graph_time(step, steps: int, warmup: int, replays: int = REPLAYS):
+    """(median, min, max) ms per step: `step(i)` launches step i's work; `steps` of them are
+    captured in one HIP graph on a side stream, replayed once untimed, then `replays` times,
+    each bracketed by events recorded on that stream (the stream the kernels run on)."""
     stream = torch.cuda.Stream()
     with torch.no_grad():
-        y = layers[0](x)
         for i in range(max(warmup, 1)):
-            layers[i % len(layers)](x)
+            step(i)
         torch.cuda.synchronize()
         stream.wait_stream(torch.cuda.current_stream())
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.stream(stream):
             with torch.cuda.graph(graph, stream=stream):
                 for i in range(steps):
-                    y = layers[i % len(layers)](x)
+                    step(i)
         graph.replay()  # warm replay
         torch.cuda.synchronize()
-        start = torch.cuda.Event(enable_timing=True)
-        stop = torch.cuda.Event(enable_timing=True)
-        with torch.cuda.stream(stream):
-            start.record(stream)
-            graph.replay()
-            stop.record(stream)
-        stop.synchronize()
+        per = []
+        for _ in range(replays):
+            start = torch.cuda.Event(enable_timing=True)
+            stop = torch.cuda.Event(enable_timing=True)
+            with torch.cuda.stream(stream):
+                start.record(stream)
+                graph.replay()
+                stop.record(stream)
+            stop.synchronize()
+            per.append(start.elapsed_time(stop) / steps)
         del graph
-    return start.elapsed_time(stop) / steps
+    return statistics.median(per), min(per), max(per)
+
+
+def time_layers(layers, x, steps: int, warmup: int):
+    """graph_time of one forward per step, cycling the weight copies."""
+    return graph_time(lambda i: layers[i % len(layers)](x), steps, warmup)
 
 
 PROFILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
-                       "decode_int8_m1_18944x3584.txt")
+                       "decode_int4_g128_m1_18944x3584.txt")
 
 
 def measured_traffic():
@@ -172,6 +189,41 @@ def copies_for(nbytes: int) -> int:
     return max(2, min(32, -(-2 * MALL_BYTES // max(nbytes, 1)) + 1))
 
 
+READ_SHAPES = ((256, 1024), (256, 512), (512, 512), (512, 1024), (1024, 256))
+
+
+def bench_floors(nbytes: int, steps: int, warmup: int, device) -> dict:
+    """Floors for one launch of the headline, timed the same way in the same run: an empty
+    kernel (what one graph node costs with no work) and a bare streaming read of `nbytes`
+    (lsq_probe_read: the same bytes, nothing computed), cycling enough buffers to exceed
+    the Infinity Cache; the read floor is the fastest of READ_SHAPES (grid, threads)."""
+    from localstrm_amd import _lib
+
+    lib = _lib.load()
+    copies = copies_for(nbytes)
+    bufs = [torch.randint(0, 256, (nbytes,), dtype=torch.uint8, device=device) for _ in range(copies)]
+    sink = torch.empty(max(g for g, _ in READ_SHAPES) * 64, dtype=torch.float32, device=device)
+
+    def empty(i):
+        _lib.check(lib.lsq_probe_empty(_lib.stream_handle(device)), "lsq_probe_empty")
+
+    launch = graph_time(empty, steps, warmup)[0]
+    per_shape = {}
+    for grid, block in READ_SHAPES:
+        def read(i, grid=grid, block=block):
+            _lib.check(lib.lsq_probe_read(bufs[i % copies].data_ptr(), nbytes, sink.data_ptr(), grid, block,
+                                          _lib.stream_handle(device)), "lsq_probe_read")
+        per_shape[f"{grid}x{block}"] = graph_time(read, steps, warmup)[0] * 1e3
+    best = min(per_shape, key=per_shape.get)
+    del bufs
+    torch.cuda.empty_cache()
+    return {
+        "launch_us": launch * 1e3, "bare_read_bytes": nbytes, "bare_read_us": per_shape[best],
+        "bare_read_shape": best, "bare_read_GB_s": nbytes / (per_shape[best] * 1e-6) / 1e9,
+        "bare_read_us_by_shape": per_shape, "buffers": copies,
+    }
+
+
 def bench_decode(kind: str, n: int, k: int, m: int, steps: int, warmup: int, device, group=128):
     if kind in ("int8", "w8a8"):
         w, s, x = make_int8(n, k, m)
@@ -180,7 +232,7 @@ def bench_decode(kind: str, n: int, k: int, m: int, steps: int, warmup: int, dev
     wbytes = w.numel()
     copies = copies_for(wbytes)
     layers = _layers(kind, w, s, group, copies, device)
-    ms = time_layers(layers, x.to(device), steps, warmup)
+    ms, lo, hi = time_layers(layers, x.to(device), steps, warmup)
     nbytes = decode_bytes(kind, n, k, m, group)
     flops = 2.0 * m * n * k
     del layers
@@ -188,7 +240,7 @@ def bench_decode(kind: str, n: int, k: int, m: int, steps: int, warmup: int, dev
     peak = MFMA_INT8_PEAK_TOPS if kind == "w8a8" else MFMA_BF16_PEAK_TF
     return {
         "kind": kind, "M": m, "N": n, "K": k, "group": None if kind in ("int8", "w8a8") else group,
-        "us_per_call": ms * 1e3, "GB_s": nbytes / (ms * 1e-3) / 1e9,
+        "us_per_call": ms * 1e3, "us_range": [lo * 1e3, hi * 1e3], "GB_s": nbytes / (ms * 1e-3) / 1e9,
         "TFLOP_s": flops / (ms * 1e-3) / 1e12, "bytes": nbytes, "weight_copies": copies,
         "frac_hbm": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
         "frac_mfma": flops / (ms * 1e-3) / 1e12 / peak,
@@ -236,38 +288,19 @@ def bench_stack(steps: int, warmup: int, device, m: int = 32, n_layers: int = 24
     stacks = [[lin for _ in range(n_layers) for lin in one_layer()] for _ in range(copies)]
     xs = {k: torch.randn(m, k, generator=_gen(k)).to(torch.bfloat16).to(device) for k in (896, 4864)}
 
-    stream = torch.cuda.Stream()
-    with torch.no_grad():
-        def run(i):
-            for lin in stacks[i % copies]:
-                lin(xs[lin.in_features])
-        for i in range(max(warmup, 1)):
-            run(i)
-        torch.cuda.synchronize()
-        stream.wait_stream(torch.cuda.current_stream())
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.stream(stream):
-            with torch.cuda.graph(graph, stream=stream):
-                for i in range(steps):
-                    run(i)
-        graph.replay()
-        torch.cuda.synchronize()
-        start = torch.cuda.Event(enable_timing=True)
-        stop = torch.cuda.Event(enable_timing=True)
-        with torch.cuda.stream(stream):
-            start.record(stream)
-            graph.replay()
-            stop.record(stream)
-        stop.synchronize()
-        del graph
-    ms = start.elapsed_time(stop) / steps
+    def run(i):
+        for lin in stacks[i % copies]:
+            lin(xs[lin.in_features])
+
+    ms, lo, hi = graph_time(run, steps, warmup)
     del stacks
     torch.cuda.empty_cache()
     flops = 2.0 * m * n_layers * sum(n * k for _, n, k, _ in QWEN05_LINEARS)
     return {
         "kind": "int4 stack" + (" fused" if fused else ""), "M": m, "layers": n_layers,
         "forwards": n_layers * len(QWEN05_LINEARS), "launches": n_layers * (4 if fused else 7),
-        "group": group, "us_per_call": ms * 1e3, "GB_s": per_step / (ms * 1e-3) / 1e9,
+        "group": group, "us_per_call": ms * 1e3, "us_range": [lo * 1e3, hi * 1e3],
+        "GB_s": per_step / (ms * 1e-3) / 1e9,
         "TFLOP_s": flops / (ms * 1e-3) / 1e12, "bytes": per_step, "stack_copies": copies,
         "frac_hbm": per_step / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
         "frac_mfma": flops / (ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TF,
@@ -302,37 +335,17 @@ def bench_mlp(steps: int, warmup: int, device, m: int = 32, n_layers: int = 24, 
 
     stacks = [[one_layer() for _ in range(n_layers)] for _ in range(copies)]
     x = torch.randn(m, 896, generator=_gen(5)).to(torch.bfloat16).to(device)
-    stream = torch.cuda.Stream()
-    with torch.no_grad():
-        def run(i):
-            for mlp in stacks[i % copies]:
-                mlp(x)
-        for i in range(max(warmup, 1)):
-            run(i)
-        torch.cuda.synchronize()
-        stream.wait_stream(torch.cuda.current_stream())
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.stream(stream):
-            with torch.cuda.graph(graph, stream=stream):
-                for i in range(steps):
-                    run(i)
-        graph.replay()
-        torch.cuda.synchronize()
-        start = torch.cuda.Event(enable_timing=True)
-        stop = torch.cuda.Event(enable_timing=True)
-        with torch.cuda.stream(stream):
-            start.record(stream)
-            graph.replay()
-            stop.record(stream)
-        stop.synchronize()
-        del graph
-    ms = start.elapsed_time(stop) / steps
+    def run(i):
+        for mlp in stacks[i % copies]:
+            mlp(x)
+
+    ms, lo, hi = graph_time(run, steps, warmup)
     del stacks
     torch.cuda.empty_cache()
     return {
         "kind": "int4 mlp" + (" fused silu_mul" if fused else ""), "M": m, "layers": n_layers,
         "launches": n_layers * (2 if fused else 5), "group": group, "us_per_call": ms * 1e3,
-        "GB_s": per_step / (ms * 1e-3) / 1e9, "bytes": per_step, "stack_copies": copies,
+        "us_range": [lo * 1e3, hi * 1e3], "GB_s": per_step / (ms * 1e-3) / 1e9, "bytes": per_step, "stack_copies": copies,
         "frac_hbm": per_step / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
     }
 
@@ -366,36 +379,17 @@ def bench_paged(steps: int, warmup: int, device, b: int = 32, h: int = 14, hkv: 
     esz = 1 if int8 else 2
     per_step = n_layers * (2 * b * seq * hkv * d * esz + (2 * b * seq * hkv * 2 if int8 else 0)
                            + 2 * b * h * d * 2)
-    stream = torch.cuda.Stream()
-    with torch.no_grad():
-        def run():
-            for kp, vp, ks, vs in pools:
-                paged_attention_decode(q, kp, vp, bt, sl, bs, ks, vs, max_sl=seq)
-        for _ in range(max(warmup, 1)):
-            run()
-        torch.cuda.synchronize()
-        stream.wait_stream(torch.cuda.current_stream())
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.stream(stream):
-            with torch.cuda.graph(graph, stream=stream):
-                for _ in range(steps):
-                    run()
-        graph.replay()
-        torch.cuda.synchronize()
-        start = torch.cuda.Event(enable_timing=True)
-        stop = torch.cuda.Event(enable_timing=True)
-        with torch.cuda.stream(stream):
-            start.record(stream)
-            graph.replay()
-            stop.record(stream)
-        stop.synchronize()
-        del graph
-    ms = start.elapsed_time(stop) / steps
+    def run(i):
+        for kp, vp, ks, vs in pools:
+            paged_attention_decode(q, kp, vp, bt, sl, bs, ks, vs, max_sl=seq)
+
+    ms, lo, hi = graph_time(run, steps, warmup)
     del pools
     torch.cuda.empty_cache()
     return {
         "kind": "paged attention" + (" int8 kv" if int8 else " fp16 kv"), "B": b, "H": h, "Hkv": hkv,
         "D": d, "seq": seq, "layers": n_layers, "us_per_call": ms * 1e3,
+        "us_range": [lo * 1e3, hi * 1e3],
         "us_per_layer": ms * 1e3 / n_layers, "GB_s": per_step / (ms * 1e-3) / 1e9,
         "bytes": per_step, "frac_hbm": per_step / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
     }
@@ -404,38 +398,50 @@ def bench_paged(steps: int, warmup: int, device, b: int = 32, h: int = 14, hkv: 
 # ----------------------------------------------------------------------------- CPU baseline
 
 
-def cpu_baseline(n: int, k: int, m: int, budget_s: float = 15.0):
-    """The reference's CPU path (dequantize in the activation dtype, then F.linear) on the
-    host cores, on the headline shape, for about `budget_s` seconds."""
-    from oracle import torch_ref
-
-    torch.set_num_threads(os.cpu_count() or 1)
-    w, s, x = make_int8(n, k, m)
-    times = []
-    with torch.no_grad():
-        for _ in range(2):
-            torch_ref.forward_int8(x, w, s)
-        t_end = time.perf_counter() + budget_s
-        while time.perf_counter() < t_end and len(times) < 2000:
-            t0 = time.perf_counter()
-            torch_ref.forward_int8(x, w, s)
-            times.append(time.perf_counter() - t0)
-    med = statistics.median(times)
-    cpu_model = "unknown"
+def _cpu_model() -> str:
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
                 if line.startswith("model name"):
-                    cpu_model = line.split(":", 1)[1].strip()
-                    break
+                    return line.split(":", 1)[1].strip()
     except OSError:
         pass
+    return "unknown"
+
+
+def cpu_baseline(kind: str, n: int, k: int, m: int, budget_s: float = 10.0, min_runs: int = 3,
+                 group: int = 128):
+    """The reference's CPU path (quantization.py:104-141: dequantize in the activation dtype,
+    then F.linear) on the host cores, on the same seeded inputs as the GPU case, repeated for
+    about `budget_s` seconds (at least `min_runs` timed runs after one warm-up). Decode
+    shapes report GB/s of the same algorithmic bytes as the GPU; M >= 256 reports TFLOP/s."""
+    from oracle import torch_ref
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    if kind == "int8":
+        w, s, x = make_int8(n, k, m)
+        fwd = lambda: torch_ref.forward_int8(x, w, s)
+    else:
+        w, s, x = make_int4(n, k, m, group)
+        fwd = lambda: torch_ref.forward_int4(x, w, s, k, group)
+    times = []
+    with torch.no_grad():
+        fwd()
+        t_end = time.perf_counter() + budget_s
+        while (time.perf_counter() < t_end or len(times) < min_runs) and len(times) < 2000:
+            t0 = time.perf_counter()
+            fwd()
+            times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    prefill = m >= 256
+    value = 2.0 * m * n * k / med / 1e12 if prefill else decode_bytes(kind, n, k, m, group) / med / 1e9
+    what = f"{kind}" + ("" if kind == "int8" else f" group-{group}") + (" prefill" if prefill else " decode")
     return {
-        "value": decode_bytes("int8", n, k, m) / med / 1e9, "unit": "GB/s",
+        "value": value, "unit": "TFLOP/s" if prefill else "GB/s", "ms_per_call": med * 1e3,
         "cores": torch.get_num_threads(), "kind": "port",
-        "sample": (f"int8 decode {n}x{k} M={m}, bf16: torch CPU dequantize + F.linear, "
-                   f"median of {len(times)} runs ({med * 1e3:.1f} ms/call), cpu '{cpu_model}', "
-                   f"os.cpu_count()={os.cpu_count()}"),
+        "sample": (f"{what} {n}x{k} M={m}, bf16: torch CPU dequantize + F.linear on the same "
+                   f"seeded inputs, median of {len(times)} runs ({med * 1e3:.1f} ms/call), cpu "
+                   f"'{_cpu_model()}', os.cpu_count()={os.cpu_count()}"),
     }
 
 
@@ -494,13 +500,14 @@ def main() -> int:
         print(json.dumps(r), flush=True)
         return 0
 
-    N, K, M = 18944, 3584, 1
-    head = bench_decode("int8", N, K, M, args.steps, args.warmup, device)
+    N, K, M, G = 18944, 3584, 1, 128
+    head = bench_decode("int4", N, K, M, args.steps, args.warmup, device, group=G)
+    floors = bench_floors(decode_bytes("int4", N, K, M, G), args.steps, args.warmup, device)
     sweep = []
     if not args.no_sweep:
-        for m in (8, 32, 64):
+        for m in (1, 8, 32, 64):
             sweep.append(bench_decode("int8", N, K, m, args.steps, args.warmup, device))
-        for m in (1, 16, 64):
+        for m in (16, 64):
             sweep.append(bench_decode("int4", N, K, m, args.steps, args.warmup, device))
         for m in (256, 2048, 8192):
             sweep.append(bench_decode("int4", 14336, 4096, m, max(10, args.steps // 20),
@@ -518,7 +525,10 @@ def main() -> int:
         sweep.append(bench_mlp(max(5, args.steps // 20), 2, device))
         sweep.append(bench_mlp(max(5, args.steps // 20), 2, device, fused=True))
         sweep.append(bench_paged(max(5, args.steps // 20), 2, device))
-    cpu = None if args.no_cpu else cpu_baseline(N, K, M)
+    cpu, cpu_more = None, []
+    if not args.no_cpu:
+        cpu = cpu_baseline("int4", N, K, M, group=G)
+        cpu_more = [cpu_baseline("int8", N, K, M), cpu_baseline("int4", 14336, 4096, 2048, group=G)]
 
     ms = head["us_per_call"] / 1e3
     line = {
@@ -535,15 +545,20 @@ def main() -> int:
         "dtype": "bf16",
         "data": "synthetic: seeded torch.Generator(0) inputs of the stated shapes",
         "config": {
-            "workload": "int8 per-channel decode GEMV, W int8 18944x3584, x bf16 [1,3584]",
-            "M": M, "N": N, "K": K, "weight_copies": head["weight_copies"],
-            "timing": "HIP graph of `steps` launches, events on the launch stream",
+            "workload": ("int4 group-128 decode GEMV, W int4 18944x3584 (packed 2 per byte, bf16 "
+                         "scales [18944, 28]), x bf16 [1, 3584]"),
+            "M": M, "N": N, "K": K, "group": G, "weight_copies": head["weight_copies"],
+            "timing": (f"median of {REPLAYS} replays of a HIP graph of `steps` launches, events "
+                       "on the launch stream"),
+            "us_range": head["us_range"],
         },
         "roofline": {
             "bound": "hbm", "achieved": round(head["GB_s"], 2), "peak": HBM_PEAK_GBS,
             "unit": "GB/s", "frac": round(head["frac_hbm"], 4), "traffic": measured_traffic(),
         },
+        "floors": dict(floors, kernel_vs_bare_read=head["us_per_call"] / floors["bare_read_us"]),
         "cpu_baseline": cpu,
+        "cpu_baselines_more": cpu_more,
         "sweep": sweep,
         "host": platform.node(),
     }

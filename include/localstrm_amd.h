@@ -240,6 +240,16 @@ int lsq_paged_attention_decode(const void* query, const void* k_pool, const void
                                int64_t num_blocks, int64_t max_seq_len, int head_mapping,
                                void* workspace, int64_t workspace_bytes, void* stream);
 
+/* ---- Measurement floors (no reference counterpart; for benchmarks) ----
+ * lsq_probe_empty launches one empty workgroup: the cost of a launch itself.
+ * lsq_probe_read streams `bytes` (1 .. 2^31 - 1) of `buf` once with 16-byte loads and
+ * computes nothing: `grid` workgroups of `block` threads (64..1024, a multiple of 64), each
+ * reading a contiguous share with 4 loads in flight per lane, write grid * 64 floats to
+ * `sink` (so the loads are kept). Its time is a floor for any kernel that must stream the
+ * same bytes in one launch on this device. */
+int lsq_probe_empty(void* stream);
+int lsq_probe_read(const void* buf, int64_t bytes, float* sink, int grid, int block, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -343,6 +343,11 @@ def test_library_rejects_bad_arguments_without_gpu():
                              16, None) == -1  # M > 0 needs x
     assert lib.lsq_w8_linear(1 << 20, 128, 1 << 20, (1 << 20) + 8, 1 << 20, 0, None, 0, 1 << 20,
                              16, 2, 1, 16, 128, None) == -6  # tiled copy not 16-byte aligned
+    # measurement probes: sizes and launch shapes are checked before any HIP call
+    assert lib.lsq_probe_read(1 << 20, 0, 1 << 20, 256, 512, None) == -2
+    assert lib.lsq_probe_read(1 << 20, 1 << 31, 1 << 20, 256, 512, None) == -2
+    assert lib.lsq_probe_read(1 << 20, 4096, 1 << 20, 256, 96, None) == -2
+    assert lib.lsq_probe_read(None, 4096, 1 << 20, 256, 512, None) == -1
     # the allocation-free W8A8 entry point refuses what its fixed scratch cannot hold
     # (2047 rows x 4096 int8 + 2047 fp32 scales > 8 MiB), before any HIP call
     assert lib.lsq_w8a8_linear_noalloc(None, 4096, None, None, 0, None, 0, None, 64, 2, 2047, 64,
