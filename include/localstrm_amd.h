@@ -240,6 +240,29 @@ int lsq_paged_attention_decode(const void* query, const void* k_pool, const void
                                int64_t num_blocks, int64_t max_seq_len, int head_mapping,
                                void* workspace, int64_t workspace_bytes, void* stream);
 
+/* ---- Weight quantization on the GPU ----
+ * Replace the CPU quantization of QuantizedLinear.from_float / Int8GEMMLinear.from_float
+ * (src/kernels/quantization.py:72-94, :341-344; the loader stages it at :593-610) for
+ * weights already in device memory, with the same fp32 steps and results bit for bit:
+ * scale = max(max|w| / qmax, fp32(1e-8)) per row (qmax 127 / 7; IEEE division), q =
+ * clamp(rint(w / scale), qmin, qmax) (IEEE division, round half to even). w [N, K] is
+ * f32 / f16 / bf16 with row stride ldw elements. Writes the canonical layout, the tiled
+ * layout (16-byte aligned, K % 128 == 0), or both; NULL skips one, not both. Rows holding
+ * NaN or infinities give unspecified q (as the reference's float -> int8 cast of NaN). */
+
+/* INT8 per channel: scale [N] fp32, weight_q [N, K] int8, tiled as lsq_w8_retile writes
+ * it (which is also the W8A8 tiled layout at K % 128 == 0). */
+int lsq_quantize_w8(const void* w, int w_dtype, int64_t ldw, int64_t N, int64_t K, float* scale,
+                    int8_t* weight_q, int8_t* tiled, void* stream);
+
+/* INT4: group_size 0 or >= K is the reference's per-channel INT4 (scale [N] fp32,
+ * scale_dtype must be LSQ_F32); 1 <= group_size < K quantizes each group of group_size
+ * columns against its scale rounded to scale_dtype (stored [N, ceil(K / group_size)]).
+ * weight_packed [N, ceil(K/2)] (low nibble = even column), tiled as lsq_w4_retile writes
+ * it (group_size a multiple of 8 there). */
+int lsq_quantize_w4(const void* w, int w_dtype, int64_t ldw, int64_t N, int64_t K, int64_t group_size,
+                    void* scale, int scale_dtype, uint8_t* weight_packed, uint8_t* tiled, void* stream);
+
 /* ---- Measurement floors (no reference counterpart; for benchmarks) ----
  * lsq_probe_empty launches one empty workgroup: the cost of a launch itself.
  * lsq_probe_read streams `bytes` (1 .. 2^31 - 1) of `buf` once with 16-byte loads and

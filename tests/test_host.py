@@ -343,6 +343,15 @@ def test_library_rejects_bad_arguments_without_gpu():
                              16, None) == -1  # M > 0 needs x
     assert lib.lsq_w8_linear(1 << 20, 128, 1 << 20, (1 << 20) + 8, 1 << 20, 0, None, 0, 1 << 20,
                              16, 2, 1, 16, 128, None) == -6  # tiled copy not 16-byte aligned
+    # the quantizer: shapes, dtypes, missing outputs and layouts before any HIP call
+    assert lib.lsq_quantize_w8(1 << 20, 2, 8, 16, 16, 1 << 20, 1 << 20, None, None) == -2  # ldw < K
+    assert lib.lsq_quantize_w8(1 << 20, 3, 16, 16, 16, 1 << 20, 1 << 20, None, None) == -3  # int8 input
+    assert lib.lsq_quantize_w8(1 << 20, 2, 16, 16, 16, 1 << 20, None, None, None) == -1  # no output
+    assert lib.lsq_quantize_w8(1 << 20, 2, 100, 16, 100, 1 << 20, None, 1 << 20, None) == -5  # tiled, K % 128
+    assert lib.lsq_quantize_w4(1 << 20, 2, 16, 16, 16, -1, 1 << 20, 0, 1 << 20, None, None) == -4
+    assert lib.lsq_quantize_w4(1 << 20, 2, 16, 16, 16, 0, 1 << 20, 2, 1 << 20, None, None) == -3  # per channel: fp32
+    assert lib.lsq_quantize_w4(1 << 20, 2, 256, 16, 256, 12, 1 << 20, 2, None, 1 << 20, None) == -5  # group % 8
+    assert lib.lsq_quantize_w4(None, 2, 16, 0, 16, 0, None, 0, None, None, None) == 0  # N = 0: nothing to do
     # measurement probes: sizes and launch shapes are checked before any HIP call
     assert lib.lsq_probe_read(1 << 20, 0, 1 << 20, 256, 512, None) == -2
     assert lib.lsq_probe_read(1 << 20, 1 << 31, 1 << 20, 256, 512, None) == -2

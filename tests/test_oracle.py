@@ -145,6 +145,24 @@ def test_group_quantizer_reduces_to_per_channel():
     assert np.array_equal(pg, pc)
 
 
+def test_group_quantizer_uses_the_stored_scale_known_answer():
+    """Group-wise INT4 quantizes against the scale as stored (rounded to its dtype), worked
+    by hand. Group 0 = [7.013671875, 3.50390625]: max / 7 = 1 + 2^-9 exactly in fp32. bf16
+    keeps 7 mantissa bits, so 1 + 2^-9 (a quarter ulp above 1.0) is stored as 1.0 and
+    3.50390625 / 1.0 rounds to 4; fp16 keeps 10 bits, stores 1 + 2^-9 exactly, and
+    3.50390625 / 1.001953125 = 3.4970... rounds to 3. Group 1 = [-7.0, 2.5]: scale 1.0,
+    2.5 is a tie and rounds to the even 2. A quantizer using the unrounded fp32 scale would
+    give 3 for bf16 too; one rounding ties away from zero would give 3 for 2.5."""
+    w = np.array([[7.013671875, 3.50390625, -7.0, 2.5]], np.float32)
+    p, s = qo.quantize_int4(w, group_size=2, scale_dt="bf16")
+    assert s.tolist() == [[1.0, 1.0]]
+    assert qo.unpack_int4(p, 4).tolist() == [[7, 4, -7, 2]]
+    assert p.tolist() == [[0xCF, 0xA1]]  # q + 8 = 15, 12 | 1, 10; low nibble = even column
+    p16, s16 = qo.quantize_int4(w, group_size=2, scale_dt="f16")
+    assert s16.tolist() == [[1.001953125, 1.0]]
+    assert qo.unpack_int4(p16, 4).tolist() == [[7, 3, -7, 2]]
+
+
 # ----------------------------------------------------------------------------- dequant
 
 
