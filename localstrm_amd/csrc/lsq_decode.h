@@ -56,6 +56,13 @@ int launch_decode_a8(const LinearArgs& a, bool fused, hipStream_t s);
 template <int DT>
 int launch_gemv(int kind, const LinearArgs& a, hipStream_t s);
 
+// Batched decode GEMV for 17..64 tokens on the tiled layouts of layers with ~1000+ row
+// tiles (lsq_bgemv.hip): whole row tiles per workgroup, K split over its waves, the
+// activations loaded into registers. Returns LSQ_E_LAYOUT without launching anything for
+// what it does not cover.
+template <int DT>
+int launch_bgemv(int kind, const LinearArgs& a, hipStream_t s);
+
 // Batched decode, 16 < M <= 64 tokens (activations streamed through LDS in chunks).
 // Same contract as launch_decode.
 template <int DT>

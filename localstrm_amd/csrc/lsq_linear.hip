@@ -153,6 +153,7 @@ static int dispatch(bool w4, const void* x, int64_t ldx, const uint8_t* w, const
       // K = 18944) the chunked decode; else the prefill GEMM
       int rc = LSQ_E_LAYOUT;
       if (M <= 16) rc = launch_gemv<DT>(kind, a, s);
+      if (rc == LSQ_E_LAYOUT && M > 16 && M <= 64) rc = launch_bgemv<DT>(kind, a, s);
       if (rc == LSQ_E_LAYOUT && M <= 64) rc = launch_decode<DT>(kind, a, s);
       if (rc == LSQ_E_LAYOUT && M <= 64) rc = launch_decode_mb<DT>(kind, a, s);
       if (rc == LSQ_E_LAYOUT && M > 16) rc = launch_gemm<DT>(kind, a, s);
