@@ -4,11 +4,11 @@
 // decode tokens (the engine's batched decode step, src/engine/model_runner.py:199-205).
 //
 // Work split. As in the 1..16-token GEMV (lsq_gemv.hip) the workgroups take balanced,
-// contiguous ranges of whole 16-row tiles (at most 5: 237 workgroups at N = 18944), so no
-// output is shared between workgroups. Inside a workgroup 8 waves (two per SIMD, so that
-// one wave's VALU work overlaps the other's MFMAs) split K and the tokens: wave w takes k
-// tiles p, p + 4, p + 8, ... (p = w % 4) of token half h = w / 4, for all the workgroup's
-// row tiles. A wave thus needs only the activations of its own k tiles and tokens: it DMAs
+// contiguous ranges of whole 16-row tiles (at most 1, 3 or 5 by layer size: 56 workgroups
+// at N = 896, 203 at 9728, 237 at 18944), so no output is shared between workgroups.
+// Inside a workgroup 8 waves (two per SIMD, so that one wave's VALU work overlaps the
+// other's MFMAs) split K and the tokens: wave w takes k tiles p, p + 4, p + 8, ...
+// (p = w % 4) of token half h = w / 4, for all the workgroup's row tiles. A wave thus needs only the activations of its own k tiles and tokens: it DMAs
 // them (buffer_load ... lds, 1 KB contiguous per instruction) into an LDS slab of its own,
 // double-buffered, and reads them back in MFMA operand order; x is read once per
 // workgroup, and the main loop has no workgroup barrier, so the waves never wait for each
@@ -46,7 +46,7 @@ namespace {
 constexpr int kBgPhases = 4;              // k phases: wave w takes k tiles w % 4 + 4 i
 constexpr int kBgHalves = 2;              // token halves: wave w takes tokens of half w / 4
 constexpr int kBgWaves = kBgPhases * kBgHalves;
-constexpr int kBgRows = 5;   // row tiles per workgroup, at most
+constexpr int kBgRows = 5;   // row tiles per workgroup, at most (layers of 769+ row tiles)
 constexpr int kBgDepth = 2;  // k tiles in flight per wave
 
 // 16 bytes per lane from `r` at per-lane offset `voff` into LDS at `lds` + 16 * lane (a
@@ -63,14 +63,14 @@ __device__ __forceinline__ void dma16(rsrc_t r, unsigned char* lds, uint32_t vof
 // 8 KB x MT of its slabs).
 __host__ __device__ constexpr int bgemv_slab(int mt) { return 16 * mt * 256; }
 __host__ __device__ constexpr int bgemv_slabs_bytes(int mt) { return kBgWaves * kBgDepth * bgemv_slab(mt); }
-__host__ __device__ inline int64_t bgemv_lds(int mt, int64_t ngs) {
-  return bgemv_slabs_bytes(mt) + (int64_t(kBgRows) * kTileN * ngs * 2 + 15) / 16 * 16;
+__host__ __device__ inline int64_t bgemv_lds(int mt, int rm, int64_t ngs) {
+  return bgemv_slabs_bytes(mt) + (int64_t(rm) * kTileN * ngs * 2 + 15) / 16 * 16;
 }
 static_assert(kBgRows * 4 * 64 * 4 <= kBgDepth * 16 * 256, "the partial sums must fit the activation slabs");
 
-template <int DT, bool W4, bool GROUPED, int MT>
+template <int DT, bool W4, bool GROUPED, int MT, int RM>
 __global__ void __launch_bounds__(64 * kBgWaves) bgemv_kernel(LinearArgs p) {
-  constexpr int P = kBgPhases, RM = kBgRows, D = kBgDepth;
+  constexpr int P = kBgPhases, D = kBgDepth;
   constexpr int kTileB = W4 ? kTileBytes : kTileBytes8;
   constexpr int LPT = W4 ? 1 : 2;    // 16-byte weight loads per lane per unit
   constexpr int kDma = 16 * MT / 4;  // DMA instructions per slab (4 rows = 1 KB each)
@@ -300,11 +300,15 @@ __global__ void __launch_bounds__(64 * kBgWaves) bgemv_kernel(LinearArgs p) {
 
 // ------------------------------------------------------------------ launch
 
-// LSQ_BGEMV=0 turns this kernel off, LSQ_BGEMV=1 uses it for every shape it covers; by
-// default it serves INT4 layers at 33..64 tokens, where it measured faster than the
-// chunked decode kernel (18944 x 3584, M = 64: 23.3 vs 32.0 us). INT8 (its weights are
-// streamed once per token half, 2 KB per tile) and up to 32 tokens measured slower
-// (INT8 M = 64 30.6 vs 25.2 us; INT4 M = 32 17.8 vs 16.9 us).
+// LSQ_BGEMV=0 turns this kernel off, LSQ_BGEMV=1 uses it for every shape it covers. By
+// default it serves the shapes where it measured faster than the decode kernels: INT4 at
+// 33..64 tokens (18944 x 3584, M = 64: 23.3 vs 32.0 us) and at 17..32 tokens below 1000
+// row tiles (896 x 4864 M = 20: 7.8 vs 13.2 us; 9728 x 896 M = 32: 6.5 vs 7.5 us), INT8
+// up to 256 row tiles (896 x 4864 M = 32: 10.2 vs 12.1 us; 4096 x 14336 M = 64: 38 vs
+// 49 us). Larger INT8 layers (their weights are streamed once per token half, 2 KB per
+// tile) and INT4 up to 32 tokens at 1000+ row tiles measured slower (INT8 18944 x 3584
+// M = 64 30.6 vs 25.2 us, 9728 x 896 M = 32 7.7 vs 7.1 us; INT4 18944 x 3584 M = 32
+// 17.8 vs 16.9 us).
 int bgemv_mode() {
   const char* e = std::getenv("LSQ_BGEMV");
   return e && e[0] == '0' ? 0 : (e && e[0] == '1' ? 1 : 2);
@@ -324,10 +328,10 @@ int bgemv_max_lds() {
   return v;
 }
 
-template <int DT, bool W4, bool GROUPED, int MT>
+template <int DT, bool W4, bool GROUPED, int MT, int RM>
 int bgemv_one(const LinearArgs& a, int grid, hipStream_t s) {
-  auto kern = bgemv_kernel<DT, W4, GROUPED, MT>;
-  const int64_t lds = bgemv_lds(MT, GROUPED ? a.ngroups : 1);
+  auto kern = bgemv_kernel<DT, W4, GROUPED, MT, RM>;
+  const int64_t lds = bgemv_lds(MT, RM, GROUPED ? a.ngroups : 1);
   if (lds > bgemv_max_lds()) return LSQ_E_LAYOUT;
   if (lds > 64 * 1024) {
     static std::atomic<int> attr_set{0};
@@ -338,14 +342,23 @@ int bgemv_one(const LinearArgs& a, int grid, hipStream_t s) {
       attr_set.store(1, std::memory_order_release);
     }
   }
-  bgemv_kernel<DT, W4, GROUPED, MT><<<dim3(static_cast<unsigned>(grid)), dim3(64 * kBgWaves), static_cast<size_t>(lds), s>>>(a);
+  bgemv_kernel<DT, W4, GROUPED, MT, RM><<<dim3(static_cast<unsigned>(grid)), dim3(64 * kBgWaves), static_cast<size_t>(lds), s>>>(a);
   return static_cast<int>(hipGetLastError());
 }
 
-template <int DT, bool W4, bool GROUPED>
+template <int DT, bool W4, bool GROUPED, int RM>
 int bgemv_kind(const LinearArgs& a, int grid, hipStream_t s) {
   // token blocks per wave: two halves of 1 (up to 32 tokens) or 2 (up to 64) blocks
-  return a.M <= 32 ? bgemv_one<DT, W4, GROUPED, 1>(a, grid, s) : bgemv_one<DT, W4, GROUPED, 2>(a, grid, s);
+  return a.M <= 32 ? bgemv_one<DT, W4, GROUPED, 1, RM>(a, grid, s) : bgemv_one<DT, W4, GROUPED, 2, RM>(a, grid, s);
+}
+
+// Row tiles per workgroup: 1 up to 256 row tiles, 3 up to 768, 5 beyond (at most 256
+// workgroups each way but for 769..999 row tiles, 154-200 workgroups).
+template <int DT, bool W4, bool GROUPED>
+int bgemv_rows(const LinearArgs& a, int64_t nrt, hipStream_t s) {
+  if (nrt <= 256) return bgemv_kind<DT, W4, GROUPED, 1>(a, static_cast<int>(nrt), s);
+  if (nrt <= 768) return bgemv_kind<DT, W4, GROUPED, 3>(a, static_cast<int>((nrt + 2) / 3), s);
+  return bgemv_kind<DT, W4, GROUPED, kBgRows>(a, static_cast<int>((nrt + kBgRows - 1) / kBgRows), s);
 }
 
 }  // namespace
@@ -356,25 +369,22 @@ int launch_bgemv(int kind, const LinearArgs& a, hipStream_t s) {
   if (mode == 0 || a.act != LSQ_ACT_NONE || a.xscale) return LSQ_E_LAYOUT;
   if (kind != kW4Tiled && kind != kW8Tiled) return LSQ_E_LAYOUT;
   if (a.M <= 16 || a.M > 64 || a.K % kTileK != 0 || a.K < kTileK || a.N < 1) return LSQ_E_LAYOUT;
-  if (mode == 2 && (kind != kW4Tiled || a.M <= 32)) return LSQ_E_LAYOUT;
   const bool w4 = kind == kW4Tiled;
+  // Every workgroup owns whole row tiles (1, 3 or 5 by layer size: 896 x 4864 runs 56
+  // workgroups of one, 9728 x 896 203 of three, 18944 x 3584 237 of five).
+  const int64_t nrt = (a.N + kTileN - 1) / kTileN;
+  if (mode == 2 && (w4 ? (a.M <= 32 && nrt >= 1000) : nrt > 256)) return LSQ_E_LAYOUT;
   const bool grouped = w4 && a.group < a.K;
   if (grouped && (a.group % kTileK != 0 || ((a.group / kTileK) & (a.group / kTileK - 1)) != 0)) return LSQ_E_LAYOUT;
   auto aligned4 = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 3) == 0; };
   if (!aligned4(a.scale) || (a.bias && !aligned4(a.bias))) return LSQ_E_LAYOUT;
-  // Layers with many row tiles: every workgroup owns whole row tiles, at most 5, so the
-  // grid covers the CUs only from ~1000 row tiles on (18944 rows: 237 workgroups).
-  const int64_t nrt = (a.N + kTileN - 1) / kTileN;
-  if (nrt < 1000) return LSQ_E_LAYOUT;
-  const int64_t grid = (nrt + kBgRows - 1) / kBgRows;
-  if (grid > 65535) return LSQ_E_LAYOUT;
+  if ((nrt + kBgRows - 1) / kBgRows > 65535) return LSQ_E_LAYOUT;
   // 32-bit buffer offsets: 64 token rows of x (a token row past M is out of range by its
   // row offset alone), one workgroup's weights and scales
   if ((int64_t(64) * a.ldx + a.K) * 2 >= (int64_t(1) << 31)) return LSQ_E_LAYOUT;
   if (int64_t(kBgRows) * (a.K / kTileK) * kTileBytes8 >= (int64_t(1) << 31)) return LSQ_E_LAYOUT;
-  if (!w4) return bgemv_kind<DT, false, false>(a, static_cast<int>(grid), s);
-  return grouped ? bgemv_kind<DT, true, true>(a, static_cast<int>(grid), s)
-                 : bgemv_kind<DT, true, false>(a, static_cast<int>(grid), s);
+  if (!w4) return bgemv_rows<DT, false, false>(a, nrt, s);
+  return grouped ? bgemv_rows<DT, true, true>(a, nrt, s) : bgemv_rows<DT, true, false>(a, nrt, s);
 }
 
 template int launch_bgemv<LSQ_BF16>(int, const LinearArgs&, hipStream_t);

@@ -1,8 +1,9 @@
-"""GPU parity of the batched decode GEMV (lsq_bgemv.hip: 17..64 tokens on layers of 1000+
-row tiles, whole row tiles per workgroup, K and the tokens split over its 8 waves,
-activations DMA'd into per-wave LDS slabs, the phases' partial sums added in order). By
-default the kernel serves INT4 at 33..64 tokens; the tests force it for every shape it
-covers (LSQ_BGEMV=1) so that every instantiation runs.
+"""GPU parity of the batched decode GEMV (lsq_bgemv.hip: 17..64 tokens, whole row tiles per
+workgroup (1, 3 or 5 by layer size), K and the tokens split over its 8 waves, activations
+DMA'd into per-wave LDS slabs, the phases' partial sums added in order). By default the
+kernel serves INT4 at 33..64 tokens, INT4 at 17..32 tokens below 1000 row tiles and INT8
+up to 256 row tiles; most tests force it for every shape it covers (LSQ_BGEMV=1) so that
+every instantiation runs, and one runs the default dispatch on the Qwen2.5-0.5B shapes.
 
 Bars as in test_gpu_parity.py: rel = max|y - y_ref| / max|y_ref| <= 1e-2 against the
 float64 oracle (oracle.quant_oracle.linear_f64 on the oracle's dequantized weights,
@@ -131,3 +132,31 @@ def test_bgemv_deterministic_and_matches_previous_kernel(monkeypatch):
     err = qo.rel_err(y1, y_old.astype(np.float64))
     _say(f"  new vs chunked decode kernel: rel={err:.3e}")
     assert err <= REL_TOL
+
+
+@pytest.mark.parametrize("m", [17, 32, 48, 64])
+@pytest.mark.parametrize("kind", ["int4", "int8"])
+def test_bgemv_small_layers(kind, m):
+    """The one- and three-row-tile workgroups: the Qwen2.5-0.5B projections of the batched
+    decode step (896 x 4864 down: 56 workgroups of one row tile; 4864 x 896 gate / up: 102
+    of three; 1152 x 896 fused q/k/v: 72 of one; 128 x 896 k / v: 8 of one)."""
+    for n, k in ((896, 4864), (4864, 896), (1152, 896), (128, 896)):
+        _check(kind, n, k, m, bias=(n != 896), seed=n + k + m)
+
+
+@pytest.mark.parametrize("n", [4090, 4096, 4112, 12288, 12304])
+def test_bgemv_row_tile_bands(n):
+    """Row-tile counts at the 1 / 3 / 5 boundaries: 256 (one each), 257 (86 workgroups of
+    three or two), 768 (256 of three), 769 (154 of five or four); 4090 rows end in a
+    partial tile."""
+    for kind in ("int4", "int8"):
+        _check(kind, n, 1024, 40, bias=True, seed=n)
+
+
+@pytest.mark.parametrize("m", [20, 32, 64])
+def test_bgemv_default_dispatch_qwen05b(m, monkeypatch):
+    """The default policy (no LSQ_BGEMV) on the 0.5B shapes it now takes, INT4 and INT8."""
+    monkeypatch.delenv("LSQ_BGEMV", raising=False)
+    for kind in ("int4", "int8"):
+        for n, k in ((896, 4864), (9728, 896), (896, 896)):
+            _check(kind, n, k, m, seed=3 * n + k + m)
