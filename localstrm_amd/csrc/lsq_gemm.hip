@@ -41,6 +41,13 @@ typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
+// 16 bytes per lane from `r` (per-lane offset `voff`, scalar offset `soff`) into LDS at
+// `lds` + 16 * lane (a device function of its own: with the builtin in a kernel body,
+// clang emitted no host launch stub for some instantiations).
+__device__ __forceinline__ void dma16_lds(rsrc_t r, unsigned char* lds, uint32_t voff, int soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, soff, 0, 0);
+}
+
 constexpr int BM = 256, BN = 256, BK = 64, NT = 512;
 constexpr int WTM = 128, WTN = 64;  // wave tile: 2 x 4 waves
 constexpr int FM = WTM / 32, FN = WTN / 32;  // 32x32 MFMA blocks per wave
@@ -211,9 +218,7 @@ __global__ void __launch_bounds__(NT) gemm_kernel(LinearArgs p) {
 #pragma unroll
     for (int b = 0; b < kXB; ++b) {
       const int rb = (wid * kXB + b) * 8;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          rx, (__attribute__((address_space(3))) void*)(dst + rb * BK * 2), 16,
-          x_lane_off[b], static_cast<int>(gstep(st) * BK * 2), 0, 0);
+      dma16_lds(rx, dst + rb * BK * 2, x_lane_off[b], static_cast<int>(gstep(st) * BK * 2));
     }
   };
 
@@ -398,27 +403,25 @@ __global__ void __launch_bounds__(NT) gemm_kernel(LinearArgs p) {
 }
 
 // ---------------------------------------------------------------------------------------
-// Register-weight variant. A workgroup of 4 waves computes a 128 x 128 tile (128 x 256
-// selectable, half the workgroups); two such workgroups share a CU (one wave of
-// each per SIMD), each with its own barrier, so one workgroup's barrier and LDS latency
-// bubbles are filled by the other's MFMAs. Wave w owns columns [64 w, 64 w + 64) (or
-// [32 w, 32 w + 32)) for all 128 rows (4 x 2 or 4 x 1 blocks of 32 x 32). Only the
-// activations go through LDS (two 16 KB stages, DMA one step ahead); each wave loads its
+// Register-weight variant, two shapes. 128 x 128 tiles: 4 waves, two workgroups per CU
+// (one wave of each per SIMD), each with its own barrier, so one workgroup's barrier and
+// LDS latency bubbles are filled by the other's MFMAs. 256 x 256 tiles: 8 waves (two per
+// SIMD), one workgroup per CU. Either way wave w owns weight rows (output columns)
+// [32 w, 32 w + 32) for all the tile's activation rows (RFM x 1 blocks of 32 x 32). Only
+// the activations go through LDS (two stages, DMA one step ahead); each wave loads its
 // own weight rows straight into registers in MFMA operand order (three steps in flight)
 // and dequantizes them right before use, so weight tiles never touch LDS.
 // K order inside a step: lane l at 16-column sub-step kk multiplies columns
 // 32 (l >> 5) + 8 kk .. +7 (the same permutation on both operands), which makes each
 // lane's weights one contiguous 32-column chunk per step.
-constexpr int RBM = 128, RNT = 256;
-constexpr int RFM = RBM / 32;
-constexpr int kRLdsBytes = 2 * RBM * BK * 2;
+__host__ __device__ constexpr int rw_lds_bytes(int rbm) { return 2 * rbm * BK * 2; }
 
-// RFN_ 32-column blocks per wave: 2 (128 x 256 tiles) or 1 (128 x 128 tiles, twice the
-// workgroups, for layers whose 128 x 256 tiles would leave CUs idle).
-template <int DT, int KIND, bool GROUPED, int RFN_>
-__global__ void __launch_bounds__(RNT, 2) gemm_rw_kernel(LinearArgs p) {
-  constexpr int RFN = RFN_;
-  constexpr int RBN = 4 * 32 * RFN;
+// RFN_ 32-column blocks per wave, RFM_ 32-row blocks, RNT_ threads, MINB workgroups per CU.
+template <int DT, int KIND, bool GROUPED, int RFN_, int RFM_, int RNT_, int MINB>
+__global__ void __launch_bounds__(RNT_, MINB) gemm_rw_kernel(LinearArgs p) {
+  constexpr int RFN = RFN_, RFM = RFM_, RNT = RNT_;
+  constexpr int RBM = 32 * RFM;
+  constexpr int RBN = (RNT / 64) * 32 * RFN;
   constexpr bool W4 = KIND == kW4Tiled || KIND == kW4Canon;
   constexpr bool TILED = KIND == kW4Tiled || KIND == kW8Tiled;
   constexpr int WLB = W4 ? 1 : 2;  // 16-byte loads per lane per 32-row block per step
@@ -487,9 +490,7 @@ __global__ void __launch_bounds__(RNT, 2) gemm_rw_kernel(LinearArgs p) {
 #pragma unroll
     for (int b = 0; b < kXB; ++b) {
       const int rb = (wid * kXB + b) * 8;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          rx, (__attribute__((address_space(3))) void*)(dst + rb * BK * 2), 16,
-          x_lane_off[b], static_cast<int>(gstep(st) * BK * 2), 0, 0);
+      dma16_lds(rx, dst + rb * BK * 2, x_lane_off[b], static_cast<int>(gstep(st) * BK * 2));
     }
   };
 
@@ -536,16 +537,20 @@ __global__ void __launch_bounds__(RNT, 2) gemm_rw_kernel(LinearArgs p) {
   const int frow = lane & 31;
   auto frag_off = [&](int kk) { return frow * (BK * 2) + (((4 * h + kk) ^ ((frow >> 1) & 7)) << 4); };
 
+  // A fragments, double-buffered by sub-step; a[0] holds sub-step 0 of the next step when
+  // a step starts. The step's barrier sits before its last sub-step's MFMAs: right after
+  // it the next step's first fragments are read from the other LDS stage while those
+  // MFMAs run, so the MFMA pipe does not drain at the barrier.
+  u32x4 a[2][RFM];
+  auto load_a = [&](int buf, int kk, u32x4 (&aa)[RFM]) {
+    const unsigned char* xb = smem + buf * kStage;
+    const int off = frag_off(kk);
+#pragma unroll
+    for (int i = 0; i < RFM; ++i) aa[i] = *reinterpret_cast<const u32x4*>(xb + 32 * i * (BK * 2) + off);
+  };
   auto step = [&](int st, const WSet& cur, WSet& nxt2) {
     const int buf = st & 1;
-    const unsigned char* xb = smem + buf * kStage;
-    u32x4 a[2][RFM];
-    auto load_a = [&](int kk, u32x4 (&aa)[RFM]) {
-      const int off = frag_off(kk);
-#pragma unroll
-      for (int i = 0; i < RFM; ++i) aa[i] = *reinterpret_cast<const u32x4*>(xb + 32 * i * (BK * 2) + off);
-    };
-    load_a(0, a[0]);
+    // stage buf ^ 1 was last read before the previous step's barrier
     issue_x(st + 1, buf ^ 1);
     issue_w(st + 2, nxt2);
     float sf[RFN], cf[RFN];
@@ -572,19 +577,38 @@ __global__ void __launch_bounds__(RNT, 2) gemm_rw_kernel(LinearArgs p) {
 #pragma unroll
     for (int kk = 0; kk < BK / 16; ++kk) {
       if (kk + 1 < BK / 16) {
-        load_a(kk + 1, a[(kk + 1) & 1]);
+        load_a(buf, kk + 1, a[(kk + 1) & 1]);
         dequant(kk + 1, b[(kk + 1) & 1]);
+      } else {
+        // The next step's activation DMA must have landed (the weight loads issued after
+        // it, for two steps ahead, stay in flight); the barrier also orders every wave's
+        // reads of this stage before the next step's DMA into it.
+        constexpr int kAfter = RFN * WLB + (GROUPED ? RFN : 0);
+        __builtin_amdgcn_s_waitcnt((kAfter & 15) | (7 << 4) | ((kAfter >> 4) << 14));
+        lds_barrier();
+        load_a(buf ^ 1, 0, a[0]);
       }
 #pragma unroll
       for (int i = 0; i < RFM; ++i)
 #pragma unroll
         for (int j = 0; j < RFN; ++j) acc[i][j] = Mma32<DT>::mma(a[kk & 1][i], b[kk & 1][j], acc[i][j]);
+      if constexpr (W4 && RFM * RFN == 8) {
+        // Issue order for the INT4 256 x 32 wave tile, twice per sub-step: four of the
+        // next fragment reads, then four MFMAs with three VALU ops (dequantization) after
+        // each. Measured 3 % faster than the compiler's own order (14336 x 4096, INT4
+        // g128: M=2048 226 -> 219 us, M=8192 909 -> 883 us); the INT8 instances spill
+        // registers under it and keep the compiler's order.
+#pragma unroll
+        for (int h2 = 0; h2 < 2; ++h2) {
+          __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);  // DS reads
+#pragma unroll
+          for (int m = 0; m < 4; ++m) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // VALU
+          }
+        }
+      }
     }
-    // Before the barrier only this step's activation DMA must have landed: the weight
-    // loads issued after it (for two steps ahead) stay in flight.
-    constexpr int kAfter = RFN * WLB + (GROUPED ? RFN : 0);
-    __builtin_amdgcn_s_waitcnt((kAfter & 15) | (7 << 4) | ((kAfter >> 4) << 14));
-    lds_barrier();
   };
 
   WSet r0, r1, r2;
@@ -596,6 +620,7 @@ __global__ void __launch_bounds__(RNT, 2) gemm_rw_kernel(LinearArgs p) {
     __builtin_amdgcn_s_waitcnt((kAfter & 15) | (7 << 4) | ((kAfter >> 4) << 14));
   }
   lds_barrier();
+  load_a(0, 0, a[0]);
   int st = 0;
   for (; st + 3 <= nsteps; st += 3) {
     step(st, r0, r2);
@@ -637,36 +662,42 @@ __global__ void __launch_bounds__(RNT, 2) gemm_rw_kernel(LinearArgs p) {
     }
 }
 
-template <int DT, int KIND, bool GROUPED>
-int launch_rw(const LinearArgs& a, hipStream_t s) {
-  const int64_t mt = (a.M + RBM - 1) / RBM;
-  const int64_t wide = mt * ((a.N + 255) / 256);
-  // 128-column tiles measured faster at every size this kernel serves (14336 x 4096:
-  // M=256 77 -> 55 us, M=768 136 -> 130 us); LSQ_GEMM_RW_N=2 forces 256 (tests, tuning).
-  const char* e = std::getenv("LSQ_GEMM_RW_N");
-  const bool narrow = !(e && e[0] == '2');
-  if (narrow) {
-    const int64_t tiles = mt * ((a.N + 127) / 128);
-    gemm_rw_kernel<DT, KIND, GROUPED, 1><<<dim3(static_cast<unsigned>(tiles)), dim3(RNT), kRLdsBytes, s>>>(a);
-  } else {
-    gemm_rw_kernel<DT, KIND, GROUPED, 2><<<dim3(static_cast<unsigned>(wide)), dim3(RNT), kRLdsBytes, s>>>(a);
-  }
+template <int DT, int KIND, bool GROUPED, int RFN, int RFM, int RNT, int MINB>
+int launch_rw_shape(const LinearArgs& a, hipStream_t s) {
+  constexpr int rbm = 32 * RFM, rbn = (RNT / 64) * 32 * RFN;
+  const int64_t tiles = ((a.M + rbm - 1) / rbm) * ((a.N + rbn - 1) / rbn);
+  gemm_rw_kernel<DT, KIND, GROUPED, RFN, RFM, RNT, MINB>
+      <<<dim3(static_cast<unsigned>(tiles)), dim3(RNT), rw_lds_bytes(rbm), s>>>(a);
   return static_cast<int>(hipGetLastError());
 }
 
-// Which prefill kernel: the register-weight one up to 768 tokens (it launches twice as
-// many workgroups, which decides small M), the LDS-weight one above (fewer dequantized
-// weights per output). LSQ_GEMM=reg|lds forces one (tests, tuning).
-bool use_rw(int64_t M) {
+// Register-weight shapes: 0 = 128 x 128 tiles (4 waves of 128 x 32, two workgroups per
+// CU), 1 = 256 x 256 (8 waves of 256 x 32, one workgroup per CU).
+template <int DT, int KIND, bool GROUPED>
+int launch_rw(const LinearArgs& a, int shape, hipStream_t s) {
+  if (shape == 1) return launch_rw_shape<DT, KIND, GROUPED, 1, 8, 512, 1>(a, s);
+  return launch_rw_shape<DT, KIND, GROUPED, 1, 4, 256, 2>(a, s);
+}
+
+// Which prefill kernel. Up to 768 tokens the register-weight kernel with 128 x 128 tiles
+// (four times the workgroups of 256 x 256 tiles, which decides small M; 14336 x 4096
+// M=256: 55 us against 77 us with 128 x 256 tiles); above, the register-weight kernel
+// with 256 x 256 tiles: each weight is dequantized once per 256 activation rows, as in
+// the LDS-weight kernel, but never stored to LDS (14336 x 4096 INT4 g128, same box:
+// M=2048 244 -> 219 us, M=8192 ~945 -> 883 us). LSQ_GEMM=reg|wide|lds forces one (tests,
+// tuning). Returns the register-weight shape, or -1 for the LDS-weight kernel.
+int rw_shape(int64_t M) {
   const char* e = std::getenv("LSQ_GEMM");
-  if (e && e[0] == 'r') return true;
-  if (e && e[0] == 'l') return false;
-  return M <= 768;
+  if (e && e[0] == 'r') return 0;
+  if (e && e[0] == 'w') return 1;
+  if (e && e[0] == 'l') return -1;
+  return M <= 768 ? 0 : 1;
 }
 
 template <int DT, int KIND, bool GROUPED>
 int launch_kind(const LinearArgs& a, hipStream_t s) {
-  if (use_rw(a.M)) return launch_rw<DT, KIND, GROUPED>(a, s);
+  const int shape = rw_shape(a.M);
+  if (shape >= 0) return launch_rw<DT, KIND, GROUPED>(a, shape, s);
   auto kern = gemm_kernel<DT, KIND, GROUPED>;
   static std::atomic<int> attr_set{0};
   if (!attr_set.load(std::memory_order_acquire)) {

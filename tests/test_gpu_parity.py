@@ -250,16 +250,14 @@ def test_int4_g128_prefill_config_shape(m, layout, monkeypatch):
     assert err <= REL_TOL
 
 
-@pytest.mark.parametrize("variant", ["reg", "reg-wide", "lds"])
+@pytest.mark.parametrize("variant", ["reg", "wide", "lds"])
 @pytest.mark.parametrize("kind", ["int8", "int4"])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_gemm_edges_bias_and_dtypes(kind, dtype, variant, monkeypatch):
-    """Both prefill kernels (register weights with 128- and 256-column tiles, LDS weights)
-    on ragged M and N edges (M=300, N=272 = 256 + 16), bias, both dtypes, per-channel INT8,
-    group-128 INT4, and per-channel INT4."""
-    monkeypatch.setenv("LSQ_GEMM", "reg" if variant.startswith("reg") else variant)
-    if variant == "reg-wide":
-        monkeypatch.setenv("LSQ_GEMM_RW_N", "2")
+    """Every prefill kernel (register weights with 128 x 128 and 256 x 256 tiles, LDS
+    weights) on ragged M and N edges (M=300, N=272 = 256 + 16), bias, both dtypes,
+    per-channel INT8, group-128 INT4, and per-channel INT4."""
+    monkeypatch.setenv("LSQ_GEMM", variant)
     _check_layer(kind, 272, 512, 300, group=128, dtype=dtype, bias=True, seed=7)
     if kind == "int4":
         _check_layer("int4", 272, 512, 300, group=512, dtype=dtype, bias=True, seed=8)
