@@ -585,7 +585,7 @@ __global__ void __launch_bounds__(64 * RG * KS) decode_kernel(LinearArgs p) {
             const int m = 16 * mb + 4 * q + e;
             const float g = vt[mb][e];
             const float u = xch[(((rg >> 1) * MB + mb) * 4 + e) * 64 + lane];
-            const float sg = Act<DT>::round(opaque(g / (1.f + __expf(-g))));
+            const float sg = Act<DT>::round(opaque(g / (1.f + expf(-g))));
             // fp32 product, then the rounding to T (not one fused multiply-round)
             if (m < M && 2 * j < N) y[static_cast<int64_t>(m) * p.ldy + j] = Act<DT>::from_f32(opaque(sg * u));
           }

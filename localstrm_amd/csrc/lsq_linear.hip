@@ -180,7 +180,7 @@ __global__ void __launch_bounds__(256) silu_mul_kernel(const typename Act<DT>::s
   const int64_t c = 32 * (j >> 4) + (j & 15);
   const float g = Act<DT>::to_f32(in[m * ldi + c]);
   const float u = Act<DT>::to_f32(in[m * ldi + c + 16]);
-  const float sg = Act<DT>::round(opaque(g / (1.f + __expf(-g))));
+  const float sg = Act<DT>::round(opaque(g / (1.f + expf(-g))));
   out[m * ldo + j] = Act<DT>::from_f32(opaque(sg * u));  // fp32 product, then round to T
 }
 

@@ -222,6 +222,25 @@ def test_decode_large_k_small_n(kind, m):
     _check_layer(kind, 3584, 18944, m, rows=rows, bias=(m % 2 == 0), seed=m)
 
 
+@pytest.mark.parametrize("kind", ["int8", "int4"])
+def test_chunked_decode_6x2_one_block(kind):
+    """16384 x 16384 at 8 tokens: x (256 KB) exceeds LDS, so the chunked decode runs its
+    6 x 2 workgroups with one 16-token block; oracle on 256 rows."""
+    rows = np.sort(np.random.default_rng(300).choice(16384, 256, replace=False))
+    _check_layer(kind, 16384, 16384, 8, rows=rows, bias=True, seed=11)
+
+
+@pytest.mark.parametrize("rg", ["4", "8"])
+@pytest.mark.parametrize("m", [4, 16])
+def test_chunked_decode_waves_per_workgroup(m, rg, monkeypatch):
+    """3584 x 18944 with LSQ_DECODE_MB_RG forcing 4 or 8 waves per workgroup (the 2 x 2
+    and 4 x 1 fallbacks of the one-block path); oracle on 256 rows."""
+    monkeypatch.setenv("LSQ_DECODE_MB_RG", rg)
+    rows = np.sort(np.random.default_rng(400 + m).choice(3584, 256, replace=False))
+    for kind in ("int4", "int8"):
+        _check_layer(kind, 3584, 18944, m, rows=rows, bias=(m == 4), seed=m + 1)
+
+
 @pytest.mark.parametrize("m", [9, 16])
 def test_decode_qwen05b_down_proj_16_tokens(m):
     """896 x 4864 (Qwen2.5-0.5B down_proj) at 9 and 16 tokens: chunked decode."""

@@ -258,6 +258,21 @@ def test_w8a8_large_k_token_blocks(m, n, k):
 
 
 @pytest.mark.parametrize("dt", ["bf16", "f16", "f32"])
+@pytest.mark.parametrize("m", [1, 2])
+def test_w8a8_long_rows_quantized_in_kernel_dtypes(dt, m):
+    # one or two rows of 18944 activations (the decode kernel quantizes them itself) in
+    # every activation type: fp32 at M=1 is 4736 16-byte chunks
+    _say(f"w8a8 long rows {dt} M={m} N=3584 K=18944")
+    x, wq, sw, bias = _lin_inputs(dt, m, 3584, 18944)
+    y, _, _ = _linear(x.to(DEV), wq, sw, bias)
+    ref = qo.w8a8_linear(x.float().numpy(), wq.numpy(), sw.numpy(),
+                         None if bias is None else bias.float().numpy(), dt)
+    got = y.float().cpu().numpy()
+    mism = np.count_nonzero(_bits(got) != _bits(ref))
+    assert mism == 0, f"{mism} of {got.size} outputs differ"
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16", "f32"])
 @pytest.mark.parametrize("m,n,k", [(1, 272, 896), (5, 1000, 896), (16, 272, 2048), (64, 272, 896)])
 def test_w8a8_unfused_decode_bit_exact(monkeypatch, dt, m, n, k):
     # the same shapes through act_quant_kernel + the decode kernel on x_q
