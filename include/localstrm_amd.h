@@ -126,6 +126,27 @@ int lsq_w4_linear(const void* x, int64_t ldx, const uint8_t* weight_packed,
                   int64_t group_size, const void* bias, int bias_dtype, void* y, int64_t ldy,
                   int dtype, int64_t M, int64_t N, int64_t K, void* stream);
 
+/* ---- The same forwards with a caller-provided workspace ----
+ * Same contract and results as lsq_w8_linear / lsq_w4_linear (the same reference lines,
+ * quantization.py:129-141), plus `workspace` (device memory, 16-byte aligned, or NULL) of
+ * `workspace_bytes`. With at least lsq_linear_workspace_bytes(M, N, K) bytes, decode
+ * shapes of 1-16 tokens on layers of fewer than 1024 16-row tiles and K of 8+ 128-column
+ * tiles (down projections such as 3584 x 18944) split K over workgroups: each slice's
+ * fp32 partial sums go to the workspace and a second kernel adds them in slice order,
+ * adds the bias and rounds to T. With a smaller or NULL workspace these calls behave
+ * exactly like the plain entry points. The workspace is scratch for the duration of the
+ * call on `stream` (its contents are not read before being written). */
+int64_t lsq_linear_workspace_bytes(int64_t M, int64_t N, int64_t K);
+int lsq_w8_linear_ws(const void* x, int64_t ldx, const int8_t* weight_q, const int8_t* tiled,
+                     const void* scale, int scale_dtype, const void* bias, int bias_dtype, void* y,
+                     int64_t ldy, int dtype, int64_t M, int64_t N, int64_t K, void* workspace,
+                     int64_t workspace_bytes, void* stream);
+int lsq_w4_linear_ws(const void* x, int64_t ldx, const uint8_t* weight_packed,
+                     const uint8_t* tiled, const void* scale, int scale_dtype,
+                     int64_t group_size, const void* bias, int bias_dtype, void* y, int64_t ldy,
+                     int dtype, int64_t M, int64_t N, int64_t K, void* workspace,
+                     int64_t workspace_bytes, void* stream);
+
 /* ---- Fused gate / up with the SiLU.mul epilogue ----
  * The MLP of the reference's decoder layers computes down_proj(silu(gate_proj(x)) *
  * up_proj(x)) (modeling_qwen2.py:46-48), two launches and two elementwise kernels. No

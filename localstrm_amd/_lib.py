@@ -44,6 +44,17 @@ SIGNATURES = {
         _int,
         [_vp, _i64, _vp, _vp, _vp, _int, _i64, _vp, _int, _vp, _i64, _int, _i64, _i64, _i64, _vp],
     ),
+    "lsq_linear_workspace_bytes": (_i64, [_i64, _i64, _i64]),
+    "lsq_w8_linear_ws": (
+        _int,
+        [_vp, _i64, _vp, _vp, _vp, _int, _vp, _int, _vp, _i64, _int, _i64, _i64, _i64, _vp, _i64,
+         _vp],
+    ),
+    "lsq_w4_linear_ws": (
+        _int,
+        [_vp, _i64, _vp, _vp, _vp, _int, _i64, _vp, _int, _vp, _i64, _int, _i64, _i64, _i64, _vp,
+         _i64, _vp],
+    ),
     "lsq_w8_linear_act": (
         _int,
         [_vp, _i64, _vp, _vp, _vp, _int, _vp, _int, _vp, _i64, _int, _i64, _i64, _i64, _int, _vp],

@@ -31,6 +31,9 @@ struct LinearArgs {
   const float* xscale = nullptr;  // W8A8 only: per-token activation scales [M]
   int act = 0;                    // LSQ_ACT_SILU_MUL: gate / up rows interleaved by 16-row
                                   // tiles, y [M, N / 2] = silu(gate) * up (decode kernel only)
+  float* part = nullptr;          // split-K workspace: fp32 partial sums [ksplit][M][N]
+  int64_t part_bytes = 0;         // its size (0: no split)
+  int ksplit = 1;                 // K slices of the split-K GEMV (set by its launcher)
 };
 
 // Launches the LDS-staged decode kernel when the shape fits it (M <= 64, K % 128 == 0,
@@ -50,11 +53,16 @@ template <int DT>
 int launch_decode_a8(const LinearArgs& a, bool fused, hipStream_t s);
 
 // Decode GEMV for 1..16 tokens on the tiled INT4 / INT8 layouts (lsq_gemv.hip): whole row
-// tiles per workgroup, balanced over the grid. Returns LSQ_E_LAYOUT without launching
-// anything for shapes, layouts or modes it does not cover (canonical layouts, the SiLU.mul
-// epilogue, W8A8, activations too large for LDS).
+// tiles per workgroup, balanced over the grid; on layers of fewer than 1024 row tiles with
+// a workspace (a.part), split over K slices, the slices' fp32 sums added by a second
+// kernel in slice order. Returns LSQ_E_LAYOUT without launching anything for shapes,
+// layouts or modes it does not cover (canonical layouts, the SiLU.mul epilogue, W8A8,
+// activations too large for LDS).
 template <int DT>
 int launch_gemv(int kind, const LinearArgs& a, hipStream_t s);
+
+// Workspace bytes launch_gemv's split-K path needs for this shape (0: it does not split).
+int64_t gemv_split_bytes(int64_t M, int64_t N, int64_t K);
 
 // Batched decode GEMV for 17..64 tokens on the tiled layouts of layers with ~1000+ row
 // tiles (lsq_bgemv.hip): whole row tiles per workgroup, K split over its waves, the

@@ -39,6 +39,7 @@
 #include "lsq_decode.h"
 #include "lsq_mfma16.h"
 
+#include <algorithm>
 #include <atomic>
 #include <cstdio>
 #include <cstdlib>
@@ -66,6 +67,14 @@ __host__ __device__ inline GemvLds gemv_lds(int64_t M, int64_t K, int64_t rows, 
   l.sb = l.ss + align16(rows * ngs * 2);
   l.total = l.sb + align16(rows * 2);
   return l;
+}
+
+// Scale groups per row the LDS layout holds: all ngs, or with S > 1 slices of at most
+// kst k tiles the most one slice can touch (it may straddle a group boundary).
+__host__ __device__ inline int gemv_lds_groups(int ngs, int S, int kst, int gtiles, bool grouped) {
+  if (S <= 1 || !grouped) return ngs;
+  const int g = (kst + gtiles - 1) / gtiles + 1;
+  return g < ngs ? g : ngs;
 }
 
 // Sum of a float over each row of 16 lanes, in every lane of the row (DPP).
@@ -100,12 +109,26 @@ __global__ void __launch_bounds__(64 * W) gemv_kernel(LinearArgs p) {
   extern __shared__ __align__(16) unsigned char smem[];
   using S = typename Act<DT>::storage;
 
-  const int M = static_cast<int>(p.M), N = static_cast<int>(p.N), K = static_cast<int>(p.K);
-  const int nkt = K / kTileK;
+  const int M = static_cast<int>(p.M), N = static_cast<int>(p.N);
+  // K slices (split-K: workgroup b takes slice b % NS of row-tile range b / NS; NS = 1
+  // otherwise). `nkt` counts the k tiles of this workgroup's slice, which start at k tile
+  // `kt_s0` of the layer's `nkt_all`.
+  const int NS = p.ksplit;
+  const int nkt_all = static_cast<int>(p.K / kTileK);
+  const int sl = NS > 1 ? static_cast<int>(blockIdx.x) % NS : 0;
+  const int kt_s0 = sl * nkt_all / NS;
+  const int nkt = (sl + 1) * nkt_all / NS - kt_s0;
+  const int K = nkt * kTileK;  // columns of the slice
+  const int kmax = ((nkt_all + NS - 1) / NS) * kTileK;  // the widest slice (LDS layout)
   const int nrt = (N + kTileN - 1) / kTileN;
   const int ngs = GROUPED ? static_cast<int>(p.ngroups) : 1;
   const int gtiles = static_cast<int>(p.group / kTileK);
-  const int ldxb = (K + 8) * 2;  // LDS bytes per staged activation row
+  const int gshift = __builtin_ctz(static_cast<uint32_t>(gtiles));  // k tiles per group: a power of two
+  // scale groups staged per row: all of them, or with a split those of the slice
+  const int gs0 = NS > 1 && GROUPED ? kt_s0 >> gshift : 0;
+  const int ngs_s = NS > 1 && GROUPED ? ((kt_s0 + nkt - 1) >> gshift) - gs0 + 1 : ngs;
+  const int ngs_lds = gemv_lds_groups(ngs, NS, kmax / kTileK, gtiles, GROUPED);
+  const int ldxb = (kmax + 8) * 2;  // LDS bytes per staged activation row
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -113,8 +136,8 @@ __global__ void __launch_bounds__(64 * W) gemv_kernel(LinearArgs p) {
   const int r = lane & 15, q = lane >> 4;
   // Row tiles: the first `rem` workgroups take base + 1, the others base (one 32-bit
   // division; the code before the first load is on every wave's critical path).
-  const int G = gridDim.x;
-  const int b = blockIdx.x;
+  const int G = gridDim.x / NS;
+  const int b = blockIdx.x / NS;
   const int base = nrt / G;
   const int rem = nrt - base * G;
   const int rt_lo = b * base + min(b, rem);
@@ -125,7 +148,7 @@ __global__ void __launch_bounds__(64 * W) gemv_kernel(LinearArgs p) {
   const int row0 = rt_lo * kTileN;
   const int rows_valid = min(R * kTileN, N - row0);
 
-  const GemvLds L = gemv_lds(M, K, int64_t(rmax) * kTileN, ngs, W, NE);
+  const GemvLds L = gemv_lds(M, kmax, int64_t(rmax) * kTileN, ngs_lds, W, NE);
   unsigned char* xs = smem + L.xs;
   float* red = reinterpret_cast<float*>(smem + L.red);
   int* cnt = reinterpret_cast<int*>(smem + L.cnt);
@@ -136,11 +159,13 @@ __global__ void __launch_bounds__(64 * W) gemv_kernel(LinearArgs p) {
   // ---- descriptors over what this workgroup reads
   const int es_s = p.scale_dt == LSQ_F32 ? 4 : 2;
   const int es_b = p.bias_dt == LSQ_F32 ? 4 : 2;
-  const rsrc_t rx = make_rsrc(p.x, static_cast<uint32_t>(((M - 1) * p.ldx + K) * 2));
-  const rsrc_t rw = make_rsrc(p.w + static_cast<int64_t>(rt_lo) * nkt * kTileB,
-                              static_cast<uint32_t>(T * kTileB));
+  const rsrc_t rx = make_rsrc(static_cast<const uint16_t*>(p.x) + static_cast<int64_t>(kt_s0) * kTileK,
+                              static_cast<uint32_t>(((M - 1) * p.ldx + K) * 2));
+  const rsrc_t rw = make_rsrc(p.w + static_cast<int64_t>(rt_lo) * nkt_all * kTileB,
+                              static_cast<uint32_t>(R * nkt_all * kTileB));
   const int nsc = rows_valid * ngs;
   const int nsd = (nsc * es_s + 3) / 4;
+  const int nse = rows_valid * ngs_s;  // scale elements staged (split: one per load)
   // The dword holding the last 16-bit element may extend 2 bytes past the array; an
   // aligned dword never crosses a page, so reading it is always safe.
   const rsrc_t rs = make_rsrc(static_cast<const uint8_t*>(p.scale) + static_cast<int64_t>(row0) * ngs * es_s,
@@ -167,11 +192,16 @@ __global__ void __launch_bounds__(64 * W) gemv_kernel(LinearArgs p) {
     const int m = row_of(c);
     return c < nch ? static_cast<uint32_t>((m * p.ldx + (c - m * K8) * 8) * 2) : kOOB;
   };
+  // Unit i of this wave's run: k tile kt0 + i of the run's first row tile, or (from
+  // kt0 + i = nkt on) of the next one; in memory a row tile holds all nkt_all k tiles.
+  const int rt_first = t_lo / nkt;
+  const int kt0 = t_lo - rt_first * nkt;
+  const int u_base = (rt_first * nkt_all + kt_s0 + kt0) * kTileB + lane * 16;
+  const int u_skip = (nkt_all - nkt) * kTileB;  // into the next row tile (0 without split)
   u32x4 wbuf[D][LPT];
   auto issue = [&](u32x4 (&wv)[LPT], int i) {
-    const int t = t_lo + i;
-    const bool real = t < t_hi;
-    const uint32_t off = static_cast<uint32_t>(t * kTileB + lane * 16);
+    const bool real = t_lo + i < t_hi;
+    const uint32_t off = static_cast<uint32_t>(u_base + i * kTileB + (kt0 + i >= nkt ? u_skip : 0));
     wv[0] = bload16<kNT>(rw, real ? off : kOOB);
     if (LPT == 2) wv[LPT - 1] = bload16<kNT>(rw, real ? off + kTileB / 2 : kOOB);
   };
@@ -201,14 +231,30 @@ __global__ void __launch_bounds__(64 * W) gemv_kernel(LinearArgs p) {
 #pragma unroll
     for (int u = 0; u < XB; ++u) v[u] = bload16<0>(rx, x_off(c0 + u * NT + tid));
   };
+  // Split: element e of the staged scales is group gs0 + e % ngs_s of row e / ngs_s.
+  auto s_byte = [&](int e) {
+    const int row = e / ngs_s;
+    return static_cast<uint32_t>((row * ngs + gs0 + (e - row * ngs_s)) * es_s);
+  };
   auto load_s = [&](uint32_t (&v)[kGemvSB], int t0) {
 #pragma unroll
     for (int u = 0; u < kGemvSB; ++u) {
       const int t = t0 + u * NT + tid;
-      v[u] = bload4(rs, t < nsd ? t * 4 : kOOB);
+      if (NS > 1)
+        v[u] = bload4(rs, t < nse ? s_byte(t) & ~3u : kOOB);
+      else
+        v[u] = bload4(rs, t < nsd ? t * 4 : kOOB);
     }
   };
   auto put_scales = [&](const uint32_t (&v)[kGemvSB], int t0) {
+    if (NS > 1) {  // uniform
+#pragma unroll
+      for (int u = 0; u < kGemvSB; ++u) {
+        const int t = t0 + u * NT + tid;
+        if (t < nse) ss[t] = Act<DT>::from_f32(dword_elem(v[u], (s_byte(t) >> 1) & 1, p.scale_dt));
+      }
+      return;
+    }
     if (p.scale_dt == DT) {  // uniform: already T, copy the stored bits
 #pragma unroll
       for (int u = 0; u < kGemvSB; ++u) {
@@ -239,7 +285,8 @@ __global__ void __launch_bounds__(64 * W) gemv_kernel(LinearArgs p) {
     }
   };
   // (bias: rows * 4 <= 16 W * 4 bytes, one dword per thread at most)
-  if (nch <= NT * XB && nsd <= NT * kGemvSB) {  // uniform
+  const int nsl = NS > 1 ? nse : nsd;  // scale loads
+  if (nch <= NT * XB && nsl <= NT * kGemvSB) {  // uniform
     u32x4 xv[XB];
     uint32_t sv[kGemvSB];
     load_x(xv, 0);
@@ -257,7 +304,7 @@ __global__ void __launch_bounds__(64 * W) gemv_kernel(LinearArgs p) {
       load_x(xv, c0);
       put_x(xv, c0);
     }
-    for (int t0 = 0; t0 < nsd; t0 += NT * kGemvSB) {
+    for (int t0 = 0; t0 < nsl; t0 += NT * kGemvSB) {
       uint32_t sv[kGemvSB];
       load_s(sv, t0);
       put_scales(sv, t0);
@@ -281,13 +328,10 @@ __global__ void __launch_bounds__(64 * W) gemv_kernel(LinearArgs p) {
   // of the next one; each unit's sum goes into acc_a or acc_b accordingly (uniform).
   f32x4 acc_a = {0.f, 0.f, 0.f, 0.f}, acc_b = {0.f, 0.f, 0.f, 0.f};
   const int n_my = t_hi - t_lo;
-  const int rt_first = t_lo / nkt;
-  const int kt0 = t_lo - rt_first * nkt;
-  const int gshift = __builtin_ctz(static_cast<uint32_t>(gtiles));  // k tiles per group: a power of two
   const unsigned char* xrow = xs + min(r, M) * ldxb + 32 * q * 2;
   // this lane's scale row in the run's first and second row tile
-  const uint16_t* srow_a = ss + (rt_first * kTileN + r) * ngs;
-  const uint16_t* srow_b = srow_a + kTileN * ngs;
+  const uint16_t* srow_a = ss + (rt_first * kTileN + r) * ngs_s;
+  const uint16_t* srow_b = srow_a + kTileN * ngs_s;
   uint32_t nib_mask = 0, magic = 0;
   if constexpr (W4) {
     // constants in registers, so that the unpack selects v_and_or_b32
@@ -315,7 +359,7 @@ __global__ void __launch_bounds__(64 * W) gemv_kernel(LinearArgs p) {
 #pragma unroll
             for (int e = 0; e < NE; ++e) xo[e] = x4[e];
           }
-          scg = Act<DT>::to_f32((second ? srow_b : srow_a)[kt >> gshift]);
+          scg = Act<DT>::to_f32((second ? srow_b : srow_a)[((kt_s0 + kt) >> gshift) - gs0]);
         }
 #pragma unroll
         for (int d = 0; d < 4; ++d)
@@ -368,8 +412,12 @@ __global__ void __launch_bounds__(64 * W) gemv_kernel(LinearArgs p) {
         for (int k2 = 0; k2 < nkt; ++k2) tot += xsum[k2 * 16 + m];
         val = fmaf(-Mma<DT>::kOff4, tot, val);
       }
-      if (m < M && n < N)
-        y[static_cast<int64_t>(m) * p.ldy + n] = Act<DT>::from_f32(opaque(GROUPED ? val + bias : fmaf(val, sc, bias)));
+      if (m < M && n < N) {
+        if (NS > 1)  // this slice's scaled sum; the bias and the rounding come in the merge
+          p.part[(static_cast<int64_t>(sl) * M + m) * N + n] = GROUPED ? val : val * sc;
+        else
+          y[static_cast<int64_t>(m) * p.ldy + n] = Act<DT>::from_f32(opaque(GROUPED ? val + bias : fmaf(val, sc, bias)));
+      }
     }
   };
   auto publish = [&](int j, int slot, const f32x4& part) {
@@ -425,6 +473,47 @@ GemvCfg pick_gemv(int64_t nrt, int64_t nkt) {
   return GemvCfg{rpw, w, 3};
 }
 
+// Split-K plan for layers of at most 512 row tiles whose activations are too large for
+// the LDS-staged decode kernel (more than 96 KB: 4+ tokens at K = 18944, 16 at K = 4864),
+// which the chunked decode kernel serves otherwise (down projections: 3584 x 18944,
+// 4096 x 14336, 896 x 4864). K is cut into S slices of at least 4 k tiles, with x of one
+// slice no larger than one staging batch of 16 waves (16 KB for one token, 32 KB up to 4,
+// 64 KB up to 16: then its loads are issued together with the weight ring), and about one
+// workgroup per CU: `ranges` balanced row-tile ranges of at most 16 row tiles, times S.
+// Measured (us, INT4 g128, unsplit -> split): 3584 x 18944 M=4 25.6 -> 15.4, M=16
+// 26.4 -> 18.1 (S = 5..20: 18.1-27.3), 4096 x 14336 M=16 20.9 -> 16.4; smaller x stays
+// unsplit (3584 x 18944 M=2: 11.9 unsplit, 14.8-15.2 split), as do wider layers
+// (14336 x 4096 M=16: 13.9 unsplit, 15.2 split). S = 1: no split. LSQ_SPLITK=0 turns the
+// split off, LSQ_SPLITK=n forces n slices (read at every call).
+struct GemvSplit {
+  int64_t S, ranges, bytes;
+};
+
+GemvSplit gemv_split_plan(int64_t M, int64_t N, int64_t K) {
+  const int64_t nrt = (N + kTileN - 1) / kTileN;
+  const int64_t nkt = K / kTileK;
+  GemvSplit sp{1, 0, 0};
+  if (M < 1 || M > 16 || K % kTileK != 0 || nrt >= 1024 || nkt < 8) return sp;
+  const char* e = std::getenv("LSQ_SPLITK");
+  if (e && e[0] == '0') return sp;
+  const int64_t forced = e ? std::atoi(e) : 0;  // LSQ_SPLITK=n >= 2: n slices (sweeps)
+  if (forced < 2 && (nrt > 512 || M * K * 2 <= 96 * 1024)) return sp;
+  const int64_t rmin_ranges = (nrt + 15) / 16;
+  const int64_t batch = int64_t(16) * 1024 * gemv_xb(M == 1 ? 1 : (M <= 4 ? 4 : 16), 1024);
+  int64_t S = (M * K * 2 + batch - 1) / batch;
+  if (S < 1) S = 1;
+  for (; S <= nkt / 4; ++S) {
+    const int64_t ranges = std::min(nrt, std::max(rmin_ranges, int64_t(256) / S));
+    if (ranges * S >= 192) break;
+  }
+  if (forced >= 2) S = forced;
+  if (S < 2 || S > nkt / 4) return sp;
+  sp.S = S;
+  sp.ranges = std::min(nrt, std::max(rmin_ranges, int64_t(256) / S));
+  sp.bytes = S * M * N * 4;
+  return sp;
+}
+
 int g_gemv_max_lds = -1;
 
 int gemv_max_lds() {
@@ -441,13 +530,21 @@ int gemv_max_lds() {
 
 template <int DT, bool W4, bool GROUPED, int MT, int W, int D>
 int gemv_one(const LinearArgs& a, int grid, hipStream_t s) {
+  // grid = row-tile ranges x a.ksplit K slices
+  const int S = a.ksplit;
   const int64_t nrt = (a.N + kTileN - 1) / kTileN;
-  const int64_t rmax = (nrt + grid - 1) / grid;
-  const int64_t rmin = nrt / grid;
+  const int64_t ranges = grid / S;
+  const int64_t rmax = (nrt + ranges - 1) / ranges;
+  const int64_t rmin = nrt / ranges;
+  const int64_t nkt = a.K / kTileK;
+  const int64_t kst_min = nkt / S, kst_max = (nkt + S - 1) / S;  // k tiles per slice
   // a wave's run stays within two row tiles (R <= W) and is never empty (T >= W)
-  if (rmax > W || rmin * (a.K / kTileK) < W) return LSQ_E_LAYOUT;
+  if (rmax > W || rmin * kst_min < W) return LSQ_E_LAYOUT;
   constexpr int NE = MT < 4 ? MT : 4;
-  const GemvLds L = gemv_lds(a.M, a.K, rmax * kTileN, GROUPED ? a.ngroups : 1, W, NE);
+  const int ngs = GROUPED ? static_cast<int>(a.ngroups) : 1;
+  const GemvLds L = gemv_lds(a.M, kst_max * kTileK, rmax * kTileN,
+                             gemv_lds_groups(ngs, S, static_cast<int>(kst_max), static_cast<int>(a.group / kTileK), GROUPED),
+                             W, NE);
   if (L.total > gemv_max_lds()) return LSQ_E_LAYOUT;
   auto kern = gemv_kernel<DT, W4, GROUPED, MT, W, D>;
   if (L.total > 64 * 1024) {
@@ -478,17 +575,57 @@ int gemv_mt(const LinearArgs& a, const GemvCfg& c, int grid, hipStream_t s) {
 }
 
 template <int DT, bool W4, bool GROUPED>
+int gemv_grid(const LinearArgs& a, const GemvCfg& c, int grid, hipStream_t s) {
+  if (a.M == 1) return gemv_mt<DT, W4, GROUPED, 1>(a, c, grid, s);
+  if (a.M <= 4) return gemv_mt<DT, W4, GROUPED, 4>(a, c, grid, s);
+  return gemv_mt<DT, W4, GROUPED, 16>(a, c, grid, s);
+}
+
+// y[m, n] = round_T(sum over slices s = 0.. S-1, in that order, of part[s][m][n] +
+// round_T(bias[n])): the merge of the split-K GEMV.
+template <int DT>
+__global__ void __launch_bounds__(256) gemv_merge_kernel(const float* __restrict__ part, int S, int M, int N,
+                                                         const void* bias, int bias_dt,
+                                                         typename Act<DT>::storage* __restrict__ y, int64_t ldy) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= M * N) return;
+  const int m = i / N, n = i - m * N;
+  float v = part[i];
+  for (int sl = 1; sl < S; ++sl) v += part[static_cast<int64_t>(sl) * M * N + i];
+  if (bias) {
+    const uint16_t* b16 = static_cast<const uint16_t*>(bias);
+    const float bv = bias_dt == LSQ_F32 ? static_cast<const float*>(bias)[n]
+                                        : (bias_dt == LSQ_BF16 ? bf16_to_f32(b16[n]) : f16_to_f32(b16[n]));
+    v = opaque(v + Act<DT>::round(bv));
+  }
+  y[static_cast<int64_t>(m) * ldy + n] = Act<DT>::from_f32(v);
+}
+
+template <int DT, bool W4, bool GROUPED>
 int gemv_kind(const LinearArgs& a, hipStream_t s) {
   const int64_t nrt = (a.N + kTileN - 1) / kTileN;
   const int64_t nkt = a.K / kTileK;
   const GemvCfg c = pick_gemv(nrt, nkt);
-  if (c.rpw < 1) return LSQ_E_LAYOUT;
-  const int64_t rpw = c.rpw;
-  const int64_t grid = (nrt + rpw - 1) / rpw;
-  if (grid < 1 || grid > 65535) return LSQ_E_LAYOUT;
-  if (a.M == 1) return gemv_mt<DT, W4, GROUPED, 1>(a, c, static_cast<int>(grid), s);
-  if (a.M <= 4) return gemv_mt<DT, W4, GROUPED, 4>(a, c, static_cast<int>(grid), s);
-  return gemv_mt<DT, W4, GROUPED, 16>(a, c, static_cast<int>(grid), s);
+  if (c.rpw >= 1) {
+    const int64_t rpw = c.rpw;
+    const int64_t grid = (nrt + rpw - 1) / rpw;
+    if (grid < 1 || grid > 65535) return LSQ_E_LAYOUT;
+    return gemv_grid<DT, W4, GROUPED>(a, c, static_cast<int>(grid), s);
+  }
+  // Fewer than 1024 row tiles: the split-K form when it applies and a workspace is given.
+  const GemvSplit sp = gemv_split_plan(a.M, a.N, a.K);
+  if (sp.S < 2 || !a.part || a.part_bytes < sp.bytes) return LSQ_E_LAYOUT;
+  const int64_t units = (nrt / sp.ranges) * (nkt / sp.S);  // of the smallest workgroup
+  const GemvCfg cs{1, units >= 16 ? 16 : (units >= 8 ? 8 : 4), 3};
+  LinearArgs as = a;
+  as.ksplit = sp.S;
+  const int rc = gemv_grid<DT, W4, GROUPED>(as, cs, static_cast<int>(sp.ranges * sp.S), s);
+  if (rc != LSQ_OK) return rc;
+  using St = typename Act<DT>::storage;
+  const int64_t outs = a.M * a.N;
+  gemv_merge_kernel<DT><<<dim3(static_cast<unsigned>((outs + 255) / 256)), dim3(256), 0, s>>>(
+      a.part, sp.S, static_cast<int>(a.M), static_cast<int>(a.N), a.bias, a.bias_dt, static_cast<St*>(a.y), a.ldy);
+  return static_cast<int>(hipGetLastError());
 }
 
 }  // namespace
@@ -508,6 +645,11 @@ int launch_gemv(int kind, const LinearArgs& a, hipStream_t s) {
   if (int64_t(16) * (a.K / kTileK) * kTileBytes8 >= (int64_t(1) << 31)) return LSQ_E_LAYOUT;
   if (!w4) return gemv_kind<DT, false, false>(a, s);
   return grouped ? gemv_kind<DT, true, true>(a, s) : gemv_kind<DT, true, false>(a, s);
+}
+
+int64_t gemv_split_bytes(int64_t M, int64_t N, int64_t K) {
+  if (!gemv_enabled()) return 0;
+  return gemv_split_plan(M, N, K).bytes;
 }
 
 template int launch_gemv<LSQ_BF16>(int, const LinearArgs&, hipStream_t);

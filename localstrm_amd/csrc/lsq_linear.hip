@@ -133,7 +133,7 @@ template <int DT>
 static int dispatch(bool w4, const void* x, int64_t ldx, const uint8_t* w, const uint8_t* tiled,
                     const void* scale, int scale_dt, int64_t group, const void* bias, int bias_dt,
                     void* y, int64_t ldy, int64_t M, int64_t N, int64_t K, hipStream_t s,
-                    int act = LSQ_ACT_NONE) {
+                    int act = LSQ_ACT_NONE, void* ws = nullptr, int64_t ws_bytes = 0) {
   const int64_t ng = (K + group - 1) / group;
   if constexpr (DT != LSQ_F32) {
     const void* wf = tiled ? static_cast<const void*>(tiled) : static_cast<const void*>(w);
@@ -148,6 +148,8 @@ static int dispatch(bool w4, const void* x, int64_t ldx, const uint8_t* w, const
     if (mfma_ok) {
       LinearArgs a{x, ldx, tiled ? tiled : w, scale, scale_dt, bias, bias_dt, y, ldy,
                    M, N, K, group, ng};
+      a.part = static_cast<float*>(ws);
+      a.part_bytes = ws ? ws_bytes : 0;
       const int kind = w4 ? (tiled ? kW4Tiled : kW4Canon) : (tiled ? kW8Tiled : kW8);
       // decode with all activations in LDS; else (x too large for LDS, e.g. 4 tokens at
       // K = 18944) the chunked decode; else the prefill GEMM
@@ -221,7 +223,8 @@ extern "C" const char* lsq_status_string(int status) {
 
 static int w8_linear(const void* x, int64_t ldx, const int8_t* weight_q, const int8_t* tiled,
                      const void* scale, int scale_dtype, const void* bias, int bias_dtype, void* y,
-                     int64_t ldy, int dtype, int64_t M, int64_t N, int64_t K, void* stream, int act) {
+                     int64_t ldy, int dtype, int64_t M, int64_t N, int64_t K, void* stream, int act,
+                     void* ws = nullptr, int64_t ws_bytes = 0) {
   const int64_t ny = act == LSQ_ACT_SILU_MUL ? N / 2 : N;  // output columns
   const int rc = check_common(x, ldx, weight_q, tiled, scale, y, ldy, dtype, bias_dtype, bias, M, ny, K);
   if (rc != LSQ_OK) return rc;
@@ -229,15 +232,16 @@ static int w8_linear(const void* x, int64_t ldx, const int8_t* weight_q, const i
   if (scale_dtype != LSQ_F32 && scale_dtype != LSQ_F16 && scale_dtype != LSQ_BF16) return LSQ_E_DTYPE;
   if (tiled && (reinterpret_cast<uintptr_t>(tiled) & 15)) return LSQ_E_ALIGN;
   if (tiled && K % kTileK != 0) return LSQ_E_LAYOUT;
+  if (ws && ((reinterpret_cast<uintptr_t>(ws) & 15) || ws_bytes < 0)) return LSQ_E_ALIGN;
   if (M == 0 || N == 0) return LSQ_OK;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const uint8_t* w = reinterpret_cast<const uint8_t*>(weight_q);
   const uint8_t* t = reinterpret_cast<const uint8_t*>(tiled);
   const int64_t group = K > 0 ? K : 1;
   switch (dtype) {
-    case LSQ_F32: return dispatch<LSQ_F32>(false, x, ldx, w, t, scale, scale_dtype, group, bias, bias_dtype, y, ldy, M, N, K, s, act);
-    case LSQ_F16: return dispatch<LSQ_F16>(false, x, ldx, w, t, scale, scale_dtype, group, bias, bias_dtype, y, ldy, M, N, K, s, act);
-    default: return dispatch<LSQ_BF16>(false, x, ldx, w, t, scale, scale_dtype, group, bias, bias_dtype, y, ldy, M, N, K, s, act);
+    case LSQ_F32: return dispatch<LSQ_F32>(false, x, ldx, w, t, scale, scale_dtype, group, bias, bias_dtype, y, ldy, M, N, K, s, act, ws, ws_bytes);
+    case LSQ_F16: return dispatch<LSQ_F16>(false, x, ldx, w, t, scale, scale_dtype, group, bias, bias_dtype, y, ldy, M, N, K, s, act, ws, ws_bytes);
+    default: return dispatch<LSQ_BF16>(false, x, ldx, w, t, scale, scale_dtype, group, bias, bias_dtype, y, ldy, M, N, K, s, act, ws, ws_bytes);
   }
 }
 
@@ -247,6 +251,15 @@ extern "C" int lsq_w8_linear(const void* x, int64_t ldx, const int8_t* weight_q,
                              int64_t M, int64_t N, int64_t K, void* stream) {
   return w8_linear(x, ldx, weight_q, tiled, scale, scale_dtype, bias, bias_dtype, y, ldy, dtype, M,
                    N, K, stream, LSQ_ACT_NONE);
+}
+
+extern "C" int lsq_w8_linear_ws(const void* x, int64_t ldx, const int8_t* weight_q,
+                                const int8_t* tiled, const void* scale, int scale_dtype,
+                                const void* bias, int bias_dtype, void* y, int64_t ldy, int dtype,
+                                int64_t M, int64_t N, int64_t K, void* workspace,
+                                int64_t workspace_bytes, void* stream) {
+  return w8_linear(x, ldx, weight_q, tiled, scale, scale_dtype, bias, bias_dtype, y, ldy, dtype, M,
+                   N, K, stream, LSQ_ACT_NONE, workspace, workspace_bytes);
 }
 
 extern "C" int lsq_w8_linear_act(const void* x, int64_t ldx, const int8_t* weight_q,
@@ -260,7 +273,7 @@ extern "C" int lsq_w8_linear_act(const void* x, int64_t ldx, const int8_t* weigh
 static int w4_linear(const void* x, int64_t ldx, const uint8_t* weight_packed, const uint8_t* tiled,
                      const void* scale, int scale_dtype, int64_t group_size, const void* bias,
                      int bias_dtype, void* y, int64_t ldy, int dtype, int64_t M, int64_t N, int64_t K,
-                     void* stream, int act) {
+                     void* stream, int act, void* ws = nullptr, int64_t ws_bytes = 0) {
   const int64_t ny = act == LSQ_ACT_SILU_MUL ? N / 2 : N;  // output columns
   const int rc = check_common(x, ldx, weight_packed, tiled, scale, y, ldy, dtype, bias_dtype, bias, M, ny, K);
   if (rc != LSQ_OK) return rc;
@@ -269,13 +282,14 @@ static int w4_linear(const void* x, int64_t ldx, const uint8_t* weight_packed, c
   if (scale_dtype != LSQ_F32 && scale_dtype != LSQ_F16 && scale_dtype != LSQ_BF16) return LSQ_E_DTYPE;
   if (tiled && (reinterpret_cast<uintptr_t>(tiled) & 15)) return LSQ_E_ALIGN;
   if (tiled && K % kTileK != 0) return LSQ_E_LAYOUT;
+  if (ws && ((reinterpret_cast<uintptr_t>(ws) & 15) || ws_bytes < 0)) return LSQ_E_ALIGN;
   if (M == 0 || N == 0) return LSQ_OK;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int64_t group = K > 0 ? (group_size < K ? group_size : K) : 1;
   switch (dtype) {
-    case LSQ_F32: return dispatch<LSQ_F32>(true, x, ldx, weight_packed, tiled, scale, scale_dtype, group, bias, bias_dtype, y, ldy, M, N, K, s, act);
-    case LSQ_F16: return dispatch<LSQ_F16>(true, x, ldx, weight_packed, tiled, scale, scale_dtype, group, bias, bias_dtype, y, ldy, M, N, K, s, act);
-    default: return dispatch<LSQ_BF16>(true, x, ldx, weight_packed, tiled, scale, scale_dtype, group, bias, bias_dtype, y, ldy, M, N, K, s, act);
+    case LSQ_F32: return dispatch<LSQ_F32>(true, x, ldx, weight_packed, tiled, scale, scale_dtype, group, bias, bias_dtype, y, ldy, M, N, K, s, act, ws, ws_bytes);
+    case LSQ_F16: return dispatch<LSQ_F16>(true, x, ldx, weight_packed, tiled, scale, scale_dtype, group, bias, bias_dtype, y, ldy, M, N, K, s, act, ws, ws_bytes);
+    default: return dispatch<LSQ_BF16>(true, x, ldx, weight_packed, tiled, scale, scale_dtype, group, bias, bias_dtype, y, ldy, M, N, K, s, act, ws, ws_bytes);
   }
 }
 
@@ -285,6 +299,21 @@ extern "C" int lsq_w4_linear(const void* x, int64_t ldx, const uint8_t* weight_p
                              int64_t ldy, int dtype, int64_t M, int64_t N, int64_t K, void* stream) {
   return w4_linear(x, ldx, weight_packed, tiled, scale, scale_dtype, group_size, bias, bias_dtype, y,
                    ldy, dtype, M, N, K, stream, LSQ_ACT_NONE);
+}
+
+extern "C" int lsq_w4_linear_ws(const void* x, int64_t ldx, const uint8_t* weight_packed,
+                                const uint8_t* tiled, const void* scale, int scale_dtype,
+                                int64_t group_size, const void* bias, int bias_dtype, void* y,
+                                int64_t ldy, int dtype, int64_t M, int64_t N, int64_t K,
+                                void* workspace, int64_t workspace_bytes, void* stream) {
+  return w4_linear(x, ldx, weight_packed, tiled, scale, scale_dtype, group_size, bias, bias_dtype, y,
+                   ldy, dtype, M, N, K, stream, LSQ_ACT_NONE, workspace, workspace_bytes);
+}
+
+extern "C" int64_t lsq_linear_workspace_bytes(int64_t M, int64_t N, int64_t K) {
+  if (M < 0 || N < 0 || K < 0) return 0;
+  const int64_t b = gemv_split_bytes(M, N, K);
+  return (b + 255) / 256 * 256;
 }
 
 extern "C" int lsq_w4_linear_act(const void* x, int64_t ldx, const uint8_t* weight_packed,

@@ -125,3 +125,92 @@ def test_gemv_matches_previous_kernel_and_is_deterministic(monkeypatch):
     err = qo.rel_err(y1, y_old.astype(np.float64))
     _say(f"  new vs LDS-staged decode kernel: rel={err:.3e}")
     assert err <= REL_TOL
+
+
+# ---- split-K form (layers of fewer than 1024 row tiles, 8+ k tiles, 1-16 tokens): the
+# forward passes a workspace (lsq_linear_workspace_bytes), workgroups take (row-tile
+# range, K slice) pairs, a second kernel adds the slices in order.
+
+@pytest.mark.parametrize("m", [2, 3, 4, 8, 13, 16])
+@pytest.mark.parametrize("kind", ["int4", "int8"])
+def test_split_k_down_projection(kind, m, monkeypatch):
+    """3584 x 18944 (224 row tiles, 148 k tiles; 3 to 10 slices by M; at 2 tokens, whose
+    x the unsplit kernels serve by default, 3 slices forced), bias on odd M."""
+    if m == 2:
+        monkeypatch.setenv("LSQ_SPLITK", "3")
+    rows = np.sort(np.random.default_rng(500 + m).choice(3584, 384, replace=False))
+    _check(kind, 3584, 18944, m, bias=(m % 2 == 1), seed=m, rows=rows)
+
+
+@pytest.mark.parametrize("m", [1, 5, 16])
+@pytest.mark.parametrize("kind", ["int4", "int8"])
+def test_split_k_small_layers(kind, m, monkeypatch):
+    """896 x 4864 (Qwen2.5-0.5B down_proj: 56 row tiles, 38 k tiles in 4 slices of 9-10)
+    and 3590 x 8192 (a partial last row tile; 2-4 slices); the split is forced where the
+    default leaves these small activations to the unsplit kernels."""
+    if m < 16:
+        monkeypatch.setenv("LSQ_SPLITK", "4")
+    _check(kind, 896, 4864, m, bias=True, seed=m)
+    if m < 16:
+        monkeypatch.setenv("LSQ_SPLITK", "2")
+    rows = np.unique(np.concatenate([np.sort(np.random.default_rng(m).choice(3590, 256, replace=False)), [3589]]))
+    _check(kind, 3590, 8192, m, bias=(m != 5), seed=m + 1, rows=rows)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("group", [128, 256, 1024, 8192])
+def test_split_k_groups_and_dtypes(group, dtype):
+    """1040 x 8192 at 6 tokens (65 row tiles, 3 slices of 21-22 k tiles: slices straddle
+    group boundaries for groups of 2 and 8 k tiles), per-channel INT4 at group = K."""
+    _check("int4", 1040, 8192, 6, group=group, dtype=dtype, bias=True, seed=group)
+
+
+@pytest.mark.parametrize("sdt", [torch.float16, torch.float32])
+def test_split_k_scale_dtypes(sdt):
+    _check("int4", 1040, 8192, 7, scale_dtype=sdt, seed=13)
+
+
+def test_split_k_workspace_contract():
+    """Through the C ABI: the workspace size query, the split result bit-identical on a
+    repeat, a too-small or NULL workspace giving the unsplit kernels' result (the plain
+    entry point's, bit for bit), both within the contract of each other."""
+    from localstrm_amd import _lib
+    n, k, m = 3584, 18944, 8
+    w, s, x = bench.make_int4(n, k, m, 128, seed=31)
+    ql = QuantizedLinear.from_quantized(w.to(DEV), s.to(DEV), quant_type="int4", in_features=k,
+                                        group_size=128)
+    lib = _lib.load()
+    nws = lib.lsq_linear_workspace_bytes(m, n, k)
+    assert nws >= 4 * m * n * 2 and nws % 256 == 0
+    assert lib.lsq_linear_workspace_bytes(m, 18944, 3584) == 0   # 1184 row tiles: no split
+    assert lib.lsq_linear_workspace_bytes(32, n, k) == 0         # 17+ tokens: no split
+    xd = x.to(DEV)
+    tiled = ql.weight_tiled
+    stream = _lib.stream_handle(DEV)
+
+    def call(ws, nbytes):
+        y = torch.empty(m, n, dtype=torch.bfloat16, device=DEV)
+        args = (xd.data_ptr(), k, None, tiled.data_ptr(), ql.scale.data_ptr(),
+                _lib.dtype_code(ql.scale.dtype), 128, None, 0, y.data_ptr(), n,
+                _lib.dtype_code(torch.bfloat16), m, n, k)
+        if ws is False:
+            rc = lib.lsq_w4_linear(*args, stream)
+        else:
+            rc = lib.lsq_w4_linear_ws(*args, _lib.ptr(ws), nbytes, stream)
+        _lib.check(rc, "lsq_w4_linear(_ws)")
+        return y.float().cpu().numpy()
+
+    ws = torch.empty(nws, dtype=torch.uint8, device=DEV)
+    ys1, ys2 = call(ws, nws), call(ws, nws)
+    y_small = call(ws, nws - 256)
+    y_null = call(None, 0)
+    y_plain = call(False, 0)
+    assert np.array_equal(ys1.view(np.uint32), ys2.view(np.uint32))
+    assert np.array_equal(y_small.view(np.uint32), y_plain.view(np.uint32))
+    assert np.array_equal(y_null.view(np.uint32), y_plain.view(np.uint32))
+    err = qo.rel_err(ys1, y_plain.astype(np.float64))
+    _say(f"  split vs unsplit: rel={err:.3e}")
+    assert err <= REL_TOL
+    with torch.no_grad():
+        y_mod = ql(xd).float().cpu().numpy()   # the module passes a workspace
+    assert np.array_equal(y_mod.view(np.uint32), ys1.view(np.uint32))
