@@ -37,6 +37,7 @@
 #include "lsq_decode.h"
 #include "lsq_mfma16.h"
 
+#include <algorithm>
 #include <atomic>
 #include <cstdlib>
 
@@ -80,7 +81,13 @@ __global__ void __launch_bounds__(64 * kBgWaves) bgemv_kernel(LinearArgs p) {
   using S = typename Act<DT>::storage;
 
   const int M = static_cast<int>(p.M), N = static_cast<int>(p.N), K = static_cast<int>(p.K);
-  const int nkt = K / kTileK;
+  // K slices (split-K: workgroup b takes slice b % NS of row-tile range b / NS; NS = 1
+  // otherwise); `nkt` counts this slice's k tiles, from k tile `kt_s0` of `nkt_all`.
+  const int NS = p.ksplit;
+  const int nkt_all = K / kTileK;
+  const int sl = NS > 1 ? static_cast<int>(blockIdx.x) % NS : 0;
+  const int kt_s0 = sl * nkt_all / NS;
+  const int nkt = (sl + 1) * nkt_all / NS - kt_s0;
   const int nrt = (N + kTileN - 1) / kTileN;
   const int ngs = GROUPED ? static_cast<int>(p.ngroups) : 1;
   const int gshift = GROUPED ? __builtin_ctz(static_cast<uint32_t>(p.group / kTileK)) : 0;
@@ -91,8 +98,8 @@ __global__ void __launch_bounds__(64 * kBgWaves) bgemv_kernel(LinearArgs p) {
   const int ph = wid % P, half = wid / P;  // k phase, token half
   const int r = lane & 15, q = lane >> 4;
   // row tiles: the first `rem` workgroups take base + 1, the others base
-  const int G = gridDim.x;
-  const int b = blockIdx.x;
+  const int G = gridDim.x / NS;
+  const int b = blockIdx.x / NS;
   const int base = nrt / G;
   const int rem = nrt - base * G;
   const int rt_lo = b * base + min(b, rem);
@@ -103,8 +110,8 @@ __global__ void __launch_bounds__(64 * kBgWaves) bgemv_kernel(LinearArgs p) {
 
   // ---- descriptors over what this workgroup reads
   const rsrc_t rx = make_rsrc(p.x, static_cast<uint32_t>(((M - 1) * p.ldx + K) * 2));
-  const rsrc_t rw = make_rsrc(p.w + static_cast<int64_t>(rt_lo) * nkt * kTileB,
-                              static_cast<uint32_t>(R * nkt * kTileB));
+  const rsrc_t rw = make_rsrc(p.w + static_cast<int64_t>(rt_lo) * nkt_all * kTileB,
+                              static_cast<uint32_t>(R * nkt_all * kTileB));
   const int es_s = p.scale_dt == LSQ_F32 ? 4 : 2;
   // (the dword holding the last 16-bit element may reach 2 bytes past the array; an
   // aligned dword never crosses a page)
@@ -131,11 +138,11 @@ __global__ void __launch_bounds__(64 * kBgWaves) bgemv_kernel(LinearArgs p) {
 #pragma unroll
     for (int rt = 0; rt < RM; ++rt) {
       // row tiles >= R lie past the weight descriptor
-      const uint32_t off = static_cast<uint32_t>((rt * nkt + kt) * kTileB + lane * 16);
+      const uint32_t off = static_cast<uint32_t>((rt * nkt_all + kt_s0 + kt) * kTileB + lane * 16);
       wv[s][rt][0] = bload16<kNT>(rw, real ? off : kOOB);
       if (LPT == 2) wv[s][rt][LPT - 1] = bload16<kNT>(rw, real ? off + kTileB / 2 : kOOB);
     }
-    const uint32_t kx = static_cast<uint32_t>(kt * kTileK * 2);
+    const uint32_t kx = static_cast<uint32_t>((kt_s0 + kt) * kTileK * 2);
     unsigned char* dst = slabs + s * kSlab;
 #pragma unroll
     for (int j = 0; j < kDma; ++j)
@@ -217,7 +224,7 @@ __global__ void __launch_bounds__(64 * kBgWaves) bgemv_kernel(LinearArgs p) {
           for (int t = 0; t < MT; ++t) part[rt][t] = Mma<DT>::mma(xa[t], bb, d ? part[rt][t] : zero4);
         }
       }
-      const int g = min((ph + P * i) >> gshift, ngs - 1);
+      const int g = min((kt_s0 + ph + P * i) >> gshift, ngs - 1);
 #pragma unroll
       for (int rt = 0; rt < RM; ++rt) {
         const float sc = Act<DT>::to_f32(ss[srow[rt] + g]);
@@ -293,6 +300,10 @@ __global__ void __launch_bounds__(64 * kBgWaves) bgemv_kernel(LinearArgs p) {
     for (int w = 1; w < P; ++w) v += red[(P * hf + w) * kPart + pi];
     const uint32_t ebb = static_cast<uint32_t>(nl * es_b);
     const float bias = p.bias ? Act<DT>::round(dword_elem(bload4(rb, ebb & ~3u), (ebb >> 1) & 1, p.bias_dt)) : 0.f;
+    if (NS > 1) {  // this slice's scaled sum; the bias and the rounding come in the merge
+      p.part[(static_cast<int64_t>(sl) * M + m) * N + row0 + nl] = GROUPED ? v : v * Act<DT>::to_f32(ss[nl]);
+      continue;
+    }
     const float out = GROUPED ? v + bias : fmaf(v, Act<DT>::to_f32(ss[nl]), bias);
     y[static_cast<int64_t>(m) * p.ldy + row0 + nl] = Act<DT>::from_f32(opaque(out));
   }
@@ -352,6 +363,32 @@ int bgemv_kind(const LinearArgs& a, int grid, hipStream_t s) {
   return a.M <= 32 ? bgemv_one<DT, W4, GROUPED, 1, RM>(a, grid, s) : bgemv_one<DT, W4, GROUPED, 2, RM>(a, grid, s);
 }
 
+// Split-K plan for small-N layers with many k tiles (at most 128 row tiles, 16+ k tiles:
+// the Qwen2.5-0.5B down projection 896 x 4864), where one workgroup per row tile leaves
+// most CUs idle and each wave walks ~nkt / 4 k tiles: S slices of ~10 k tiles (2-3 per
+// wave), one row tile per workgroup, at most 512 workgroups; the merge adds the slices in
+// order. LSQ_SPLITK=0 turns it off, LSQ_SPLITK=n forces n slices.
+struct BgSplit {
+  int64_t S, bytes;
+};
+
+BgSplit bgemv_split_plan(int64_t M, int64_t N, int64_t K) {
+  BgSplit sp{1, 0};
+  const int64_t nrt = (N + kTileN - 1) / kTileN;
+  const int64_t nkt = K / kTileK;
+  if (M <= 16 || M > 64 || K % kTileK != 0 || nrt > 128 || nkt < 16) return sp;
+  const char* e = std::getenv("LSQ_SPLITK");
+  if (e && e[0] == '0') return sp;
+  const int64_t forced = e ? std::atoi(e) : 0;
+  int64_t S = forced >= 2 ? forced : (nkt + 9) / 10;
+  S = std::min<int64_t>(S, std::min<int64_t>(16, nkt));
+  if (forced < 2) S = std::min<int64_t>(S, 512 / nrt);
+  if (S < 2) return sp;
+  sp.S = S;
+  sp.bytes = S * M * N * 4;
+  return sp;
+}
+
 // Row tiles per workgroup: 1 up to 256 row tiles, 3 up to 768, 5 beyond (at most 256
 // workgroups each way but for 769..999 row tiles, 154-200 workgroups).
 template <int DT, bool W4, bool GROUPED>
@@ -383,8 +420,24 @@ int launch_bgemv(int kind, const LinearArgs& a, hipStream_t s) {
   // row offset alone), one workgroup's weights and scales
   if ((int64_t(64) * a.ldx + a.K) * 2 >= (int64_t(1) << 31)) return LSQ_E_LAYOUT;
   if (int64_t(kBgRows) * (a.K / kTileK) * kTileBytes8 >= (int64_t(1) << 31)) return LSQ_E_LAYOUT;
+  const BgSplit sp = bgemv_split_plan(a.M, a.N, a.K);
+  if (sp.S >= 2 && a.part && a.part_bytes >= sp.bytes) {
+    // one row tile per workgroup, times S slices
+    LinearArgs as = a;
+    as.ksplit = static_cast<int>(sp.S);
+    const int grid = static_cast<int>(nrt * sp.S);
+    const int rc = !w4 ? bgemv_kind<DT, false, false, 1>(as, grid, s)
+                       : (grouped ? bgemv_kind<DT, true, true, 1>(as, grid, s) : bgemv_kind<DT, true, false, 1>(as, grid, s));
+    if (rc != LSQ_OK) return rc;
+    return launch_split_merge<DT>(a.part, static_cast<int>(sp.S), a.M, a.N, a.bias, a.bias_dt, a.y, a.ldy, s);
+  }
   if (!w4) return bgemv_rows<DT, false, false>(a, nrt, s);
   return grouped ? bgemv_rows<DT, true, true>(a, nrt, s) : bgemv_rows<DT, true, false>(a, nrt, s);
+}
+
+int64_t bgemv_split_bytes(int64_t M, int64_t N, int64_t K) {
+  if (bgemv_mode() == 0) return 0;
+  return bgemv_split_plan(M, N, K).bytes;
 }
 
 template int launch_bgemv<LSQ_BF16>(int, const LinearArgs&, hipStream_t);

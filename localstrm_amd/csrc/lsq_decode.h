@@ -64,6 +64,15 @@ int launch_gemv(int kind, const LinearArgs& a, hipStream_t s);
 // Workspace bytes launch_gemv's split-K path needs for this shape (0: it does not split).
 int64_t gemv_split_bytes(int64_t M, int64_t N, int64_t K);
 
+// Workspace bytes launch_bgemv's split-K path needs for this shape (0: it does not split).
+int64_t bgemv_split_bytes(int64_t M, int64_t N, int64_t K);
+
+// y[m, n] = round_T(sum over s < S, in order, of part[s][m][n] + round_T(bias[n])): the
+// merge of the split-K GEMV kernels (lsq_gemv.hip).
+template <int DT>
+int launch_split_merge(const float* part, int S, int64_t M, int64_t N, const void* bias, int bias_dt,
+                       void* y, int64_t ldy, hipStream_t s);
+
 // Batched decode GEMV for 17..64 tokens on the tiled layouts of layers with ~1000+ row
 // tiles (lsq_bgemv.hip): whole row tiles per workgroup, K split over its waves, the
 // activations loaded into registers. Returns LSQ_E_LAYOUT without launching anything for

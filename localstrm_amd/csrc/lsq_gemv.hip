@@ -45,6 +45,11 @@
 #include <cstdlib>
 
 namespace lsq {
+
+template <int DT>
+int launch_split_merge(const float* part, int S, int64_t M, int64_t N, const void* bias, int bias_dt,
+                       void* y, int64_t ldy, hipStream_t s);
+
 namespace {
 
 // LDS layout (byte offsets), shared by kernel and host: partial sums `red` (two slots per
@@ -621,11 +626,7 @@ int gemv_kind(const LinearArgs& a, hipStream_t s) {
   as.ksplit = sp.S;
   const int rc = gemv_grid<DT, W4, GROUPED>(as, cs, static_cast<int>(sp.ranges * sp.S), s);
   if (rc != LSQ_OK) return rc;
-  using St = typename Act<DT>::storage;
-  const int64_t outs = a.M * a.N;
-  gemv_merge_kernel<DT><<<dim3(static_cast<unsigned>((outs + 255) / 256)), dim3(256), 0, s>>>(
-      a.part, sp.S, static_cast<int>(a.M), static_cast<int>(a.N), a.bias, a.bias_dt, static_cast<St*>(a.y), a.ldy);
-  return static_cast<int>(hipGetLastError());
+  return launch_split_merge<DT>(a.part, static_cast<int>(sp.S), a.M, a.N, a.bias, a.bias_dt, a.y, a.ldy, s);
 }
 
 }  // namespace
@@ -646,6 +647,18 @@ int launch_gemv(int kind, const LinearArgs& a, hipStream_t s) {
   if (!w4) return gemv_kind<DT, false, false>(a, s);
   return grouped ? gemv_kind<DT, true, true>(a, s) : gemv_kind<DT, true, false>(a, s);
 }
+
+template <int DT>
+int launch_split_merge(const float* part, int S, int64_t M, int64_t N, const void* bias, int bias_dt,
+                       void* y, int64_t ldy, hipStream_t s) {
+  using St = typename Act<DT>::storage;
+  const int64_t outs = M * N;
+  gemv_merge_kernel<DT><<<dim3(static_cast<unsigned>((outs + 255) / 256)), dim3(256), 0, s>>>(
+      part, S, static_cast<int>(M), static_cast<int>(N), bias, bias_dt, static_cast<St*>(y), ldy);
+  return static_cast<int>(hipGetLastError());
+}
+template int launch_split_merge<LSQ_BF16>(const float*, int, int64_t, int64_t, const void*, int, void*, int64_t, hipStream_t);
+template int launch_split_merge<LSQ_F16>(const float*, int, int64_t, int64_t, const void*, int, void*, int64_t, hipStream_t);
 
 int64_t gemv_split_bytes(int64_t M, int64_t N, int64_t K) {
   if (!gemv_enabled()) return 0;

@@ -15,6 +15,8 @@
 //  * generic kernel (below): any dtype / shape / group size, exact per-element dequant and
 //    fp32 FMA. Used for fp32 activations and shapes the fast kernels do not cover.
 
+#include <algorithm>
+
 #include "lsq_common.h"
 #include "lsq_internal.h"
 #include "lsq_gemm.h"
@@ -312,7 +314,7 @@ extern "C" int lsq_w4_linear_ws(const void* x, int64_t ldx, const uint8_t* weigh
 
 extern "C" int64_t lsq_linear_workspace_bytes(int64_t M, int64_t N, int64_t K) {
   if (M < 0 || N < 0 || K < 0) return 0;
-  const int64_t b = gemv_split_bytes(M, N, K);
+  const int64_t b = std::max(gemv_split_bytes(M, N, K), bgemv_split_bytes(M, N, K));
   return (b + 255) / 256 * 256;
 }
 

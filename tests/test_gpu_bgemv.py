@@ -160,3 +160,39 @@ def test_bgemv_default_dispatch_qwen05b(m, monkeypatch):
     for kind in ("int4", "int8"):
         for n, k in ((896, 4864), (9728, 896), (896, 896)):
             _check(kind, n, k, m, seed=3 * n + k + m)
+
+
+# ---- split-K form (at most 128 row tiles, 16+ k tiles, with the module's workspace):
+# one row tile per workgroup times S K slices, the slices added in order by a merge kernel.
+
+@pytest.mark.parametrize("m", [17, 32, 33, 64])
+@pytest.mark.parametrize("kind", ["int4", "int8"])
+def test_bgemv_split_k_down_proj(kind, m, monkeypatch):
+    """Qwen2.5-0.5B down_proj 896 x 4864 (56 row tiles, 38 k tiles: 4 slices by default),
+    bias on odd M; the split is the default here, so LSQ_BGEMV is left unset."""
+    monkeypatch.delenv("LSQ_BGEMV", raising=False)
+    _check(kind, 896, 4864, m, bias=(m % 2 == 1), seed=m)
+
+
+@pytest.mark.parametrize("splits", ["2", "5", "16"])
+def test_bgemv_split_k_forced(splits, monkeypatch):
+    """Forced slice counts on 2000 x 8192 (125 row tiles, the last partial; 64 k tiles),
+    INT4 group-wise and per-channel, INT8, fp16 activations."""
+    monkeypatch.setenv("LSQ_SPLITK", splits)
+    _check("int4", 2000, 8192, 40, bias=True, seed=int(splits))
+    _check("int4", 2000, 8192, 24, group=8192, seed=int(splits) + 1)
+    _check("int8", 2000, 8192, 64, bias=True, seed=int(splits) + 2)
+    _check("int4", 2000, 8192, 48, dtype=torch.float16, group=256, seed=int(splits) + 3)
+
+
+def test_bgemv_split_k_deterministic_and_matches_unsplit(monkeypatch):
+    monkeypatch.delenv("LSQ_BGEMV", raising=False)
+    ql, xd, y1 = _check("int4", 896, 4864, 32, seed=41)
+    with torch.no_grad():
+        y2 = ql(xd).float().cpu().numpy()
+        monkeypatch.setenv("LSQ_SPLITK", "0")
+        y0 = ql(xd).float().cpu().numpy()
+    assert np.array_equal(y1.view(np.uint32), y2.view(np.uint32))
+    err = qo.rel_err(y1, y0.astype(np.float64))
+    _say(f"  split vs unsplit: rel={err:.3e}")
+    assert err <= REL_TOL
