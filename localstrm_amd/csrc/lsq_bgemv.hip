@@ -69,7 +69,7 @@ __host__ __device__ inline int64_t bgemv_lds(int mt, int rm, int64_t ngs) {
 }
 static_assert(kBgRows * 4 * 64 * 4 <= kBgDepth * 16 * 256, "the partial sums must fit the activation slabs");
 
-template <int DT, bool W4, bool GROUPED, int MT, int RM>
+template <int DT, bool W4, bool GROUPED, int MT, int RM, bool SPLIT>
 __global__ void __launch_bounds__(64 * kBgWaves) bgemv_kernel(LinearArgs p) {
   constexpr int P = kBgPhases, D = kBgDepth;
   constexpr int kTileB = W4 ? kTileBytes : kTileBytes8;
@@ -83,7 +83,7 @@ __global__ void __launch_bounds__(64 * kBgWaves) bgemv_kernel(LinearArgs p) {
   const int M = static_cast<int>(p.M), N = static_cast<int>(p.N), K = static_cast<int>(p.K);
   // K slices (split-K: workgroup b takes slice b % NS of row-tile range b / NS; NS = 1
   // otherwise); `nkt` counts this slice's k tiles, from k tile `kt_s0` of `nkt_all`.
-  const int NS = p.ksplit;
+  const int NS = SPLIT ? p.ksplit : 1;  // (a constant 1 in the unsplit instances)
   const int nkt_all = K / kTileK;
   const int sl = NS > 1 ? static_cast<int>(blockIdx.x) % NS : 0;
   const int kt_s0 = sl * nkt_all / NS;
@@ -339,9 +339,9 @@ int bgemv_max_lds() {
   return v;
 }
 
-template <int DT, bool W4, bool GROUPED, int MT, int RM>
+template <int DT, bool W4, bool GROUPED, int MT, int RM, bool SPLIT>
 int bgemv_one(const LinearArgs& a, int grid, hipStream_t s) {
-  auto kern = bgemv_kernel<DT, W4, GROUPED, MT, RM>;
+  auto kern = bgemv_kernel<DT, W4, GROUPED, MT, RM, SPLIT>;
   const int64_t lds = bgemv_lds(MT, RM, GROUPED ? a.ngroups : 1);
   if (lds > bgemv_max_lds()) return LSQ_E_LAYOUT;
   if (lds > 64 * 1024) {
@@ -353,14 +353,15 @@ int bgemv_one(const LinearArgs& a, int grid, hipStream_t s) {
       attr_set.store(1, std::memory_order_release);
     }
   }
-  bgemv_kernel<DT, W4, GROUPED, MT, RM><<<dim3(static_cast<unsigned>(grid)), dim3(64 * kBgWaves), static_cast<size_t>(lds), s>>>(a);
+  bgemv_kernel<DT, W4, GROUPED, MT, RM, SPLIT><<<dim3(static_cast<unsigned>(grid)), dim3(64 * kBgWaves), static_cast<size_t>(lds), s>>>(a);
   return static_cast<int>(hipGetLastError());
 }
 
-template <int DT, bool W4, bool GROUPED, int RM>
+template <int DT, bool W4, bool GROUPED, int RM, bool SPLIT = false>
 int bgemv_kind(const LinearArgs& a, int grid, hipStream_t s) {
   // token blocks per wave: two halves of 1 (up to 32 tokens) or 2 (up to 64) blocks
-  return a.M <= 32 ? bgemv_one<DT, W4, GROUPED, 1, RM>(a, grid, s) : bgemv_one<DT, W4, GROUPED, 2, RM>(a, grid, s);
+  return a.M <= 32 ? bgemv_one<DT, W4, GROUPED, 1, RM, SPLIT>(a, grid, s)
+                   : bgemv_one<DT, W4, GROUPED, 2, RM, SPLIT>(a, grid, s);
 }
 
 // Split-K plan for small-N layers with many k tiles (at most 128 row tiles, 16+ k tiles:
@@ -426,8 +427,9 @@ int launch_bgemv(int kind, const LinearArgs& a, hipStream_t s) {
     LinearArgs as = a;
     as.ksplit = static_cast<int>(sp.S);
     const int grid = static_cast<int>(nrt * sp.S);
-    const int rc = !w4 ? bgemv_kind<DT, false, false, 1>(as, grid, s)
-                       : (grouped ? bgemv_kind<DT, true, true, 1>(as, grid, s) : bgemv_kind<DT, true, false, 1>(as, grid, s));
+    const int rc = !w4 ? bgemv_kind<DT, false, false, 1, true>(as, grid, s)
+                       : (grouped ? bgemv_kind<DT, true, true, 1, true>(as, grid, s)
+                                  : bgemv_kind<DT, true, false, 1, true>(as, grid, s));
     if (rc != LSQ_OK) return rc;
     return launch_split_merge<DT>(a.part, static_cast<int>(sp.S), a.M, a.N, a.bias, a.bias_dt, a.y, a.ldy, s);
   }

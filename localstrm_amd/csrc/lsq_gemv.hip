@@ -104,7 +104,7 @@ __device__ __forceinline__ int run_lo(int w, int T, int W) {
   return w * T / W;  // T <= 16 row tiles x 2^14 k tiles: no overflow
 }
 
-template <int DT, bool W4, bool GROUPED, int MT, int W, int D>
+template <int DT, bool W4, bool GROUPED, int MT, int W, int D, bool SPLIT>
 __global__ void __launch_bounds__(64 * W) gemv_kernel(LinearArgs p) {
   constexpr int NT = 64 * W;
   constexpr int kTileB = W4 ? kTileBytes : kTileBytes8;
@@ -118,7 +118,7 @@ __global__ void __launch_bounds__(64 * W) gemv_kernel(LinearArgs p) {
   // K slices (split-K: workgroup b takes slice b % NS of row-tile range b / NS; NS = 1
   // otherwise). `nkt` counts the k tiles of this workgroup's slice, which start at k tile
   // `kt_s0` of the layer's `nkt_all`.
-  const int NS = p.ksplit;
+  const int NS = SPLIT ? p.ksplit : 1;  // (a constant 1 in the unsplit instances)
   const int nkt_all = static_cast<int>(p.K / kTileK);
   const int sl = NS > 1 ? static_cast<int>(blockIdx.x) % NS : 0;
   const int kt_s0 = sl * nkt_all / NS;
@@ -533,7 +533,7 @@ int gemv_max_lds() {
   return v;
 }
 
-template <int DT, bool W4, bool GROUPED, int MT, int W, int D>
+template <int DT, bool W4, bool GROUPED, int MT, int W, int D, bool SPLIT>
 int gemv_one(const LinearArgs& a, int grid, hipStream_t s) {
   // grid = row-tile ranges x a.ksplit K slices
   const int S = a.ksplit;
@@ -551,7 +551,7 @@ int gemv_one(const LinearArgs& a, int grid, hipStream_t s) {
                              gemv_lds_groups(ngs, S, static_cast<int>(kst_max), static_cast<int>(a.group / kTileK), GROUPED),
                              W, NE);
   if (L.total > gemv_max_lds()) return LSQ_E_LAYOUT;
-  auto kern = gemv_kernel<DT, W4, GROUPED, MT, W, D>;
+  auto kern = gemv_kernel<DT, W4, GROUPED, MT, W, D, SPLIT>;
   if (L.total > 64 * 1024) {
     static std::atomic<int> attr_set{0};
     if (!attr_set.load(std::memory_order_acquire)) {
@@ -565,25 +565,27 @@ int gemv_one(const LinearArgs& a, int grid, hipStream_t s) {
   return static_cast<int>(hipGetLastError());
 }
 
-template <int DT, bool W4, bool GROUPED, int MT>
+template <int DT, bool W4, bool GROUPED, int MT, bool SPLIT>
 int gemv_mt(const LinearArgs& a, const GemvCfg& c, int grid, hipStream_t s) {
 #define LSQ_GEMV_TRY(W_, D_) \
-  if (c.w == W_ && c.d == D_) return gemv_one<DT, W4, GROUPED, MT, W_, D_>(a, grid, s);
+  if (c.w == W_ && c.d == D_) return gemv_one<DT, W4, GROUPED, MT, W_, D_, SPLIT>(a, grid, s);
   LSQ_GEMV_TRY(16, 3)
-  LSQ_GEMV_TRY(16, 2)
   LSQ_GEMV_TRY(8, 3)
-  LSQ_GEMV_TRY(8, 2)
   LSQ_GEMV_TRY(4, 3)
-  LSQ_GEMV_TRY(4, 2)
+  if constexpr (!SPLIT) {  // (the split launcher uses ring depth 3 only)
+    LSQ_GEMV_TRY(16, 2)
+    LSQ_GEMV_TRY(8, 2)
+    LSQ_GEMV_TRY(4, 2)
+  }
 #undef LSQ_GEMV_TRY
   return LSQ_E_LAYOUT;
 }
 
-template <int DT, bool W4, bool GROUPED>
+template <int DT, bool W4, bool GROUPED, bool SPLIT>
 int gemv_grid(const LinearArgs& a, const GemvCfg& c, int grid, hipStream_t s) {
-  if (a.M == 1) return gemv_mt<DT, W4, GROUPED, 1>(a, c, grid, s);
-  if (a.M <= 4) return gemv_mt<DT, W4, GROUPED, 4>(a, c, grid, s);
-  return gemv_mt<DT, W4, GROUPED, 16>(a, c, grid, s);
+  if (a.M == 1) return gemv_mt<DT, W4, GROUPED, 1, SPLIT>(a, c, grid, s);
+  if (a.M <= 4) return gemv_mt<DT, W4, GROUPED, 4, SPLIT>(a, c, grid, s);
+  return gemv_mt<DT, W4, GROUPED, 16, SPLIT>(a, c, grid, s);
 }
 
 // y[m, n] = round_T(sum over slices s = 0.. S-1, in that order, of part[s][m][n] +
@@ -615,7 +617,7 @@ int gemv_kind(const LinearArgs& a, hipStream_t s) {
     const int64_t rpw = c.rpw;
     const int64_t grid = (nrt + rpw - 1) / rpw;
     if (grid < 1 || grid > 65535) return LSQ_E_LAYOUT;
-    return gemv_grid<DT, W4, GROUPED>(a, c, static_cast<int>(grid), s);
+    return gemv_grid<DT, W4, GROUPED, false>(a, c, static_cast<int>(grid), s);
   }
   // Fewer than 1024 row tiles: the split-K form when it applies and a workspace is given.
   const GemvSplit sp = gemv_split_plan(a.M, a.N, a.K);
@@ -624,7 +626,7 @@ int gemv_kind(const LinearArgs& a, hipStream_t s) {
   const GemvCfg cs{1, units >= 16 ? 16 : (units >= 8 ? 8 : 4), 3};
   LinearArgs as = a;
   as.ksplit = sp.S;
-  const int rc = gemv_grid<DT, W4, GROUPED>(as, cs, static_cast<int>(sp.ranges * sp.S), s);
+  const int rc = gemv_grid<DT, W4, GROUPED, true>(as, cs, static_cast<int>(sp.ranges * sp.S), s);
   if (rc != LSQ_OK) return rc;
   return launch_split_merge<DT>(a.part, static_cast<int>(sp.S), a.M, a.N, a.bias, a.bias_dt, a.y, a.ldy, s);
 }
