@@ -434,8 +434,23 @@ __global__ void __launch_bounds__(RNT_, MINB) gemm_rw_kernel(LinearArgs p) {
   const int ng = static_cast<int>(p.ngroups);
   const int group = static_cast<int>(p.group);
   const int mtiles = (M + RBM - 1) / RBM;
-  const int mt = blockIdx.x % mtiles;  // M fastest: consecutive workgroups share W tiles
-  const int nt = blockIdx.x / mtiles;
+  // Tile of this workgroup. Workgroups are dealt to the 8 XCDs round-robin (XCD b % 8),
+  // each XCD with its own L2. 128-row tiles: M fastest, so consecutive workgroups share
+  // W tiles. 256-row tiles: the tiles are ordered in groups of 4 M tiles (M fastest
+  // inside a group, then N, then the next group) and XCD x takes the x-th eighth of that
+  // order, so the ~32 workgroups resident on an XCD form a 4 x 8 block of tiles and, all
+  // walking K in step, share each activation tile 8 ways and each weight tile 4 ways in
+  // that XCD's L2 (when the grid does not divide so, M fastest as for 128-row tiles).
+  int mt = blockIdx.x % mtiles;
+  int nt = blockIdx.x / mtiles;
+  const int ntiles = (N + RBN - 1) / RBN;
+  const bool blocked = RFM == 8 && mtiles % 4 == 0 && (mtiles * ntiles) % 8 == 0;
+  if (blocked) {
+    const int L = (blockIdx.x & 7) * (mtiles * ntiles / 8) + (blockIdx.x >> 3);
+    const int r = L % (4 * ntiles);
+    mt = 4 * (L / (4 * ntiles)) + (r & 3);
+    nt = r >> 2;
+  }
   const int m0 = mt * RBM, n0 = nt * RBN;
   const int rows_m = min(RBM, M - m0);
   const int rows_n = min(RBN, N - n0);
@@ -448,9 +463,17 @@ __global__ void __launch_bounds__(RNT_, MINB) gemm_rw_kernel(LinearArgs p) {
   asm volatile("v_mov_b32 %0, 0x000f000f" : "=v"(nib_mask));
   asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(nib_magic));
 
-  // K rotation per workgroup (see gemm_kernel): spreads first-touch misses over K.
-  const int rot = (((blockIdx.x >> 3) & 31) * nsteps) >> 5;
+  // K rotation per workgroup (see gemm_kernel): spreads first-touch misses over K; none
+  // for the blocked 256-row tiles, whose workgroups share tiles by walking K in step
+  // (14336 x 4096 M=8192: 891 -> 792 us without it).
+  const int rot = blocked ? 0 : (((blockIdx.x >> 3) & 31) * nsteps) >> 5;
   auto gstep = [&](int st) { const int g = st + rot; return g >= nsteps ? g - nsteps : g; };
+  // scale group of K step gs (group % 64 == 0): a shift for power-of-two groups, else a
+  // division (uniform; the scalar unit is shared by the CU's waves)
+  const int spg = group / BK;
+  const int spg_sh = __builtin_ctz(static_cast<uint32_t>(spg));
+  const bool spg_pow2 = (spg & (spg - 1)) == 0;
+  auto group_of = [&](int gs) { return spg_pow2 ? gs >> spg_sh : gs / spg; };
 
   // ---- descriptors
   const rsrc_t rx = make_rsrc(static_cast<const uint16_t*>(p.x) + static_cast<int64_t>(m0) * p.ldx,
@@ -519,7 +542,7 @@ __global__ void __launch_bounds__(RNT_, MINB) gemm_rw_kernel(LinearArgs p) {
       for (int l = 0; l < WLB; ++l)
         r.w[j][l] = bload16<kNT>(rw, real ? woff[j] + kw + l * (TILED ? kTileBytes8 / 2 : 16) : kOOB);
     if (GROUPED) {
-      const int g = (gs * BK) / group;
+      const int g = group_of(gs);
 #pragma unroll
       for (int j = 0; j < RFN; ++j)
         r.s[j] = bload4(rs, static_cast<uint32_t>((lr[j] * ng + g) * es_s) & ~3u);
@@ -558,7 +581,7 @@ __global__ void __launch_bounds__(RNT_, MINB) gemm_rw_kernel(LinearArgs p) {
     for (int j = 0; j < RFN; ++j) {
       sf[j] = 1.f;
       if (GROUPED) {
-        const int g = (gstep(min(st, nsteps - 1)) * BK) / group;
+        const int g = group_of(gstep(min(st, nsteps - 1)));
         const uint32_t eb = static_cast<uint32_t>((lr[j] * ng + g) * es_s);
         sf[j] = Act<DT>::round(dword_elem(cur.s[j], (eb >> 1) & 1, p.scale_dt));
       }
