@@ -94,9 +94,10 @@ __device__ __forceinline__ float row16_add(float v) {
 constexpr int kGemvSB = 4;  // scale dwords in flight per thread while staging
 
 // Activation chunks (16 B) each thread loads per staging batch: enough for MT tokens at
-// K = 4096 in one batch, at most 4 (registers).
+// K = 4096 in one batch, at most 4 (8 for 16 tokens, so that 16 tokens at K = 3584, 115
+// KB, stage in one batch of 16 waves and the weight ring is issued alongside).
 __host__ __device__ constexpr int gemv_xb(int mt, int nt) {
-  return mt * 512 / nt < 1 ? 1 : (mt * 512 / nt > 4 ? 4 : mt * 512 / nt);
+  return mt * 512 / nt < 1 ? 1 : (mt * 512 / nt > (mt == 16 ? 8 : 4) ? (mt == 16 ? 8 : 4) : mt * 512 / nt);
 }
 
 // Units of the wave run [t_lo, t_hi) of wave `w` among W over T units.
@@ -504,7 +505,7 @@ GemvSplit gemv_split_plan(int64_t M, int64_t N, int64_t K) {
   const int64_t forced = e ? std::atoi(e) : 0;  // LSQ_SPLITK=n >= 2: n slices (sweeps)
   if (forced < 2 && (nrt > 512 || M * K * 2 <= 96 * 1024)) return sp;
   const int64_t rmin_ranges = (nrt + 15) / 16;
-  const int64_t batch = int64_t(16) * 1024 * gemv_xb(M == 1 ? 1 : (M <= 4 ? 4 : 16), 1024);
+  const int64_t batch = int64_t(16) * 1024 * std::min(4, gemv_xb(M == 1 ? 1 : (M <= 4 ? 4 : 16), 1024));
   int64_t S = (M * K * 2 + batch - 1) / batch;
   if (S < 1) S = 1;
   for (; S <= nkt / 4; ++S) {
