@@ -6,6 +6,10 @@
 // weight tiles it needs straight into LDS and feeds bf16 / fp16 MFMA from there; the
 // dequantized weight never exists in HBM.
 //
+// Two kernels. gemm_rw_kernel (register weights; the default, 128 x 128 tiles up to 768
+// tokens and 256 x 256 above) is described at its definition below. gemm_kernel (LDS
+// weights, LSQ_GEMM=lds) follows.
+//
 // Tiling. A workgroup computes a 256 x 256 tile of y with 8 waves in a 2 x 4 layout (two
 // waves per SIMD, so one issues MFMAs while the other waits); each wave owns 128 x 64
 // outputs as 4 x 2 blocks of v_mfma_f32_32x32x16_{bf16,f16} (fp32 accumulators, 128
