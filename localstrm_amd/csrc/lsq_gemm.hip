@@ -3,8 +3,8 @@
 // GPU form of QuantizedLinear.forward (src/kernels/quantization.py:129-141) for prefill:
 // y[M, N] = x[M, K] @ dequant(W)^T + bias, where the reference materializes the whole
 // dequantized weight in HBM and calls F.linear. Here each workgroup dequantizes the
-// weight tiles it needs straight into LDS and feeds bf16 / fp16 MFMA from there; the
-// dequantized weight never exists in HBM.
+// weight tiles it needs on chip (into MFMA operand registers, or into LDS) and feeds
+// bf16 / fp16 MFMA from there; the dequantized weight never exists in HBM.
 //
 // Two kernels. gemm_rw_kernel (register weights; the default, 128 x 128 tiles up to 768
 // tokens and 256 x 256 above) is described at its definition below. gemm_kernel (LDS
