@@ -224,13 +224,17 @@ def bench_floors(nbytes: int, steps: int, warmup: int, device) -> dict:
     }
 
 
-def bench_decode(kind: str, n: int, k: int, m: int, steps: int, warmup: int, device, group=128):
+def bench_decode(kind: str, n: int, k: int, m: int, steps: int, warmup: int, device, group=128,
+                 copies=None):
+    """One layer shape timed over `steps` back-to-back launches; by default the launches
+    rotate over enough weight copies to exceed the 256 MB Infinity Cache (every launch reads
+    HBM); copies=1 times the hot-cache case (one copy, resident in the Infinity Cache)."""
     if kind in ("int8", "w8a8"):
         w, s, x = make_int8(n, k, m)
     else:
         w, s, x = make_int4(n, k, m, group)
     wbytes = w.numel()
-    copies = copies_for(wbytes)
+    copies = copies or copies_for(wbytes)
     layers = _layers(kind, w, s, group, copies, device)
     ms, lo, hi = time_layers(layers, x.to(device), steps, warmup)
     nbytes = decode_bytes(kind, n, k, m, group)
@@ -502,6 +506,7 @@ def main() -> int:
 
     N, K, M, G = 18944, 3584, 1, 128
     head = bench_decode("int4", N, K, M, args.steps, args.warmup, device, group=G)
+    hot = bench_decode("int4", N, K, M, args.steps, args.warmup, device, group=G, copies=1)
     floors = bench_floors(decode_bytes("int4", N, K, M, G), args.steps, args.warmup, device)
     sweep = []
     if not args.no_sweep:
@@ -557,6 +562,11 @@ def main() -> int:
             "unit": "GB/s", "frac": round(head["frac_hbm"], 4), "traffic": measured_traffic(),
         },
         "floors": dict(floors, kernel_vs_bare_read=head["us_per_call"] / floors["bare_read_us"]),
+        "hot_cache": {
+            "what": ("the headline with one weight copy resident in the 256 MB Infinity Cache "
+                     "(not HBM-bound; value above rotates copies so every launch reads HBM)"),
+            "us_per_call": hot["us_per_call"], "GB_s": round(hot["GB_s"], 2),
+        },
         "cpu_baseline": cpu,
         "cpu_baselines_more": cpu_more,
         "sweep": sweep,
