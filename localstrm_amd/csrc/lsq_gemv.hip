@@ -513,7 +513,7 @@ GemvSplit gemv_split_plan(int64_t M, int64_t N, int64_t K) {
     if (ranges * S >= 192) break;
   }
   if (forced >= 2) S = forced;
-  if (S < 2 || S > nkt / 4) return sp;
+  if (S < 2 || S > nkt / 4 || S > 16) return sp;  // (the merge adds at most 16 slices)
   sp.S = S;
   sp.ranges = std::min(nrt, std::max(rmin_ranges, int64_t(256) / S));
   sp.bytes = S * M * N * 4;
@@ -590,23 +590,45 @@ int gemv_grid(const LinearArgs& a, const GemvCfg& c, int grid, hipStream_t s) {
 }
 
 // y[m, n] = round_T(sum over slices s = 0.. S-1, in that order, of part[s][m][n] +
-// round_T(bias[n])): the merge of the split-K GEMV.
-template <int DT>
+// round_T(bias[n])): the merge of the split-K GEMV. Each thread takes 4 consecutive
+// outputs (16-byte loads; N % 4 == 0, else one output per thread) and issues every slice's
+// load before the first add, so the kernel costs about one memory round trip.
+template <int DT, int V>
 __global__ void __launch_bounds__(256) gemv_merge_kernel(const float* __restrict__ part, int S, int M, int N,
                                                          const void* bias, int bias_dt,
                                                          typename Act<DT>::storage* __restrict__ y, int64_t ldy) {
-  const int i = blockIdx.x * 256 + threadIdx.x;
-  if (i >= M * N) return;
-  const int m = i / N, n = i - m * N;
-  float v = part[i];
-  for (int sl = 1; sl < S; ++sl) v += part[static_cast<int64_t>(sl) * M * N + i];
-  if (bias) {
-    const uint16_t* b16 = static_cast<const uint16_t*>(bias);
-    const float bv = bias_dt == LSQ_F32 ? static_cast<const float*>(bias)[n]
-                                        : (bias_dt == LSQ_BF16 ? bf16_to_f32(b16[n]) : f16_to_f32(b16[n]));
-    v = opaque(v + Act<DT>::round(bv));
+  constexpr int kMaxS = 16;
+  const int64_t MN = int64_t(M) * N;
+  const int64_t i = (int64_t(blockIdx.x) * 256 + threadIdx.x) * V;  // first output
+  if (i >= MN) return;
+  const int m = static_cast<int>(i / N), n = static_cast<int>(i - int64_t(m) * N);
+  float v[kMaxS][V];
+#pragma unroll
+  for (int sl = 0; sl < kMaxS; ++sl) {
+    if (sl < S) {
+      if constexpr (V == 4) {
+        const float4 t = *reinterpret_cast<const float4*>(part + sl * MN + i);
+        v[sl][0] = t.x; v[sl][1] = t.y; v[sl][2] = t.z; v[sl][3] = t.w;
+      } else {
+        v[sl][0] = part[sl * MN + i];
+      }
+    }
   }
-  y[static_cast<int64_t>(m) * ldy + n] = Act<DT>::from_f32(v);
+  const uint16_t* b16 = static_cast<const uint16_t*>(bias);
+#pragma unroll
+  for (int e = 0; e < V; ++e) {
+    float acc = v[0][e];
+#pragma unroll
+    for (int sl = 1; sl < kMaxS; ++sl)
+      if (sl < S) acc += v[sl][e];
+    if (bias) {
+      const int nn = n + e;
+      const float bv = bias_dt == LSQ_F32 ? static_cast<const float*>(bias)[nn]
+                                          : (bias_dt == LSQ_BF16 ? bf16_to_f32(b16[nn]) : f16_to_f32(b16[nn]));
+      acc = opaque(acc + Act<DT>::round(bv));
+    }
+    y[static_cast<int64_t>(m) * ldy + n + e] = Act<DT>::from_f32(acc);
+  }
 }
 
 template <int DT, bool W4, bool GROUPED>
@@ -655,9 +677,15 @@ template <int DT>
 int launch_split_merge(const float* part, int S, int64_t M, int64_t N, const void* bias, int bias_dt,
                        void* y, int64_t ldy, hipStream_t s) {
   using St = typename Act<DT>::storage;
+  if (S < 1 || S > 16) return LSQ_E_SHAPE;
   const int64_t outs = M * N;
-  gemv_merge_kernel<DT><<<dim3(static_cast<unsigned>((outs + 255) / 256)), dim3(256), 0, s>>>(
-      part, S, static_cast<int>(M), static_cast<int>(N), bias, bias_dt, static_cast<St*>(y), ldy);
+  if (N % 4 == 0 && (reinterpret_cast<uintptr_t>(part) & 15) == 0) {
+    gemv_merge_kernel<DT, 4><<<dim3(static_cast<unsigned>((outs / 4 + 255) / 256)), dim3(256), 0, s>>>(
+        part, S, static_cast<int>(M), static_cast<int>(N), bias, bias_dt, static_cast<St*>(y), ldy);
+  } else {
+    gemv_merge_kernel<DT, 1><<<dim3(static_cast<unsigned>((outs + 255) / 256)), dim3(256), 0, s>>>(
+        part, S, static_cast<int>(M), static_cast<int>(N), bias, bias_dt, static_cast<St*>(y), ldy);
+  }
   return static_cast<int>(hipGetLastError());
 }
 template int launch_split_merge<LSQ_BF16>(const float*, int, int64_t, int64_t, const void*, int, void*, int64_t, hipStream_t);
