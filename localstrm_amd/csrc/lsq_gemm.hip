@@ -418,7 +418,8 @@ __global__ void __launch_bounds__(NT) gemm_kernel(LinearArgs p) {
 // K order inside a step: lane l at 16-column sub-step kk multiplies columns
 // 32 (l >> 5) + 8 kk .. +7 (the same permutation on both operands), which makes each
 // lane's weights one contiguous 32-column chunk per step.
-__host__ __device__ constexpr int rw_lds_bytes(int rbm) { return 2 * rbm * BK * 2; }
+// activation stages: three for 256-row tiles (96 KB), two for 128-row tiles (32 KB)
+__host__ __device__ constexpr int rw_lds_bytes(int rbm) { return (rbm == 256 ? 3 : 2) * rbm * BK * 2; }
 
 // RFN_ 32-column blocks per wave, RFM_ 32-row blocks, RNT_ threads, MINB workgroups per CU.
 template <int DT, int KIND, bool GROUPED, int RFN_, int RFM_, int RNT_, int MINB>
@@ -501,8 +502,9 @@ __global__ void __launch_bounds__(RNT_, MINB) gemm_rw_kernel(LinearArgs p) {
   const rsrc_t rs = make_rsrc(static_cast<const uint8_t*>(p.scale) + static_cast<int64_t>(n0) * ngs * es_s,
                               static_cast<uint32_t>((rows_n * ngs * es_s + 3) & ~3));
 
-  // ---- activations: two LDS stages of 128 rows x 64 columns, chunk c of row r at
-  // position c ^ ((r >> 1) & 7); DMA as in gemm_kernel (4 x 1 KB per wave per step).
+  // ---- activations: LDS stages (two, or three for 256-row tiles) of RBM rows x 64
+  // columns, chunk c of row r at position c ^ ((r >> 1) & 7); DMA as in gemm_kernel
+  // (4 x 1 KB per wave per step).
   constexpr int kStage = RBM * BK * 2;
   constexpr int kXB = RBM / 8 / (RNT / 64);  // 4 row blocks of 8 per wave
   uint32_t x_lane_off[kXB];  // row in the range-checked per-lane offset, as in gemm_kernel
@@ -576,9 +578,13 @@ __global__ void __launch_bounds__(RNT_, MINB) gemm_rw_kernel(LinearArgs p) {
     for (int i = 0; i < RFM; ++i) aa[i] = *reinterpret_cast<const u32x4*>(xb + 32 * i * (BK * 2) + off);
   };
   auto step = [&](int st, const WSet& cur, WSet& nxt2) {
-    const int buf = st & 1;
-    // stage buf ^ 1 was last read before the previous step's barrier
-    issue_x(st + 1, buf ^ 1);
+    // 256-row tiles: three stages, the DMA two steps ahead (the stage it fills was last
+    // read before the previous step's barrier); 128-row tiles: two stages, one step ahead
+    const int buf = RFM == 8 ? st % 3 : st & 1;
+    if (RFM == 8)
+      issue_x(st + 2, (st + 2) % 3);
+    else
+      issue_x(st + 1, buf ^ 1);
     issue_w(st + 2, nxt2);
     float sf[RFN], cf[RFN];
 #pragma unroll
@@ -607,13 +613,16 @@ __global__ void __launch_bounds__(RNT_, MINB) gemm_rw_kernel(LinearArgs p) {
         load_a(buf, kk + 1, a[(kk + 1) & 1]);
         dequant(kk + 1, b[(kk + 1) & 1]);
       } else {
-        // The next step's activation DMA must have landed (the weight loads issued after
-        // it, for two steps ahead, stay in flight); the barrier also orders every wave's
-        // reads of this stage before the next step's DMA into it.
-        constexpr int kAfter = RFN * WLB + (GROUPED ? RFN : 0);
+        // The next step's activation DMA must have landed (the loads issued after it stay
+        // in flight: the weights for two steps ahead, and with three stages the DMA and
+        // weights issued in this step; in step 0 the count also waits for step 0's weights,
+        // issued after step 1's DMA in the prologue, which is merely conservative); the
+        // barrier also orders every wave's reads of this stage before a later DMA into it.
+        constexpr int kW = RFN * WLB + (GROUPED ? RFN : 0);
+        constexpr int kAfter = RFM == 8 ? 2 * kW + kXB : kW;
         __builtin_amdgcn_s_waitcnt((kAfter & 15) | (7 << 4) | ((kAfter >> 4) << 14));
         lds_barrier();
-        load_a(buf ^ 1, 0, a[0]);
+        load_a(RFM == 8 ? (st + 1) % 3 : buf ^ 1, 0, a[0]);
       }
 #pragma unroll
       for (int i = 0; i < RFM; ++i)
@@ -640,6 +649,7 @@ __global__ void __launch_bounds__(RNT_, MINB) gemm_rw_kernel(LinearArgs p) {
 
   WSet r0, r1, r2;
   issue_x(0, 0);
+  if (RFM == 8) issue_x(1, 1);
   issue_w(0, r0);
   issue_w(1, r1);
   {
@@ -693,8 +703,17 @@ template <int DT, int KIND, bool GROUPED, int RFN, int RFM, int RNT, int MINB>
 int launch_rw_shape(const LinearArgs& a, hipStream_t s) {
   constexpr int rbm = 32 * RFM, rbn = (RNT / 64) * 32 * RFN;
   const int64_t tiles = ((a.M + rbm - 1) / rbm) * ((a.N + rbn - 1) / rbn);
-  gemm_rw_kernel<DT, KIND, GROUPED, RFN, RFM, RNT, MINB>
-      <<<dim3(static_cast<unsigned>(tiles)), dim3(RNT), rw_lds_bytes(rbm), s>>>(a);
+  auto kern = gemm_rw_kernel<DT, KIND, GROUPED, RFN, RFM, RNT, MINB>;
+  if (rw_lds_bytes(rbm) > 64 * 1024) {
+    static std::atomic<int> attr_set{0};
+    if (!attr_set.load(std::memory_order_acquire)) {
+      const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, rw_lds_bytes(rbm));
+      if (e != hipSuccess) return static_cast<int>(e);
+      attr_set.store(1, std::memory_order_release);
+    }
+  }
+  kern<<<dim3(static_cast<unsigned>(tiles)), dim3(RNT), rw_lds_bytes(rbm), s>>>(a);
   return static_cast<int>(hipGetLastError());
 }
 
