@@ -418,8 +418,8 @@ __global__ void __launch_bounds__(NT) gemm_kernel(LinearArgs p) {
 // K order inside a step: lane l at 16-column sub-step kk multiplies columns
 // 32 (l >> 5) + 8 kk .. +7 (the same permutation on both operands), which makes each
 // lane's weights one contiguous 32-column chunk per step.
-// activation stages: three for 256-row tiles (96 KB), two for 128-row tiles (32 KB)
-__host__ __device__ constexpr int rw_lds_bytes(int rbm) { return (rbm == 256 ? 3 : 2) * rbm * BK * 2; }
+// three activation stages: 96 KB for 256-row tiles, 48 KB for 128-row tiles
+__host__ __device__ constexpr int rw_lds_bytes(int rbm) { return 3 * rbm * BK * 2; }
 
 // RFN_ 32-column blocks per wave, RFM_ 32-row blocks, RNT_ threads, MINB workgroups per CU.
 template <int DT, int KIND, bool GROUPED, int RFN_, int RFM_, int RNT_, int MINB>
@@ -502,9 +502,8 @@ __global__ void __launch_bounds__(RNT_, MINB) gemm_rw_kernel(LinearArgs p) {
   const rsrc_t rs = make_rsrc(static_cast<const uint8_t*>(p.scale) + static_cast<int64_t>(n0) * ngs * es_s,
                               static_cast<uint32_t>((rows_n * ngs * es_s + 3) & ~3));
 
-  // ---- activations: LDS stages (two, or three for 256-row tiles) of RBM rows x 64
-  // columns, chunk c of row r at position c ^ ((r >> 1) & 7); DMA as in gemm_kernel
-  // (4 x 1 KB per wave per step).
+  // ---- activations: three LDS stages of RBM rows x 64 columns, chunk c of row r at
+  // position c ^ ((r >> 1) & 7); DMA as in gemm_kernel (4 x 1 KB per wave per step).
   constexpr int kStage = RBM * BK * 2;
   constexpr int kXB = RBM / 8 / (RNT / 64);  // 4 row blocks of 8 per wave
   uint32_t x_lane_off[kXB];  // row in the range-checked per-lane offset, as in gemm_kernel
@@ -578,13 +577,10 @@ __global__ void __launch_bounds__(RNT_, MINB) gemm_rw_kernel(LinearArgs p) {
     for (int i = 0; i < RFM; ++i) aa[i] = *reinterpret_cast<const u32x4*>(xb + 32 * i * (BK * 2) + off);
   };
   auto step = [&](int st, const WSet& cur, WSet& nxt2) {
-    // 256-row tiles: three stages, the DMA two steps ahead (the stage it fills was last
-    // read before the previous step's barrier); 128-row tiles: two stages, one step ahead
-    const int buf = RFM == 8 ? st % 3 : st & 1;
-    if (RFM == 8)
-      issue_x(st + 2, (st + 2) % 3);
-    else
-      issue_x(st + 1, buf ^ 1);
+    // three stages, the DMA two steps ahead (the stage it fills was last read before the
+    // previous step's barrier)
+    const int buf = st % 3;
+    issue_x(st + 2, (st + 2) % 3);
     issue_w(st + 2, nxt2);
     float sf[RFN], cf[RFN];
 #pragma unroll
@@ -614,15 +610,15 @@ __global__ void __launch_bounds__(RNT_, MINB) gemm_rw_kernel(LinearArgs p) {
         dequant(kk + 1, b[(kk + 1) & 1]);
       } else {
         // The next step's activation DMA must have landed (the loads issued after it stay
-        // in flight: the weights for two steps ahead, and with three stages the DMA and
-        // weights issued in this step; in step 0 the count also waits for step 0's weights,
-        // issued after step 1's DMA in the prologue, which is merely conservative); the
-        // barrier also orders every wave's reads of this stage before a later DMA into it.
+        // in flight: its step's weight loads, and the DMA and weights issued in this step;
+        // in step 0 the count also waits for step 0's weights, issued after step 1's DMA in
+        // the prologue, which is merely conservative); the barrier also orders every wave's
+        // reads of this stage before a later DMA into it.
         constexpr int kW = RFN * WLB + (GROUPED ? RFN : 0);
-        constexpr int kAfter = RFM == 8 ? 2 * kW + kXB : kW;
+        constexpr int kAfter = 2 * kW + kXB;
         __builtin_amdgcn_s_waitcnt((kAfter & 15) | (7 << 4) | ((kAfter >> 4) << 14));
         lds_barrier();
-        load_a(RFM == 8 ? (st + 1) % 3 : buf ^ 1, 0, a[0]);
+        load_a((st + 1) % 3, 0, a[0]);
       }
 #pragma unroll
       for (int i = 0; i < RFM; ++i)
@@ -649,7 +645,7 @@ __global__ void __launch_bounds__(RNT_, MINB) gemm_rw_kernel(LinearArgs p) {
 
   WSet r0, r1, r2;
   issue_x(0, 0);
-  if (RFM == 8) issue_x(1, 1);
+  issue_x(1, 1);
   issue_w(0, r0);
   issue_w(1, r1);
   {
