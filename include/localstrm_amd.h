@@ -130,12 +130,13 @@ int lsq_w4_linear(const void* x, int64_t ldx, const uint8_t* weight_packed,
  * Same contract and results as lsq_w8_linear / lsq_w4_linear (the same reference lines,
  * quantization.py:129-141), plus `workspace` (device memory, 16-byte aligned, or NULL) of
  * `workspace_bytes`. With at least lsq_linear_workspace_bytes(M, N, K) bytes, decode
- * shapes of 1-16 tokens on layers of fewer than 1024 16-row tiles and K of 8+ 128-column
- * tiles (down projections such as 3584 x 18944) split K over workgroups: each slice's
- * fp32 partial sums go to the workspace and a second kernel adds them in slice order,
- * adds the bias and rounds to T. With a smaller or NULL workspace these calls behave
- * exactly like the plain entry points. The workspace is scratch for the duration of the
- * call on `stream` (its contents are not read before being written). */
+ * calls on down-projection-shaped layers split K over workgroups (4-16 tokens whose
+ * activations exceed 96 KB on layers of at most 512 16-row tiles, e.g. 3584 x 18944;
+ * 17-64 tokens on layers of at most 128 row tiles with 16+ 128-column tiles, e.g.
+ * 896 x 4864): each slice's fp32 partial sums go to the workspace and a second kernel adds
+ * them in slice order, adds the bias and rounds to T. With a smaller or NULL workspace
+ * these calls behave exactly like the plain entry points. The workspace is scratch for
+ * the duration of the call on `stream` (its contents are not read before being written). */
 int64_t lsq_linear_workspace_bytes(int64_t M, int64_t N, int64_t K);
 int lsq_w8_linear_ws(const void* x, int64_t ldx, const int8_t* weight_q, const int8_t* tiled,
                      const void* scale, int scale_dtype, const void* bias, int bias_dtype, void* y,
