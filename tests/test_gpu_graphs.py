@@ -70,3 +70,16 @@ def test_paged_attention_graph_replays():
     q2 = torch.randn(b, h, 1, d, generator=g).half().to(DEV)
     run = lambda qq: paged_attention_decode(qq, kp, vp, bt, sl, bs, ks, vs, max_sl=seq)
     _check_graph(lambda: run(q), lambda: run(q2))
+
+
+@pytest.mark.parametrize("n,k,m", [(3584, 18944, 8), (896, 4864, 32), (896, 4864, 16)])
+def test_split_k_graph_replays(n, k, m):
+    """The split-K decode forms (16-token split at 3584 x 18944, the batched split at
+    896 x 4864), whose workspace the module takes from torch's allocator inside forward:
+    captured, replayed three times with eager calls of the same layer in between, every
+    replay equal to the eager result bit for bit."""
+    print(f"split-K graph N={n} K={k} M={m}", flush=True)
+    torch.manual_seed(n + m)
+    layer = QuantizedLinear.from_float(nn.Linear(k, n, bias=True), "int4", group_size=128).to(DEV)
+    x = torch.randn(m, k, device=DEV).to(torch.bfloat16)
+    _check_graph(lambda: layer(x), lambda: layer(x))
