@@ -6,10 +6,17 @@
 // block into a contiguous copy, dequantizes it (keys.to(T) * scales), expands the GQA
 // heads and calls F.scaled_dot_product_attention. Here nothing is copied:
 //
-//  * paged_attn_mfma_kernel (fp16 / bf16 queries): one workgroup per (sequence, KV head,
-//    split of one or more 256-token chunks), scores and P x V on the MFMA, an online
-//    softmax across the split's chunks, each chunk's loads issued while the previous one
-//    finishes; described at the kernel;
+//  * paged_attn_i8_kernel (INT8 cache, fp16 / bf16 queries; the default there): one
+//    workgroup per (sequence, KV head, split of one or more 256-token chunks) whose four
+//    waves each take 64 tokens of a chunk with an online softmax of their own (no
+//    barrier until the end); scores and P x V on the MFMA with the probabilities used
+//    where the scores leave them and the values read transposed out of LDS
+//    (ds_read_b64_tr_b8); keys and values dequantized in registers; described at the
+//    kernel;
+//  * paged_attn_mfma_kernel (fp16 / bf16 queries with a T cache, or LSQ_PAGED_KERNEL=mfma):
+//    one workgroup per (sequence, KV head, split), the chunk's scores, softmax and P x V
+//    shared by its four waves through LDS, an online softmax across the split's chunks,
+//    each chunk's loads issued while the previous one finishes; described at the kernel;
 //  * paged_attn_split_kernel (fp32, or LSQ_PAGED_KERNEL=valu): one workgroup per
 //    (sequence, KV head, split of 256 tokens);
 //    thread t takes token t of the split: it walks the block table to the token's row,
@@ -60,6 +67,7 @@ struct PagedArgs {
   float* ws;              // [B, H, nsplit, D + 2] partials when nsplit > 1
   int B, H, Hkv, G, BS, nsplit, max_sl, interleaved;
   int cps;                // chunks of kPaNT tokens per split (MFMA kernel; the VALU kernel: 1)
+  int bs_m16;             // ceil(2^16 / BS) for BS < 64 (block / slot of a token, wave kernel)
   float sm_scale;
 };
 
@@ -597,6 +605,345 @@ __global__ void __launch_bounds__(kPaNT) paged_attn_mfma_kernel(PagedArgs p) {
   }
 }
 
+// ---------------------------------------------------------------------------------------
+// INT8 KV cache, fp16 / bf16 queries (the default for that cache): waves that work on
+// their own. Wave w of a workgroup takes tokens 64 w .. 64 w + 63 of each 256-token chunk
+// of the split (four 16-token tiles) with an online softmax of its own, so the waves meet
+// once, at the end, where their (max, sum, partial output) are merged in LDS.
+//  * Scores as S^T = K q^T on v_mfma_f32_16x16x32: A = the dequantized keys of a tile
+//    (row = token; lane l loads D / 4 contiguous bytes of token l & 15, so one k step of
+//    the product takes dims D / 4 (l >> 4) + 8 s .. +7, and q is loaded in the same
+//    order), B = q^T (column = head, zero past G). A lane then holds the scores of one
+//    head (l & 15) for tokens 4 (l >> 4) .. +3 of each tile: the running max and sum are
+//    per lane, the max shared by a head's 4 lanes through two shuffles.
+//  * Value sum as O^T = V^T P^T: B = the probabilities where the scores left them (k
+//    index 8 G + e of a 32-token step is token 4 G + e of its first tile for e < 4 and
+//    16 + 4 G + e - 4 of its second, G = l >> 4), A = the values of those tokens for 16
+//    dims. The wave stores its values in LDS as loaded (a token's bytes per lane) and
+//    reads them back transposed with ds_read_b64_tr_b8, which hands lane 16 G + 8 h + j
+//    byte j of the 8-byte rows addressed by lanes 16 G + h + 2 i, i = 0..7. O^T leaves a
+//    lane with one head's outputs, so rescaling by e^(m_old - m_new) is per lane too.
+//  * Dequantization in registers: byte b ^ 0x80 placed under the fp16 exponent of 1024
+//    (v_perm) is exactly 1024 + 128 + k; minus 1152 gives k; times an fp16 scale rounds
+//    once (v_pk_mul_f16), which is round_T(k * s), the reference's keys.to(T) * scales.
+//    Other scale / query types go through fp32 as in the kernels above.
+//  * Loads: a chunk's block-table entries one chunk ahead, its keys, values and scales
+//    while the previous chunk's softmax and value sum run.
+constexpr int kI8Waves = 4;
+constexpr int kI8Tok = kPaNT / kI8Waves;  // tokens per wave and chunk (4 tiles of 16)
+
+// Row stride (bytes) of a wave's value tile in LDS.
+__host__ __device__ constexpr int i8_vld(int d) { return d + 16; }
+
+typedef _Float16 f16x2v __attribute__((ext_vector_type(2)));
+
+// 8 int8 (two dwords) -> 8 fp16 values k exactly, as 4 packed pairs (element e of the
+// result = byte e).
+__device__ __forceinline__ void i8x8_to_f16(uint32_t w0, uint32_t w1, f16x2v (&h)[4]) {
+  const uint32_t u0 = w0 ^ 0x80808080u, u1 = w1 ^ 0x80808080u;
+  const f16x2v off = {static_cast<_Float16>(1152.f), static_cast<_Float16>(1152.f)};
+  h[0] = __builtin_bit_cast(f16x2v, __builtin_amdgcn_perm(u0, 0x64646464u, 0x00050004u)) - off;
+  h[1] = __builtin_bit_cast(f16x2v, __builtin_amdgcn_perm(u0, 0x64646464u, 0x00070006u)) - off;
+  h[2] = __builtin_bit_cast(f16x2v, __builtin_amdgcn_perm(u1, 0x64646464u, 0x00050004u)) - off;
+  h[3] = __builtin_bit_cast(f16x2v, __builtin_amdgcn_perm(u1, 0x64646464u, 0x00070006u)) - off;
+}
+
+// Two fp32 values -> packed T pair, round to nearest even.
+template <int DT>
+__device__ __forceinline__ uint32_t pack_rne(float a, float b) {
+  if constexpr (DT == LSQ_F16) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){a, b}, f16x2v));
+  } else {
+    return Mma<LSQ_BF16>::pack2(a, b);
+  }
+}
+
+// Operand of 8 dequantized elements round_T(k_e * s_e). FAST: T = fp16 with fp16 scales
+// (s2[j] = the scales of elements 2 j, 2 j + 1 as an fp16 pair); otherwise sf[e] in fp32.
+template <int DT, bool FAST>
+__device__ __forceinline__ u32x4 i8x8_dequant(uint32_t w0, uint32_t w1, const f16x2v (&s2)[4], const float (&sf)[8]) {
+  f16x2v h[4];
+  i8x8_to_f16(w0, w1, h);
+  u32x4 r;
+  if constexpr (FAST) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) r[j] = __builtin_bit_cast(uint32_t, h[j] * s2[j]);
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      r[j] = pack_rne<DT>(opaque(static_cast<float>(h[j][0]) * sf[2 * j]), opaque(static_cast<float>(h[j][1]) * sf[2 * j + 1]));
+  }
+  return r;
+}
+
+template <int DT, int D, bool FAST>
+__global__ void __launch_bounds__(kPaNT) paged_attn_i8_kernel(PagedArgs p) {
+  constexpr int KB = D / 4;          // bytes of a token row per lane
+  constexpr int NL = KB / 16;        // 16-byte loads per lane per token (1 or 2)
+  constexpr int KS = D / 32;         // k steps of the score product
+  constexpr int DTL = D / 16;        // 16-dim tiles of the value sum
+  constexpr int VLD = i8_vld(D);
+  constexpr float kNegInf = -__builtin_huge_valf();
+  constexpr float kLog2e = 1.4426950408889634f;
+  using S = typename Act<DT>::storage;
+  __shared__ __align__(16) unsigned char vt[kI8Waves * kI8Tok * VLD];  // values; merge sums after
+  __shared__ __align__(16) float vsc[kI8Waves * kI8Tok];               // value scales (0: invalid)
+  __shared__ __align__(16) unsigned char vok[kI8Waves * kI8Tok];       // token valid
+  __shared__ float ml[kI8Waves * 16 * 2];                              // per wave and head: max, sum
+  static_assert(kI8Waves * kI8Tok * VLD >= kI8Waves * 16 * D * 4, "merge sums alias the value tiles");
+
+  const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int r16 = lane & 15, q4 = lane >> 4;
+  const int G = p.G;
+  auto head = [&](int g) { return p.interleaved ? g * p.Hkv + kvh : kvh * G + g; };
+  unsigned char* vtw = vt + wid * kI8Tok * VLD;
+  float* vscw = vsc + wid * kI8Tok;
+  unsigned char* vokw = vok + wid * kI8Tok;
+
+  // q^T operand: lane (head r16, group q4), k step s -> q[head][KB q4 + 8 s .. +7]
+  u32x4 qb[KS];
+  {
+    const bool hv = r16 < G;
+    const S* qrow = static_cast<const S*>(p.q) + (static_cast<int64_t>(b) * p.H + head(hv ? r16 : 0)) * D + KB * q4;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      const u32x4 v = *reinterpret_cast<const u32x4*>(qrow + 8 * s);
+      qb[s] = hv ? v : u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+  const int seq = static_cast<int>(p.sl[b]);
+  const int nchunk = (p.max_sl + kPaNT - 1) / kPaNT;
+  const int c_lo = split * p.cps;
+  const int c_hi = min(c_lo + p.cps, nchunk);
+  // tokens below `lim` may be attended (a mask decides among them); the table holds
+  // ceil(max_seq_len / block_size) entries per sequence, read for every token below
+  // max_seq_len (later tokens read the last one and are masked)
+  const int lim = p.mask ? p.max_sl : min(p.max_sl, seq);
+  const int qmax = p.max_sl > 0 ? (p.max_sl - 1) / p.BS : 0;
+  const int BS = p.BS;
+  const int64_t* btrow = p.bt + static_cast<int64_t>(b) * p.ldbt;
+
+  // Block-table entry and in-block slot of token T0 + 16 tt + r16 (T0 = this wave's first
+  // token of chunk c): one uniform division per chunk, then per lane a wrap (BS >= 64) or
+  // a multiply-high by ceil(2^16 / BS) (exact: remainders stay below 64 + BS).
+  int64_t blk[4] = {0, 0, 0, 0};
+  int slot[4] = {0, 0, 0, 0}, slot_n[4] = {0, 0, 0, 0};
+  auto load_bt = [&](int c, int (&sl_out)[4]) {
+    if (c < c_hi) {  // uniform; then max_seq_len > 0
+      const int T0 = c * kPaNT + wid * kI8Tok;
+      const int qb0 = T0 / BS, rb0 = T0 - qb0 * BS;
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt) {
+        const int rm = rb0 + 16 * tt + r16;
+        int qa;
+        if (BS >= 64) qa = rm >= BS ? 1 : 0;
+        else qa = static_cast<int>((static_cast<uint32_t>(rm) * static_cast<uint32_t>(p.bs_m16)) >> 16);
+        sl_out[tt] = rm - qa * BS;
+        blk[tt] = btrow[min(qb0 + qa, qmax)];
+      }
+    }
+  };
+  auto block_of = [&](int64_t e) -> int {
+    const int64_t i = e < 0 ? e + p.nb : e;
+    return (i >= 0 && i < p.nb) ? static_cast<int>(i) : -1;
+  };
+  u32x4 kr[4][NL], vr[4][NL];
+  uint32_t ksw[4], vsw[4];
+  int shalf[4];
+  bool val[4];
+  const int es_s = p.scale_dt == LSQ_F32 ? 4 : 2;
+  // Keys, values and scales of tiles 2 h, 2 h + 1 of chunk c (an invalid token, or a
+  // chunk past the last, reads row 0; its results are discarded). Branch-free except
+  // for the (uniform) mask, so the compiler's waits for them are exact.
+  // the mask row (a mask row holds max_seq_len entries), or without a mask a byte that is
+  // always there (the first table entry), so that the load needs no branch
+  const bool usem = p.mask != nullptr;
+  const unsigned char* mrow = usem ? p.mask + static_cast<int64_t>(b * p.mask_rows_per_b + (p.mask_rows_per_b > 1 ? kvh : 0)) * p.ldm
+                                   : reinterpret_cast<const unsigned char*>(p.bt);
+  auto load_half = [&](int c, int h) {  // (c < c_hi: then max_seq_len > 0)
+    const int T0 = c * kPaNT + wid * kI8Tok;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int tt = 2 * h + u;
+      const int t = T0 + 16 * tt + r16;
+      const bool mok = mrow[usem ? min(t, p.max_sl - 1) : 0] != 0 || !usem;
+      const int bi = block_of(blk[tt]);
+      // the row does not wait for the mask byte: a masked token reads its own row
+      const bool in = t < lim && bi >= 0;
+      val[tt] = in && mok;
+      const int row = in ? (bi * BS + slot[tt]) * p.Hkv + kvh : 0;
+      const int64_t so = (static_cast<int64_t>(row) * es_s) & ~int64_t(3);
+      ksw[tt] = *reinterpret_cast<const uint32_t*>(static_cast<const unsigned char*>(p.ks) + so);
+      vsw[tt] = *reinterpret_cast<const uint32_t*>(static_cast<const unsigned char*>(p.vs) + so);
+      shalf[tt] = scale_half(p.scale_dt, row);
+      const int64_t ro = static_cast<int64_t>(row) * D + KB * q4;
+#pragma unroll
+      for (int i = 0; i < NL; ++i) {
+        kr[tt][i] = *reinterpret_cast<const u32x4*>(static_cast<const unsigned char*>(p.kp) + ro + 16 * i);
+        vr[tt][i] = *reinterpret_cast<const u32x4*>(static_cast<const unsigned char*>(p.vp) + ro + 16 * i);
+      }
+    }
+  };
+  if (c_lo < c_hi) {  // uniform
+    load_bt(c_lo, slot);
+    load_half(c_lo, 0);
+    load_half(c_lo, 1);
+    load_bt(c_lo + 1, slot_n);
+  }
+
+  const float c2 = p.sm_scale * kLog2e;  // scores in the log2 domain
+  float m_run = kNegInf, l_run = 0.f;
+  f32x4 ot[DTL];
+#pragma unroll
+  for (int t = 0; t < DTL; ++t) ot[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // ds_read_b64_tr_b8 source row / column of this lane: token pi(q4, i) of a 32-token
+  // step (i = (lane & 15) >> 1), dims 8 (lane & 1) .. +7 of a 16-dim tile
+  const int tr_i = r16 >> 1;
+  const int tr_row = tr_i < 4 ? 4 * q4 + tr_i : 16 + 4 * q4 + tr_i - 4;
+  const int tr_col = 8 * (lane & 1);
+
+  for (int c = c_lo; c < c_hi; ++c) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      // ---- values of tiles 2 h, 2 h + 1 (as loaded), their scales and validity into LDS
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int tt = 2 * h + u;
+        const int tl = tt * 16 + r16;
+#pragma unroll
+        for (int i = 0; i < NL; ++i) *reinterpret_cast<u32x4*>(vtw + tl * VLD + KB * q4 + 16 * i) = vr[tt][i];
+        if (q4 == 0) {
+          vscw[tl] = val[tt] ? dword_elem(vsw[tt], shalf[tt], p.scale_dt) : 0.f;
+          vokw[tl] = val[tt] ? 1 : 0;
+        }
+      }
+      // ---- scores S^T of the two tiles: A = keys (token r16), B = q^T
+      f32x4 sc[2];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int tt = 2 * h + u;
+        const float ks = dword_elem(ksw[tt], shalf[tt], p.scale_dt);
+        f16x2v s2[4];
+        float sf[8];
+        if constexpr (FAST) {
+          const _Float16 kh = static_cast<_Float16>(ks);  // exact: an fp16 scale
+#pragma unroll
+          for (int j = 0; j < 4; ++j) s2[j] = f16x2v{kh, kh};
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) sf[e] = ks;
+        }
+        sc[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+          const int i = (8 * s) / 16, o = ((8 * s) % 16) / 4;  // dwords o, o + 1 of load i
+          const u32x4 a = i8x8_dequant<DT, FAST>(kr[tt][i][o], kr[tt][i][o + 1], s2, sf);
+          sc[u] = Mma<DT>::mma(a, qb[s], sc[u]);
+        }
+      }
+      // ---- this half's registers are free: the next chunk's loads for them
+      if (c + 1 < c_hi) {  // uniform
+        if (h == 0) {
+#pragma unroll
+          for (int tt = 0; tt < 4; ++tt) slot[tt] = slot_n[tt];
+        }
+        load_half(c + 1, h);
+        if (h == 1) load_bt(c + 2, slot_n);
+      }
+      // ---- online softmax of head r16 over this lane's 8 tokens of the two tiles
+      float cmax = kNegInf;
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const uint32_t ok = *reinterpret_cast<const uint32_t*>(vokw + (2 * h + u) * 16 + 4 * q4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          sc[u][e] = ((ok >> (8 * e)) & 0xFF) ? sc[u][e] * c2 : kNegInf;
+          cmax = fmaxf(cmax, sc[u][e]);
+        }
+      }
+      cmax = fmaxf(cmax, __shfl_xor(cmax, 16));
+      cmax = fmaxf(cmax, __shfl_xor(cmax, 32));
+      const float m_new = fmaxf(m_run, cmax);
+      const float msub = m_new == kNegInf ? 0.f : m_new;  // (an all-invalid run: every p is 0)
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sc[u][e] = __builtin_amdgcn_exp2f(sc[u][e] - msub);
+      const float lsum = (sc[0][0] + sc[0][1]) + (sc[0][2] + sc[0][3]) + ((sc[1][0] + sc[1][1]) + (sc[1][2] + sc[1][3]));
+      const float f = __builtin_amdgcn_exp2f(m_run - msub);  // 0 while m_run is -inf
+      l_run = fmaf(l_run, f, lsum);
+#pragma unroll
+      for (int t = 0; t < DTL; ++t)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) ot[t][e] *= f;
+      m_run = m_new;
+      // ---- value sum O^T += V^T P^T over the half's 32 tokens
+      u32x4 pb;
+      pb[0] = pack_rne<DT>(sc[0][0], sc[0][1]);
+      pb[1] = pack_rne<DT>(sc[0][2], sc[0][3]);
+      pb[2] = pack_rne<DT>(sc[1][0], sc[1][1]);
+      pb[3] = pack_rne<DT>(sc[1][2], sc[1][3]);
+      // scales of the step's tokens pi(q4, 0..7)
+      const f32x4 s0 = *reinterpret_cast<const f32x4*>(vscw + 32 * h + 4 * q4);
+      const f32x4 s1 = *reinterpret_cast<const f32x4*>(vscw + 32 * h + 16 + 4 * q4);
+      float sf[8] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
+      f16x2v s2[4];
+      if constexpr (FAST) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) s2[j] = f16x2v{static_cast<_Float16>(sf[2 * j]), static_cast<_Float16>(sf[2 * j + 1])};
+      }
+      const unsigned char* src = vtw + (32 * h + tr_row) * VLD + tr_col;
+#pragma unroll
+      for (int t = 0; t < DTL; ++t) {
+        typedef int v2i __attribute__((ext_vector_type(2)));
+        const v2i raw = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+            (__attribute__((address_space(3))) v2i*)(src + 16 * t));
+        const u32x4 a = i8x8_dequant<DT, FAST>(static_cast<uint32_t>(raw[0]), static_cast<uint32_t>(raw[1]), s2, sf);
+        ot[t] = Mma<DT>::mma(a, pb, ot[t]);
+      }
+    }
+  }
+
+  // ---- merge the waves: sum of the head over its 4 lanes, then (max, sum, O^T) in LDS
+  l_run += __shfl_xor(l_run, 16);
+  l_run += __shfl_xor(l_run, 32);
+  __syncthreads();  // every wave is done with its value tile (the sums alias them)
+  float* accs = reinterpret_cast<float*>(vt);  // [wave][head][D]
+#pragma unroll
+  for (int t = 0; t < DTL; ++t)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) accs[(wid * 16 + r16) * D + 16 * t + 4 * q4 + e] = ot[t][e];
+  if (q4 == 0) {
+    ml[(wid * 16 + r16) * 2] = m_run;
+    ml[(wid * 16 + r16) * 2 + 1] = l_run;
+  }
+  __syncthreads();
+  for (int i = tid; i < G * D; i += kPaNT) {
+    const int g = i / D, d = i - (i / D) * D;
+    float M = kNegInf;
+#pragma unroll
+    for (int w = 0; w < kI8Waves; ++w) M = fmaxf(M, ml[(w * 16 + g) * 2]);
+    const float Ms = M == kNegInf ? 0.f : M;
+    float a = 0.f, l = 0.f;
+#pragma unroll
+    for (int w = 0; w < kI8Waves; ++w) {
+      const float fw = __builtin_amdgcn_exp2f(ml[(w * 16 + g) * 2] - Ms);  // 0 for an empty wave
+      a = fmaf(fw, accs[(w * 16 + g) * D + d], a);
+      l = fmaf(fw, ml[(w * 16 + g) * 2 + 1], l);
+    }
+    const int64_t oh = static_cast<int64_t>(b) * p.H + head(g);
+    if (p.nsplit == 1) {
+      static_cast<S*>(p.out)[oh * D + d] = Act<DT>::from_f32(opaque(a / l));
+    } else {
+      // the combine kernel works in the natural-log domain
+      float* w = p.ws + (oh * p.nsplit + split) * (D + 2);
+      if (d == 0) { w[0] = M == kNegInf ? M : M / kLog2e; w[1] = l; }
+      w[2 + d] = a;
+    }
+  }
+}
+
 // One workgroup of D threads per (sequence, head): out = sum_s e^(m_s - M) acc_s /
 // sum_s e^(m_s - M) l_s over the splits. (A ticket in the split kernel would save this
 // launch, but the device-scope release / acquire it needs writes back and invalidates
@@ -641,10 +988,15 @@ __global__ void __launch_bounds__(D) paged_attn_combine_kernel(PagedArgs p) {
   static_cast<S*>(p.out)[oh * D + d] = Act<DT>::from_f32(opaque(a / l));
 }
 
-// LSQ_PAGED_KERNEL=valu runs the VALU split kernel for fp16 / bf16 too (comparisons).
+// LSQ_PAGED_KERNEL=valu runs the VALU split kernel for fp16 / bf16 too, =mfma the
+// block-wide MFMA kernel for an INT8 cache too (comparisons).
 bool paged_valu() {
   const char* e = std::getenv("LSQ_PAGED_KERNEL");
   return e && e[0] == 'v';
+}
+bool paged_block_mfma() {
+  const char* e = std::getenv("LSQ_PAGED_KERNEL");
+  return e && e[0] == 'm';
 }
 
 // Chunks of kPaNT tokens per workgroup of the MFMA kernel (each split loops over its
@@ -673,8 +1025,16 @@ int launch_paged(const PagedArgs& a0, hipStream_t s) {
   a.nsplit = (nchunk + a.cps - 1) / a.cps;
   const dim3 grid(static_cast<unsigned>(a.nsplit), static_cast<unsigned>(a.Hkv), static_cast<unsigned>(a.B));
   if constexpr (DT != LSQ_F32) {
-    if (mfma) paged_attn_mfma_kernel<DT, I8, D><<<grid, dim3(kPaNT), 0, s>>>(a);
-    else paged_attn_split_kernel<DT, I8, D><<<grid, dim3(kPaNT), 0, s>>>(a);
+    // INT8 cache: the wave-wise kernel (its q operand is read 16 bytes at a time)
+    const bool waves = I8 && mfma && !paged_block_mfma() && (reinterpret_cast<uintptr_t>(a.q) & 15) == 0;
+    if (waves && DT == LSQ_F16 && a.scale_dt == LSQ_F16)
+      paged_attn_i8_kernel<DT, D, true><<<grid, dim3(kPaNT), 0, s>>>(a);
+    else if (waves)
+      paged_attn_i8_kernel<DT, D, false><<<grid, dim3(kPaNT), 0, s>>>(a);
+    else if (mfma)
+      paged_attn_mfma_kernel<DT, I8, D><<<grid, dim3(kPaNT), 0, s>>>(a);
+    else
+      paged_attn_split_kernel<DT, I8, D><<<grid, dim3(kPaNT), 0, s>>>(a);
   } else {
     paged_attn_split_kernel<DT, I8, D><<<grid, dim3(kPaNT), 0, s>>>(a);
   }
@@ -724,6 +1084,8 @@ extern "C" int lsq_paged_attention_decode(
   if (num_blocks * block_size * Hkv >= (int64_t(1) << 31)) return LSQ_E_SHAPE;
   if (mask && (mask_rows_per_b != 1 && mask_rows_per_b != Hkv)) return LSQ_E_SHAPE;
   if (mask && mask_stride < max_seq_len) return LSQ_E_SHAPE;
+  // masked tokens read pool row 0 (their results discarded): an empty pool has none
+  if (num_blocks == 0 && max_seq_len > 0 && B > 0) return LSQ_E_SHAPE;
   if (B == 0) return LSQ_OK;
   if (!query || !k_pool || !v_pool || !block_tables || !seq_lens || !out) return LSQ_E_NULL;
   if (i8 && (!k_scales || !v_scales)) return LSQ_E_NULL;
@@ -743,6 +1105,7 @@ extern "C" int lsq_paged_attention_decode(
   a.nsplit = static_cast<int>(nsplit); a.max_sl = static_cast<int>(max_seq_len);
   a.interleaved = head_mapping != 0;
   a.sm_scale = 1.0f / std::sqrt(static_cast<float>(D));
+  a.bs_m16 = block_size < 64 ? static_cast<int>((65536 + block_size - 1) / block_size) : 0;
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (dtype) {
     case LSQ_F32: return launch_paged_dt<LSQ_F32>(a, i8, static_cast<int>(D), s);

@@ -35,7 +35,8 @@ def _case(seed, b, h, hkv, d, bs, seqs, int8, dt, spare=5):
     return q, kp, vp, ks, vs, bt, np.array(seqs, dtype=np.int64)
 
 
-def _run(q, kp, vp, ks, vs, bt, seqs, bs, dt, mapping="contiguous", mask=None, max_sl=None):
+def _run(q, kp, vp, ks, vs, bt, seqs, bs, dt, mapping="contiguous", mask=None, max_sl=None,
+         scale_dtype=torch.float16):
     t = TDT[dt]
     kv_t = torch.int8 if kp.dtype == np.int8 else t
     args = dict(
@@ -47,8 +48,8 @@ def _run(q, kp, vp, ks, vs, bt, seqs, bs, dt, mapping="contiguous", mask=None, m
         attn_mask=None if mask is None else torch.from_numpy(mask).to(DEV),
     )
     if ks is not None:
-        args["k_scales"] = torch.from_numpy(ks).half().unsqueeze(-1).to(DEV)
-        args["v_scales"] = torch.from_numpy(vs).half().unsqueeze(-1).to(DEV)
+        args["k_scales"] = torch.from_numpy(ks).to(scale_dtype).unsqueeze(-1).to(DEV)
+        args["v_scales"] = torch.from_numpy(vs).to(scale_dtype).unsqueeze(-1).to(DEV)
     out = paged_attention_decode(**args)
     torch.cuda.synchronize()
     return out[:, :, 0, :].float().cpu().numpy()
@@ -65,13 +66,21 @@ CASES = [
 ]
 
 
-@pytest.mark.parametrize("kernel", ["mfma", "valu"])
+# kernels: "default" (an INT8 cache with fp16 / bf16 queries: the wave-wise kernel; a T
+# cache: the block-wide MFMA kernel; fp32: the VALU kernel), "block" (LSQ_PAGED_KERNEL=mfma:
+# the block-wide MFMA kernel for an INT8 cache too), "valu" (the VALU kernel throughout)
+KERNEL_ENV = {"default": None, "block": "mfma", "valu": "valu"}
+
+
+def _kernel(monkeypatch, kernel):
+    if KERNEL_ENV[kernel]:
+        monkeypatch.setenv("LSQ_PAGED_KERNEL", KERNEL_ENV[kernel])
+
+
+@pytest.mark.parametrize("kernel", ["default", "block", "valu"])
 @pytest.mark.parametrize("b,h,hkv,d,bs,seqs,int8,dt,mapping", CASES)
 def test_paged_attention_matches_oracle(monkeypatch, kernel, b, h, hkv, d, bs, seqs, int8, dt, mapping):
-    # fp16 / bf16 queries run the MFMA kernel by default; LSQ_PAGED_KERNEL=valu the VALU one
-    # (the only one for fp32)
-    if kernel == "valu":
-        monkeypatch.setenv("LSQ_PAGED_KERNEL", "valu")
+    _kernel(monkeypatch, kernel)
     print(f"paged {kernel} B={b} H={h} Hkv={hkv} D={d} BS={bs} seqs={seqs} int8={int8} {dt} {mapping}", flush=True)
     q, kp, vp, ks, vs, bt, sl = _case(b + h + d, b, h, hkv, d, bs, seqs, int8, dt)
     got = _run(q, kp, vp, ks, vs, bt, sl, bs, dt, mapping)
@@ -81,13 +90,18 @@ def test_paged_attention_matches_oracle(monkeypatch, kernel, b, h, hkv, d, bs, s
     assert err <= 1e-2
 
 
+@pytest.mark.parametrize("kernel", ["default", "block"])
 @pytest.mark.parametrize("chunks", ["2", "3", "8"])
 @pytest.mark.parametrize("b,h,hkv,d,bs,seqs,int8,dt,mapping", [c for c in CASES if c[7] != "f32"])
-def test_paged_attention_multi_chunk_splits(monkeypatch, chunks, b, h, hkv, d, bs, seqs, int8, dt, mapping):
+def test_paged_attention_multi_chunk_splits(monkeypatch, kernel, chunks, b, h, hkv, d, bs, seqs, int8, dt, mapping):
     # workgroups that loop over several 256-token chunks (online softmax across chunks,
     # next chunk's loads in flight), forced for every MFMA case; a split count that does not
     # divide the chunks leaves a short last split, and 8 chunks puts whole sequences in one
-    print(f"paged chunks={chunks} B={b} H={h} Hkv={hkv} D={d} seqs={seqs} int8={int8} {dt} {mapping}", flush=True)
+    if kernel == "block" and not int8:
+        pytest.skip("a T cache runs the block-wide kernel by default")
+    _kernel(monkeypatch, kernel)
+    print(f"paged {kernel} chunks={chunks} B={b} H={h} Hkv={hkv} D={d} seqs={seqs} int8={int8} {dt} {mapping}",
+          flush=True)
     monkeypatch.setenv("LSQ_PAGED_CHUNKS", chunks)
     q, kp, vp, ks, vs, bt, sl = _case(b + h + d + 1, b, h, hkv, d, bs, seqs, int8, dt)
     got = _run(q, kp, vp, ks, vs, bt, sl, bs, dt, mapping)
@@ -164,14 +178,13 @@ def test_paged_attention_validation():
         paged_attention_decode(q, kp.half(), kp.half(), bt, sl, max_sl=40)
 
 
-@pytest.mark.parametrize("kernel", ["mfma", "valu"])
+@pytest.mark.parametrize("kernel", ["default", "block", "valu"])
 def test_paged_attention_out_of_range_block_ids(monkeypatch, kernel):
     """Block-table entries past each sequence's length may hold anything: -1 pads, ids at
     or above the pool size, huge values. They are read (the table is read up to max_sl)
     but must neither fault nor change the result; an in-range negative entry counts from
     the end of the pool. Inside a sequence, an out-of-range entry masks its tokens."""
-    if kernel == "valu":
-        monkeypatch.setenv("LSQ_PAGED_KERNEL", "valu")
+    _kernel(monkeypatch, kernel)
     b, h, hkv, d, bs = 3, 14, 2, 64, 16
     seqs = [40, 300, 513]
     q, kp, vp, ks, vs, bt, sl = _case(77, b, h, hkv, d, bs, seqs, True, "f16")
@@ -206,3 +219,46 @@ def test_paged_attention_rejects_short_seq_lens():
     q, kp, vp, ks, vs, bt, sl = _case(5, 3, 4, 2, 64, 16, [20, 30, 40], True, "f16")
     with pytest.raises(ValueError, match="seq_lens"):
         _run(q, kp, vp, ks, vs, bt, sl[:2], 16, "f16", max_sl=40)
+
+
+@pytest.mark.parametrize("bs", [1, 5, 24, 64, 80, 256])
+def test_paged_attention_block_sizes(bs):
+    """The wave-wise kernel's block / slot arithmetic (a multiply-high below 64 tokens per
+    block, one wrap from 64 on) on block sizes that are and are not powers of two, with
+    sequences that end inside a block and cross chunk boundaries; INT8 cache, fp16 queries."""
+    seqs = [3, bs + 1, 257, 700]
+    print(f"paged block size {bs} seqs={seqs}", flush=True)
+    q, kp, vp, ks, vs, bt, sl = _case(bs + 3, 4, 14, 2, 64, bs, seqs, True, "f16")
+    got = _run(q, kp, vp, ks, vs, bt, sl, bs, "f16")
+    ref = qo.paged_attention(q, kp, vp, bt, sl, bs, "f16", ks, vs, "contiguous")
+    assert qo.rel_err(got, ref) <= 1e-2
+
+
+@pytest.mark.parametrize("kernel", ["default", "block"])
+@pytest.mark.parametrize("d,dt", [(64, "f16"), (128, "f16"), (64, "bf16")])
+def test_paged_attention_fp32_scales(monkeypatch, kernel, d, dt):
+    """fp32 per-token scales (the same values as the fp16 ones of the other tests): the
+    dequantization through fp32 instead of the packed fp16 product for fp16 queries."""
+    _kernel(monkeypatch, kernel)
+    seqs = [100, 600, 2048]
+    q, kp, vp, ks, vs, bt, sl = _case(d + 9, 3, 8, 2, d, 16, seqs, True, dt)
+    got = _run(q, kp, vp, ks, vs, bt, sl, 16, dt, scale_dtype=torch.float32)
+    ref = qo.paged_attention(q, kp, vp, bt, sl, 16, dt, ks, vs, "contiguous")
+    assert qo.rel_err(got, ref) <= 1e-2
+    half = _run(q, kp, vp, ks, vs, bt, sl, 16, dt)
+    assert qo.rel_err(got, half) <= 1e-2
+
+
+def test_paged_attention_wave_kernel_matches_block_kernel(monkeypatch):
+    """The two MFMA kernels on the benchmark's attention shapes (14 / 2 heads, head 64,
+    INT8 cache with fp16 scales, blocks of 16), 2048 tokens: within the contract of each
+    other and of the oracle."""
+    seqs = [2048, 1999, 1024, 17]
+    q, kp, vp, ks, vs, bt, sl = _case(41, 4, 14, 2, 64, 16, seqs, True, "f16")
+    wave = _run(q, kp, vp, ks, vs, bt, sl, 16, "f16")
+    monkeypatch.setenv("LSQ_PAGED_KERNEL", "mfma")
+    block = _run(q, kp, vp, ks, vs, bt, sl, 16, "f16")
+    ref = qo.paged_attention(q, kp, vp, bt, sl, 16, "f16", ks, vs, "contiguous")
+    print(f"  wave {qo.rel_err(wave, ref):.2e} block {qo.rel_err(block, ref):.2e} "
+          f"wave-block {qo.rel_err(wave, block.astype(np.float64)):.2e}", flush=True)
+    assert qo.rel_err(wave, ref) <= 1e-2 and qo.rel_err(block, ref) <= 1e-2
