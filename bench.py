@@ -23,7 +23,8 @@ copy, see --calibrate-copy) and recorded in profiles/decode_int4_g128_m1_18944x3
 
 `sweep` reports the other shapes of the same metric (INT8 per-channel decode M in
 {1,8,32,64} at 18944x3584, INT4 group-128 decode M in {16,64}, INT4 group-128 prefill M in
-{256,2048,8192} at 14336x4096 in TFLOP/s, the single INT8 layer 4864x896 at M=1, INT4
+{256,2048,8192} at 14336x4096 in TFLOP/s, the single INT8 layer 4864x896 at M=1 (bf16 and
+fp32 activations), INT4 group-128 decode M=1 at 18944x3584 with fp32 activations, INT4
 decode M in {1,16} at the transposed 3584x18944 shape, W8A8 layers, the batch-32 decode
 step through the 168 INT4 projections of a Qwen2.5-0.5B-architecture stack, its MLPs, and
 paged attention). `cpu_baseline` times the reference's CPU path (dequantize, then
@@ -88,13 +89,13 @@ def make_int4(n: int, k: int, m: int, group: int = 128, x_dtype=torch.bfloat16, 
     return pack_int4(q), s, x
 
 
-def decode_bytes(kind: str, n: int, k: int, m: int, group: int = 128) -> int:
-    """Algorithmic bytes per call: W + scales + x + y (bf16 activations). W8A8 counts the
-    layer's own inputs and outputs the same way as INT8 (its int8 activation copy is an
-    intermediate)."""
+def decode_bytes(kind: str, n: int, k: int, m: int, group: int = 128, xb: int = 2) -> int:
+    """Algorithmic bytes per call: W + scales + x + y (xb bytes per activation / output:
+    2 for bf16, 4 for fp32). W8A8 counts the layer's own inputs and outputs the same way as
+    INT8 (its int8 activation copy is an intermediate)."""
     if kind in ("int8", "w8a8"):
-        return n * k + n * 4 + m * k * 2 + m * n * 2
-    return n * k // 2 + n * (-(-k // group)) * 2 + m * k * 2 + m * n * 2
+        return n * k + n * 4 + m * k * xb + m * n * xb
+    return n * k // 2 + n * (-(-k // group)) * 2 + m * k * xb + m * n * xb
 
 
 # ----------------------------------------------------------------------------- timing
@@ -225,26 +226,27 @@ def bench_floors(nbytes: int, steps: int, warmup: int, device) -> dict:
 
 
 def bench_decode(kind: str, n: int, k: int, m: int, steps: int, warmup: int, device, group=128,
-                 copies=None):
+                 copies=None, x_dtype=torch.bfloat16):
     """One layer shape timed over `steps` back-to-back launches; by default the launches
     rotate over enough weight copies to exceed the 256 MB Infinity Cache (every launch reads
-    HBM); copies=1 times the hot-cache case (one copy, resident in the Infinity Cache)."""
+    HBM); copies=1 times the hot-cache case (one copy, resident in the Infinity Cache).
+    x_dtype: the activation (and output) type."""
     if kind in ("int8", "w8a8"):
-        w, s, x = make_int8(n, k, m)
+        w, s, x = make_int8(n, k, m, x_dtype=x_dtype)
     else:
-        w, s, x = make_int4(n, k, m, group)
+        w, s, x = make_int4(n, k, m, group, x_dtype=x_dtype)
     wbytes = w.numel()
     copies = copies or copies_for(wbytes)
     layers = _layers(kind, w, s, group, copies, device)
     ms, lo, hi = time_layers(layers, x.to(device), steps, warmup)
-    nbytes = decode_bytes(kind, n, k, m, group)
+    nbytes = decode_bytes(kind, n, k, m, group, xb=4 if x_dtype == torch.float32 else 2)
     flops = 2.0 * m * n * k
     del layers
     torch.cuda.empty_cache()
     peak = MFMA_INT8_PEAK_TOPS if kind == "w8a8" else MFMA_BF16_PEAK_TF
     return {
         "kind": kind, "M": m, "N": n, "K": k, "group": None if kind in ("int8", "w8a8") else group,
-        "us_per_call": ms * 1e3, "us_range": [lo * 1e3, hi * 1e3], "GB_s": nbytes / (ms * 1e-3) / 1e9,
+        "x_dtype": str(x_dtype).replace("torch.", ""), "us_per_call": ms * 1e3, "us_range": [lo * 1e3, hi * 1e3], "GB_s": nbytes / (ms * 1e-3) / 1e9,
         "TFLOP_s": flops / (ms * 1e-3) / 1e12, "bytes": nbytes, "weight_copies": copies,
         "frac_hbm": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
         "frac_mfma": flops / (ms * 1e-3) / 1e12 / peak,
@@ -518,6 +520,10 @@ def main() -> int:
             sweep.append(bench_decode("int4", 14336, 4096, m, max(10, args.steps // 20),
                                       max(2, args.warmup // 4), device))
         sweep.append(bench_decode("int8", 4864, 896, 1, args.steps, args.warmup, device))
+        # fp32 activations (the reference's CPU type; config 1 allows them): config 1 and
+        # the headline shape
+        sweep.append(bench_decode("int8", 4864, 896, 1, args.steps, args.warmup, device, x_dtype=torch.float32))
+        sweep.append(bench_decode("int4", N, K, 1, args.steps, args.warmup, device, group=G, x_dtype=torch.float32))
         # the transposed (down-projection) shape, whose activations exceed LDS from 4 tokens
         for m in (1, 16):
             sweep.append(bench_decode("int4", K, N, m, args.steps, args.warmup, device))

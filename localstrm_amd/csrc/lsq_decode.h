@@ -74,9 +74,9 @@ int launch_split_merge(const float* part, int S, int64_t M, int64_t N, const voi
                        void* y, int64_t ldy, hipStream_t s);
 
 // Batched decode GEMV for 17..64 tokens on the tiled layouts of layers with ~1000+ row
-// tiles (lsq_bgemv.hip): whole row tiles per workgroup, K split over its waves, the
-// activations loaded into registers. Returns LSQ_E_LAYOUT without launching anything for
-// what it does not cover.
+// tiles (lsq_bgemv.hip): whole row tiles per workgroup, K split over its waves, each wave's
+// activations DMA'd into an LDS slab of its own. Returns LSQ_E_LAYOUT without launching
+// anything for what it does not cover.
 template <int DT>
 int launch_bgemv(int kind, const LinearArgs& a, hipStream_t s);
 
@@ -84,5 +84,11 @@ int launch_bgemv(int kind, const LinearArgs& a, hipStream_t s);
 // Same contract as launch_decode.
 template <int DT>
 int launch_decode_mb(int kind, const LinearArgs& a, hipStream_t s);
+
+// Decode GEMV for fp32 activations and outputs, 1..8 tokens, on the tiled layouts
+// (lsq_gemv32.hip): each weight formed as round_fp32(q * s), products summed with fmaf on
+// the VALU. Returns LSQ_E_LAYOUT without launching anything for what it does not cover
+// (canonical layouts, more tokens, activations or scales too large for LDS).
+int launch_gemv32(int kind, const LinearArgs& a, hipStream_t s);
 
 }  // namespace lsq

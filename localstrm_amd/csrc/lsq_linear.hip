@@ -6,6 +6,10 @@
 //
 //  * decode GEMV (lsq_gemv.hip): M <= 16 on the tiled layouts, whole row tiles per
 //    workgroup balanced over the grid;
+//  * batched decode GEMV (lsq_bgemv.hip): 17 <= M <= 64 on the tiled layouts of the larger
+//    layers;
+//  * fp32 decode GEMV (lsq_gemv32.hip): fp32 activations, M <= 8, tiled layouts, on the
+//    VALU with the reference's per-weight fp32 dequantization;
 //  * decode (lsq_decode_impl.h): M <= 64, fp16/bf16, K % 128 == 0, all activations staged in
 //    LDS once (the common decode case; up to 64 tokens when x fits in LDS);
 //  * chunked decode (lsq_decode_mb.hip): M <= 64 when x does not fit (large K, e.g. 4
@@ -13,7 +17,8 @@
 //  * prefill GEMM (lsq_gemm.hip): M > 64 (and the shapes above that fit neither decode),
 //    two MFMA kernels chosen by M;
 //  * generic kernel (below): any dtype / shape / group size, exact per-element dequant and
-//    fp32 FMA. Used for fp32 activations and shapes the fast kernels do not cover.
+//    fp32 FMA. Used for what the fast kernels do not cover (fp32 activations beyond 8
+//    tokens or on the canonical layouts, odd K or group sizes).
 
 #include <algorithm>
 
@@ -161,6 +166,13 @@ static int dispatch(bool w4, const void* x, int64_t ldx, const uint8_t* w, const
       if (rc == LSQ_E_LAYOUT && M <= 64) rc = launch_decode<DT>(kind, a, s);
       if (rc == LSQ_E_LAYOUT && M <= 64) rc = launch_decode_mb<DT>(kind, a, s);
       if (rc == LSQ_E_LAYOUT && M > 16) rc = launch_gemm<DT>(kind, a, s);
+      if (rc != LSQ_E_LAYOUT) return rc;
+    }
+  } else {
+    // fp32 activations, 1..8 tokens, tiled weights: the VALU decode GEMV
+    if (tiled && act == LSQ_ACT_NONE && K % kTileK == 0 && M >= 1 && M <= 8) {
+      LinearArgs a{x, ldx, tiled, scale, scale_dt, bias, bias_dt, y, ldy, M, N, K, group, ng};
+      const int rc = launch_gemv32(w4 ? kW4Tiled : kW8Tiled, a, s);
       if (rc != LSQ_E_LAYOUT) return rc;
     }
   }
