@@ -501,8 +501,11 @@ def main() -> int:
                                    fused=args.case == "mlp-fused")), flush=True)
         return 0
     if args.case:
-        kind, n, k, m = args.case.split(",")
-        r = bench_decode(kind, int(n), int(k), int(m), args.steps, args.warmup, device)
+        # kind,N,K,M[,f32]: one layer shape; a fifth field f32 times fp32 activations
+        parts = args.case.split(",")
+        kind, n, k, m = parts[:4]
+        xdt = torch.float32 if len(parts) > 4 and parts[4] == "f32" else torch.bfloat16
+        r = bench_decode(kind, int(n), int(k), int(m), args.steps, args.warmup, device, x_dtype=xdt)
         print(json.dumps(r), flush=True)
         return 0
 

@@ -44,6 +44,18 @@ __host__ __device__ inline G32Lds g32_lds(int64_t MT, int64_t K, int64_t rows, i
   return l;
 }
 
+// Byte J of v as a float (v_cvt_f32_ubyte J: the compiler otherwise extracts bytes 1-3
+// with a separate v_bfe_u32 each).
+template <int J>
+__device__ __forceinline__ float ubyte_f32(uint32_t v) {
+  float f;
+  if constexpr (J == 0) asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(f) : "v"(v));
+  else if constexpr (J == 1) asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(f) : "v"(v));
+  else if constexpr (J == 2) asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(f) : "v"(v));
+  else asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(f) : "v"(v));
+  return f;
+}
+
 template <bool W4, bool GROUPED, int MT, int W, int D>
 __global__ void __launch_bounds__(64 * W) gemv32_kernel(LinearArgs p) {
   constexpr int NT = 64 * W;
@@ -132,6 +144,7 @@ __global__ void __launch_bounds__(64 * W) gemv32_kernel(LinearArgs p) {
       issue(wbuf[s], i + D);
       if (live) {
         const float sc = (second ? srow_b : srow_a)[GROUPED ? (kt >> gshift) : 0];
+        const float c8 = -8.f * sc;  // exact
         const float* xk = xs + kt * kTileK + 32 * q;
         float part[MT];
 #pragma unroll
@@ -140,10 +153,19 @@ __global__ void __launch_bounds__(64 * W) gemv32_kernel(LinearArgs p) {
         for (int d = 0; d < 4; ++d) {  // 8 columns 32 q + 8 d .. +7 per step
           float wq[8];
           if constexpr (W4) {
+            // nibble p holds column 8 d + tiled_nibble_k(p); byte j of `lo` / `hi` is nibble
+            // 2 j / 2 j + 1 (v_cvt_f32_ubyte j). (u - 8) s = fma(u, s, -8 s) with one
+            // rounding: u s and -8 s are exact, so this is round_fp32((u - 8) s).
             const uint32_t wd = wv[0][d];
-#pragma unroll
-            for (int pp = 0; pp < 8; ++pp)  // nibble pp holds column 8 d + tiled_nibble_k(pp)
-              wq[tiled_nibble_k(pp)] = mul_rn(static_cast<float>(static_cast<int>((wd >> (4 * pp)) & 15u) - 8), sc);
+            const uint32_t lo = wd & 0x0F0F0F0Fu, hi = (wd >> 4) & 0x0F0F0F0Fu;
+            wq[tiled_nibble_k(0)] = fmaf(ubyte_f32<0>(lo), sc, c8);
+            wq[tiled_nibble_k(1)] = fmaf(ubyte_f32<0>(hi), sc, c8);
+            wq[tiled_nibble_k(2)] = fmaf(ubyte_f32<1>(lo), sc, c8);
+            wq[tiled_nibble_k(3)] = fmaf(ubyte_f32<1>(hi), sc, c8);
+            wq[tiled_nibble_k(4)] = fmaf(ubyte_f32<2>(lo), sc, c8);
+            wq[tiled_nibble_k(5)] = fmaf(ubyte_f32<2>(hi), sc, c8);
+            wq[tiled_nibble_k(6)] = fmaf(ubyte_f32<3>(lo), sc, c8);
+            wq[tiled_nibble_k(7)] = fmaf(ubyte_f32<3>(hi), sc, c8);
           } else {
             const uint32_t w0 = wv[d >> 1][2 * (d & 1)], w1 = wv[d >> 1][2 * (d & 1) + 1];
 #pragma unroll
