@@ -6,9 +6,9 @@
 // weight tiles it needs on chip (into MFMA operand registers, or into LDS) and feeds
 // bf16 / fp16 MFMA from there; the dequantized weight never exists in HBM.
 //
-// Two kernels. gemm_rw_kernel (register weights; the default, 128 x 128 tiles up to 768
-// tokens and 256 x 256 above) is described at its definition below. gemm_kernel (LDS
-// weights, LSQ_GEMM=lds) follows.
+// Two kernels. gemm_rw_kernel (register weights; the default, in tiles of 256 x 256,
+// 128 x 128, 64 x 128 or 64 x 64 chosen by how many workgroups each gives: rw_shape) is
+// described at its definition below. gemm_kernel (LDS weights, LSQ_GEMM=lds) follows.
 //
 // Tiling. A workgroup computes a 256 x 256 tile of y with 8 waves in a 2 x 4 layout (two
 // waves per SIMD, so one issues MFMAs while the other waits); each wave owns 128 x 64
@@ -713,32 +713,45 @@ int launch_rw_shape(const LinearArgs& a, hipStream_t s) {
   return static_cast<int>(hipGetLastError());
 }
 
-// Register-weight shapes: 0 = 128 x 128 tiles (4 waves of 128 x 32, two workgroups per
-// CU), 1 = 256 x 256 (8 waves of 256 x 32, one workgroup per CU).
+// Register-weight shapes (activation rows x weight rows per workgroup): 0 = 128 x 128
+// (4 waves of 128 x 32, two workgroups per CU), 1 = 256 x 256 (8 waves of 256 x 32, one
+// workgroup per CU), 2 = 64 x 128 (4 waves of 64 x 32), 3 = 64 x 64 (2 waves of 64 x 32).
 template <int DT, int KIND, bool GROUPED>
 int launch_rw(const LinearArgs& a, int shape, hipStream_t s) {
   if (shape == 1) return launch_rw_shape<DT, KIND, GROUPED, 1, 8, 512, 1>(a, s);
+  if (shape == 2) return launch_rw_shape<DT, KIND, GROUPED, 1, 2, 256, 4>(a, s);
+  if (shape == 3) return launch_rw_shape<DT, KIND, GROUPED, 1, 2, 128, 4>(a, s);
   return launch_rw_shape<DT, KIND, GROUPED, 1, 4, 256, 2>(a, s);
 }
 
-// Which prefill kernel. Up to 768 tokens the register-weight kernel with 128 x 128 tiles
-// (four times the workgroups of 256 x 256 tiles, which decides small M; 14336 x 4096
-// M=256: 55 us against 77 us with 128 x 256 tiles); above, the register-weight kernel
-// with 256 x 256 tiles: each weight is dequantized once per 256 activation rows, as in
-// the LDS-weight kernel, but never stored to LDS (14336 x 4096 INT4 g128, same box:
-// M=2048 244 -> 219 us, M=8192 ~945 -> 883 us). LSQ_GEMM=reg|wide|lds forces one (tests,
-// tuning). Returns the register-weight shape, or -1 for the LDS-weight kernel.
-int rw_shape(int64_t M) {
+// Which prefill kernel: the register-weight kernel with the largest tile that still gives
+// the GPU enough workgroups. 256 x 256 above 768 tokens when that makes 112+ tiles (each
+// weight dequantized once per 256 activation rows: 14336 x 4096 INT4 g128 M=2048 244 ->
+// 219 us, M=8192 ~945 -> 883 us against 128 x 128); else 128 x 128 when that makes 192+
+// tiles (14336 x 4096 M=256: 55 us against 77 with 128 x 256 tiles); else 64-row tiles,
+// 128 weight rows wide, or for INT4 64 wide once that still leaves fewer than 128 tiles
+// (measured, us, 128 x 128 -> chosen shape: 14336 x 4096 M=128 INT4 42.7 -> 34.7, INT8
+// 47.6 -> 31.8; 896 x 4864 M=256 INT4 46.3 -> 37.0, INT8 54.4 -> 34.6; 4864 x 896 M=128
+// INT4 14.9 -> 10.2; 3584 x 18944 M=256 INT4 168 -> 133, INT8 195 -> 121; 896 x 4864
+// M=2048 INT4 96 (256 x 256) -> 41). LSQ_GEMM=reg|wide|mid|small|lds forces 128 x 128,
+// 256 x 256, 64 x 128, 64 x 64 or the LDS-weight kernel (tests, tuning). Returns the
+// register-weight shape, or -1 for the LDS-weight kernel.
+int rw_shape(int64_t M, int64_t N, bool w4) {
   const char* e = std::getenv("LSQ_GEMM");
   if (e && e[0] == 'r') return 0;
   if (e && e[0] == 'w') return 1;
+  if (e && e[0] == 'm') return 2;
+  if (e && e[0] == 's') return 3;
   if (e && e[0] == 'l') return -1;
-  return M <= 768 ? 0 : 1;
+  auto tiles = [&](int64_t bm, int64_t bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
+  if (M > 768 && tiles(256, 256) >= 112) return 1;
+  if (tiles(128, 128) >= 192) return 0;
+  return w4 && tiles(64, 128) < 128 ? 3 : 2;
 }
 
 template <int DT, int KIND, bool GROUPED>
 int launch_kind(const LinearArgs& a, hipStream_t s) {
-  const int shape = rw_shape(a.M);
+  const int shape = rw_shape(a.M, a.N, KIND == kW4Tiled || KIND == kW4Canon);
   if (shape >= 0) return launch_rw<DT, KIND, GROUPED>(a, shape, s);
   auto kern = gemm_kernel<DT, KIND, GROUPED>;
   static std::atomic<int> attr_set{0};

@@ -270,17 +270,32 @@ def test_int4_g128_prefill_config_shape(m, layout, monkeypatch):
     assert err <= REL_TOL
 
 
-@pytest.mark.parametrize("variant", ["reg", "wide", "lds"])
+@pytest.mark.parametrize("variant", ["reg", "wide", "mid", "small", "lds"])
 @pytest.mark.parametrize("kind", ["int8", "int4"])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_gemm_edges_bias_and_dtypes(kind, dtype, variant, monkeypatch):
-    """Every prefill kernel (register weights with 128 x 128 and 256 x 256 tiles, LDS
-    weights) on ragged M and N edges (M=300, N=272 = 256 + 16), bias, both dtypes,
-    per-channel INT8, group-128 INT4, and per-channel INT4."""
+    """Every prefill kernel (register weights with 128 x 128, 256 x 256, 64 x 128 and
+    64 x 64 tiles, LDS weights) on ragged M and N edges (M=300, N=272 = 256 + 16), bias,
+    both dtypes, per-channel INT8, group-128 INT4, and per-channel INT4."""
     monkeypatch.setenv("LSQ_GEMM", variant)
     _check_layer(kind, 272, 512, 300, group=128, dtype=dtype, bias=True, seed=7)
     if kind == "int4":
         _check_layer("int4", 272, 512, 300, group=512, dtype=dtype, bias=True, seed=8)
+
+
+@pytest.mark.parametrize("layout", ["tiled", "canonical"])
+@pytest.mark.parametrize("kind", ["int8", "int4"])
+def test_gemm_tile_choice_small_n_layers(kind, layout, monkeypatch):
+    """The default tile choice on layers where 128 x 128 tiles leave most CUs idle (64-row
+    tiles: 128 or, for INT4 with few tiles, 64 weight rows wide; 256 x 256 only when it
+    still gives 112+ workgroups), against the oracle on sampled columns: Qwen2.5-0.5B
+    down_proj 896 x 4864 and gate_proj 4864 x 896, Qwen2.5-7B down_proj 3584 x 18944, and
+    14336 x 4096 at 96 tokens."""
+    monkeypatch.setenv("LSQ_WEIGHT_LAYOUT", layout)
+    for n, k, m in ((896, 4864, 65), (896, 4864, 1024), (4864, 896, 128), (4864, 896, 256),
+                    (3584, 18944, 128), (14336, 4096, 96)):
+        cols = np.arange(n) if n <= 1024 else np.sort(np.random.default_rng(n + m).choice(n, 512, replace=False))
+        _check_layer(kind, n, k, m, bias=(m % 2 == 1), seed=n + k + m, rows=cols)
 
 
 def test_int8_single_linear_config():
