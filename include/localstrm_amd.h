@@ -133,7 +133,9 @@ int lsq_w4_linear(const void* x, int64_t ldx, const uint8_t* weight_packed,
  * calls on down-projection-shaped layers split K over workgroups (4-16 tokens whose
  * activations exceed 96 KB on layers of at most 512 16-row tiles, e.g. 3584 x 18944;
  * 17-64 tokens on layers of at most 128 row tiles with 16+ 128-column tiles, e.g.
- * 896 x 4864): each slice's fp32 partial sums go to the workspace and a second kernel adds
+ * 896 x 4864), and so do prefill calls whose GEMM tiles would leave the GPU short of
+ * workgroups (small N, or long K: e.g. 896 x 4864 or 3584 x 18944 at 65-256 tokens):
+ * each slice's fp32 partial sums go to the workspace and a second kernel adds
  * them in slice order, adds the bias and rounds to T. With a smaller or NULL workspace
  * these calls behave exactly like the plain entry points. The workspace is scratch for
  * the duration of the call on `stream` (its contents are not read before being written). */

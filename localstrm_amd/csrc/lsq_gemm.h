@@ -15,4 +15,7 @@ namespace lsq {
 template <int DT>
 int launch_gemm(int kind, const LinearArgs& a, hipStream_t s);
 
+// Workspace bytes launch_gemm's split-K path needs for this shape (0: it does not split).
+int64_t gemm_split_bytes(int64_t M, int64_t N, int64_t K);
+
 }  // namespace lsq

@@ -34,6 +34,7 @@
 #include "lsq_internal.h"
 #include "lsq_gemm.h"
 
+#include <algorithm>
 #include <atomic>
 #include <cstdlib>
 
@@ -422,7 +423,9 @@ __global__ void __launch_bounds__(NT) gemm_kernel(LinearArgs p) {
 __host__ __device__ constexpr int rw_lds_bytes(int rbm) { return 3 * rbm * BK * 2; }
 
 // RFN_ 32-column blocks per wave, RFM_ 32-row blocks, RNT_ threads, MINB workgroups per CU.
-template <int DT, int KIND, bool GROUPED, int RFN_, int RFM_, int RNT_, int MINB>
+// SPLIT: workgroup b takes K slice b % p.ksplit of tile b / p.ksplit and writes its fp32
+// sums (per-channel scale applied, no bias) to p.part [ksplit][M][N] for the merge kernel.
+template <int DT, int KIND, bool GROUPED, int RFN_, int RFM_, int RNT_, int MINB, bool SPLIT>
 __global__ void __launch_bounds__(RNT_, MINB) gemm_rw_kernel(LinearArgs p) {
   constexpr int RFN = RFN_, RFM = RFM_, RNT = RNT_;
   constexpr int RBM = 32 * RFM;
@@ -434,7 +437,12 @@ __global__ void __launch_bounds__(RNT_, MINB) gemm_rw_kernel(LinearArgs p) {
   using S = typename Act<DT>::storage;
 
   const int M = static_cast<int>(p.M), N = static_cast<int>(p.N), K = static_cast<int>(p.K);
-  const int nsteps = K / BK;
+  // K slice: steps [st0, st0 + nsteps) of the layer's 64-column steps (all of them unsplit)
+  const int NS = SPLIT ? p.ksplit : 1;
+  const int tile = SPLIT ? static_cast<int>(blockIdx.x) / NS : static_cast<int>(blockIdx.x);
+  const int sl = SPLIT ? static_cast<int>(blockIdx.x) - tile * NS : 0;
+  const int st0 = sl * (K / BK) / NS;
+  const int nsteps = (sl + 1) * (K / BK) / NS - st0;
   const int nkt = K / kTileK;
   const int ng = static_cast<int>(p.ngroups);
   const int group = static_cast<int>(p.group);
@@ -446,12 +454,12 @@ __global__ void __launch_bounds__(RNT_, MINB) gemm_rw_kernel(LinearArgs p) {
   // order, so the ~32 workgroups resident on an XCD form a 4 x 8 block of tiles and, all
   // walking K in step, share each activation tile 8 ways and each weight tile 4 ways in
   // that XCD's L2 (when the grid does not divide so, M fastest as for 128-row tiles).
-  int mt = blockIdx.x % mtiles;
-  int nt = blockIdx.x / mtiles;
+  int mt = tile % mtiles;
+  int nt = tile / mtiles;
   const int ntiles = (N + RBN - 1) / RBN;
-  const bool blocked = RFM == 8 && mtiles % 4 == 0 && (mtiles * ntiles) % 8 == 0;
+  const bool blocked = !SPLIT && RFM == 8 && mtiles % 4 == 0 && (mtiles * ntiles) % 8 == 0;
   if (blocked) {
-    const int L = (blockIdx.x & 7) * (mtiles * ntiles / 8) + (blockIdx.x >> 3);
+    const int L = (tile & 7) * (mtiles * ntiles / 8) + (tile >> 3);
     const int r = L % (4 * ntiles);
     mt = 4 * (L / (4 * ntiles)) + (r & 3);
     nt = r >> 2;
@@ -472,7 +480,7 @@ __global__ void __launch_bounds__(RNT_, MINB) gemm_rw_kernel(LinearArgs p) {
   // for the blocked 256-row tiles, whose workgroups share tiles by walking K in step
   // (14336 x 4096 M=8192: 891 -> 792 us without it).
   const int rot = blocked ? 0 : (((blockIdx.x >> 3) & 31) * nsteps) >> 5;
-  auto gstep = [&](int st) { const int g = st + rot; return g >= nsteps ? g - nsteps : g; };
+  auto gstep = [&](int st) { const int g = st + rot; return st0 + (g >= nsteps ? g - nsteps : g); };
   // scale group of K step gs (group % 64 == 0): a shift for power-of-two groups, else a
   // division (uniform; the scalar unit is shared by the CU's waves)
   const int spg = group / BK;
@@ -689,17 +697,21 @@ __global__ void __launch_bounds__(RNT_, MINB) gemm_rw_kernel(LinearArgs p) {
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         const int m = m0 + 32 * i + 8 * (v >> 2) + 4 * h + (v & 3);
-        if (m < M && n < N)
-          y[static_cast<int64_t>(m) * p.ldy + n] = Act<DT>::from_f32(fmaf(acc[i][j][v], scn[j], bsn[j]));
+        if (m < M && n < N) {
+          if constexpr (SPLIT)  // this slice's scaled sum; the bias and the rounding come in the merge
+            p.part[(static_cast<int64_t>(sl) * M + m) * N + n] = acc[i][j][v] * scn[j];
+          else
+            y[static_cast<int64_t>(m) * p.ldy + n] = Act<DT>::from_f32(fmaf(acc[i][j][v], scn[j], bsn[j]));
+        }
       }
     }
 }
 
-template <int DT, int KIND, bool GROUPED, int RFN, int RFM, int RNT, int MINB>
+template <int DT, int KIND, bool GROUPED, int RFN, int RFM, int RNT, int MINB, bool SPLIT>
 int launch_rw_shape(const LinearArgs& a, hipStream_t s) {
   constexpr int rbm = 32 * RFM, rbn = (RNT / 64) * 32 * RFN;
-  const int64_t tiles = ((a.M + rbm - 1) / rbm) * ((a.N + rbn - 1) / rbn);
-  auto kern = gemm_rw_kernel<DT, KIND, GROUPED, RFN, RFM, RNT, MINB>;
+  const int64_t tiles = ((a.M + rbm - 1) / rbm) * ((a.N + rbn - 1) / rbn) * (SPLIT ? a.ksplit : 1);
+  auto kern = gemm_rw_kernel<DT, KIND, GROUPED, RFN, RFM, RNT, MINB, SPLIT>;
   if (rw_lds_bytes(rbm) > 64 * 1024) {
     static std::atomic<int> attr_set{0};
     if (!attr_set.load(std::memory_order_acquire)) {
@@ -716,12 +728,45 @@ int launch_rw_shape(const LinearArgs& a, hipStream_t s) {
 // Register-weight shapes (activation rows x weight rows per workgroup): 0 = 128 x 128
 // (4 waves of 128 x 32, two workgroups per CU), 1 = 256 x 256 (8 waves of 256 x 32, one
 // workgroup per CU), 2 = 64 x 128 (4 waves of 64 x 32), 3 = 64 x 64 (2 waves of 64 x 32).
-template <int DT, int KIND, bool GROUPED>
+template <int DT, int KIND, bool GROUPED, bool SPLIT>
 int launch_rw(const LinearArgs& a, int shape, hipStream_t s) {
-  if (shape == 1) return launch_rw_shape<DT, KIND, GROUPED, 1, 8, 512, 1>(a, s);
-  if (shape == 2) return launch_rw_shape<DT, KIND, GROUPED, 1, 2, 256, 4>(a, s);
-  if (shape == 3) return launch_rw_shape<DT, KIND, GROUPED, 1, 2, 128, 4>(a, s);
-  return launch_rw_shape<DT, KIND, GROUPED, 1, 4, 256, 2>(a, s);
+  if constexpr (!SPLIT) {  // (256 x 256 tiles are chosen only when they fill the GPU unsplit)
+    if (shape == 1) return launch_rw_shape<DT, KIND, GROUPED, 1, 8, 512, 1, false>(a, s);
+  }
+  if (shape == 2) return launch_rw_shape<DT, KIND, GROUPED, 1, 2, 256, 4, SPLIT>(a, s);
+  if (shape == 3) return launch_rw_shape<DT, KIND, GROUPED, 1, 2, 128, 4, SPLIT>(a, s);
+  return launch_rw_shape<DT, KIND, GROUPED, 1, 4, 256, 2, SPLIT>(a, s);
+}
+
+// Split-K plan for the register-weight kernel: when the chosen tile gives fewer than 128
+// workgroups, or fewer than 384 on a long K (128+ steps of 64 columns), K is cut into S
+// slices of at least 8 steps so that about 512 workgroups run, each slice's fp32 sums
+// going to the caller's workspace [S][M][N] and the ordered merge (launch_split_merge)
+// adding them, the bias and the rounding. Measured (us, unsplit -> split): 896 x 4864
+// INT4 M=65 36.0 -> 11.0, M=256 36.5 -> 17.2, INT8 M=256 34.1 -> 16.1; 3584 x 18944 INT4
+// M=128 130 -> 56, M=256 130 -> 91, INT8 M=128 117 -> 46; kept unsplit where it measured
+// slower: 14336 x 4096 M=128 (224 tiles of 64 steps) 38.3 vs 40.3, 896 x 4864 M=2048
+// 44.7 vs 47.1. LSQ_GEMM_SPLITK=0 turns it off, =n forces n slices (sweeps).
+struct GemmSplit {
+  int64_t S, bytes;
+};
+
+GemmSplit gemm_split_plan(int64_t M, int64_t N, int64_t K, int shape) {
+  GemmSplit sp{1, 0};
+  if (shape < 0 || shape == 1 || K % BK != 0) return sp;
+  const int64_t bm = shape == 0 ? 128 : 64, bn = shape == 3 ? 64 : 128;
+  const int64_t tiles = ((M + bm - 1) / bm) * ((N + bn - 1) / bn);
+  const int64_t steps = K / BK;
+  const char* e = std::getenv("LSQ_GEMM_SPLITK");
+  if (e && e[0] == '0') return sp;
+  const int64_t forced = e ? std::atoi(e) : 0;
+  const bool split = tiles < 128 || (tiles < 384 && steps >= 128);
+  int64_t S = forced >= 2 ? forced : (split ? (512 + tiles - 1) / tiles : 1);
+  S = std::min<int64_t>(S, std::min<int64_t>(16, steps / 8));
+  if (S < 2) return sp;
+  sp.S = S;
+  sp.bytes = S * M * N * 4;
+  return sp;
 }
 
 // Which prefill kernel: the register-weight kernel with the largest tile that still gives
@@ -752,7 +797,17 @@ int rw_shape(int64_t M, int64_t N, bool w4) {
 template <int DT, int KIND, bool GROUPED>
 int launch_kind(const LinearArgs& a, hipStream_t s) {
   const int shape = rw_shape(a.M, a.N, KIND == kW4Tiled || KIND == kW4Canon);
-  if (shape >= 0) return launch_rw<DT, KIND, GROUPED>(a, shape, s);
+  if (shape >= 0) {
+    const GemmSplit sp = gemm_split_plan(a.M, a.N, a.K, shape);
+    if (sp.S >= 2 && a.part && a.part_bytes >= sp.bytes) {
+      LinearArgs as = a;
+      as.ksplit = static_cast<int>(sp.S);
+      const int rc = launch_rw<DT, KIND, GROUPED, true>(as, shape, s);
+      if (rc != LSQ_OK) return rc;
+      return launch_split_merge<DT>(a.part, static_cast<int>(sp.S), a.M, a.N, a.bias, a.bias_dt, a.y, a.ldy, s);
+    }
+    return launch_rw<DT, KIND, GROUPED, false>(a, shape, s);
+  }
   auto kern = gemm_kernel<DT, KIND, GROUPED>;
   static std::atomic<int> attr_set{0};
   if (!attr_set.load(std::memory_order_acquire)) {
@@ -792,5 +847,12 @@ int launch_gemm(int kind, const LinearArgs& a, hipStream_t s) {
 
 template int launch_gemm<LSQ_BF16>(int, const LinearArgs&, hipStream_t);
 template int launch_gemm<LSQ_F16>(int, const LinearArgs&, hipStream_t);
+
+int64_t gemm_split_bytes(int64_t M, int64_t N, int64_t K) {
+  if (M <= 16) return 0;
+  int64_t b = 0;
+  for (const bool w4 : {false, true}) b = std::max(b, gemm_split_plan(M, N, K, rw_shape(M, N, w4)).bytes);
+  return b;
+}
 
 }  // namespace lsq

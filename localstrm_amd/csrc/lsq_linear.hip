@@ -326,7 +326,7 @@ extern "C" int lsq_w4_linear_ws(const void* x, int64_t ldx, const uint8_t* weigh
 
 extern "C" int64_t lsq_linear_workspace_bytes(int64_t M, int64_t N, int64_t K) {
   if (M < 0 || N < 0 || K < 0) return 0;
-  const int64_t b = std::max(gemv_split_bytes(M, N, K), bgemv_split_bytes(M, N, K));
+  const int64_t b = std::max({gemv_split_bytes(M, N, K), bgemv_split_bytes(M, N, K), gemm_split_bytes(M, N, K)});
   return (b + 255) / 256 * 256;
 }
 

@@ -298,6 +298,40 @@ def test_gemm_tile_choice_small_n_layers(kind, layout, monkeypatch):
         _check_layer(kind, n, k, m, bias=(m % 2 == 1), seed=n + k + m, rows=cols)
 
 
+@pytest.mark.parametrize("splits", ["2", "5", "16"])
+@pytest.mark.parametrize("variant", ["reg", "mid", "small"])
+@pytest.mark.parametrize("kind", ["int8", "int4"])
+def test_gemm_split_k_forced(kind, variant, splits, monkeypatch):
+    """The prefill GEMM's split-K form (K slices over workgroups, fp32 partial sums in the
+    module's workspace, ordered merge with the bias) with forced slice counts on every
+    tile shape it serves: ragged M and N (M=300, N=272), bias, group-128 and per-channel
+    INT4, per-channel INT8, both activation types; 16 slices of K = 8192 leave 8 steps
+    each."""
+    monkeypatch.setenv("LSQ_GEMM", variant)
+    monkeypatch.setenv("LSQ_GEMM_SPLITK", splits)
+    for dtype in (torch.bfloat16, torch.float16):
+        _check_layer(kind, 272, 8192, 300, group=128, dtype=dtype, bias=True, seed=int(splits))
+    if kind == "int4":
+        _check_layer("int4", 272, 8192, 300, group=8192, bias=True, seed=3)
+
+
+def test_gemm_split_k_deterministic_and_matches_unsplit(monkeypatch):
+    """Bit-identical on a second call; the unsplit kernel (LSQ_GEMM_SPLITK=0) within the
+    contract (the slices' sums are added in a different order)."""
+    w, s, x = bench.make_int4(3584, 18944, 128, 128, seed=5)
+    ql = _layer("int4", w, s, 18944, 128)
+    xd = x.to(DEV)
+    with torch.no_grad():
+        y1 = ql(xd).float().cpu().numpy()
+        y2 = ql(xd).float().cpu().numpy()
+        monkeypatch.setenv("LSQ_GEMM_SPLITK", "0")
+        y0 = ql(xd).float().cpu().numpy()
+    assert np.array_equal(y1.view(np.uint32), y2.view(np.uint32))
+    err = qo.rel_err(y1, y0.astype(np.float64))
+    _say(f"  split vs unsplit GEMM: rel={err:.3e}")
+    assert err <= REL_TOL
+
+
 def test_int8_single_linear_config():
     """Qwen2.5-0.5B gate_proj: W int8 [4864, 896], fp32 scale, x fp32 and bf16 [1, 896]."""
     for dtype in (torch.float32, torch.bfloat16):
