@@ -730,9 +730,7 @@ int launch_rw_shape(const LinearArgs& a, hipStream_t s) {
 // workgroup per CU), 2 = 64 x 128 (4 waves of 64 x 32), 3 = 64 x 64 (2 waves of 64 x 32).
 template <int DT, int KIND, bool GROUPED, bool SPLIT>
 int launch_rw(const LinearArgs& a, int shape, hipStream_t s) {
-  if constexpr (!SPLIT) {  // (256 x 256 tiles are chosen only when they fill the GPU unsplit)
-    if (shape == 1) return launch_rw_shape<DT, KIND, GROUPED, 1, 8, 512, 1, false>(a, s);
-  }
+  if (shape == 1) return launch_rw_shape<DT, KIND, GROUPED, 1, 8, 512, 1, SPLIT>(a, s);
   if (shape == 2) return launch_rw_shape<DT, KIND, GROUPED, 1, 2, 256, 4, SPLIT>(a, s);
   if (shape == 3) return launch_rw_shape<DT, KIND, GROUPED, 1, 2, 128, 4, SPLIT>(a, s);
   return launch_rw_shape<DT, KIND, GROUPED, 1, 4, 256, 2, SPLIT>(a, s);
@@ -740,7 +738,9 @@ int launch_rw(const LinearArgs& a, int shape, hipStream_t s) {
 
 // Split-K plan for the register-weight kernel: when the chosen tile gives fewer than 128
 // workgroups, or fewer than 384 on a long K (128+ steps of 64 columns), K is cut into S
-// slices of at least 8 steps so that about 512 workgroups run, each slice's fp32 sums
+// slices of at least 8 steps so that about 512 workgroups run (256 x 256 tiles, one
+// workgroup per CU: on a long K with fewer than 256 tiles, as many slices as fit one
+// round of 256 workgroups), each slice's fp32 sums
 // going to the caller's workspace [S][M][N] and the ordered merge (launch_split_merge)
 // adding them, the bias and the rounding. Measured (us, unsplit -> split): 896 x 4864
 // INT4 M=65 36.0 -> 11.0, M=256 36.5 -> 17.2, INT8 M=256 34.1 -> 16.1; 3584 x 18944 INT4
@@ -753,15 +753,21 @@ struct GemmSplit {
 
 GemmSplit gemm_split_plan(int64_t M, int64_t N, int64_t K, int shape) {
   GemmSplit sp{1, 0};
-  if (shape < 0 || shape == 1 || K % BK != 0) return sp;
-  const int64_t bm = shape == 0 ? 128 : 64, bn = shape == 3 ? 64 : 128;
+  if (shape < 0 || K % BK != 0) return sp;
+  const int64_t bm = shape == 1 ? 256 : (shape == 0 ? 128 : 64);
+  const int64_t bn = shape == 1 ? 256 : (shape == 3 ? 64 : 128);
   const int64_t tiles = ((M + bm - 1) / bm) * ((N + bn - 1) / bn);
   const int64_t steps = K / BK;
   const char* e = std::getenv("LSQ_GEMM_SPLITK");
   if (e && e[0] == '0') return sp;
   const int64_t forced = e ? std::atoi(e) : 0;
-  const bool split = tiles < 128 || (tiles < 384 && steps >= 128);
-  int64_t S = forced >= 2 ? forced : (split ? (512 + tiles - 1) / tiles : 1);
+  int64_t S = 1;
+  if (shape == 1) {  // one workgroup per CU: as many slices as keep the grid to one round
+    if (tiles < 256 && steps >= 128) S = 256 / tiles;
+  } else if (tiles < 128 || (tiles < 384 && steps >= 128)) {
+    S = (512 + tiles - 1) / tiles;
+  }
+  if (forced >= 2) S = forced;
   S = std::min<int64_t>(S, std::min<int64_t>(16, steps / 8));
   if (S < 2) return sp;
   sp.S = S;

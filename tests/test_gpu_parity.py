@@ -299,7 +299,7 @@ def test_gemm_tile_choice_small_n_layers(kind, layout, monkeypatch):
 
 
 @pytest.mark.parametrize("splits", ["2", "5", "16"])
-@pytest.mark.parametrize("variant", ["reg", "mid", "small"])
+@pytest.mark.parametrize("variant", ["reg", "wide", "mid", "small"])
 @pytest.mark.parametrize("kind", ["int8", "int4"])
 def test_gemm_split_k_forced(kind, variant, splits, monkeypatch):
     """The prefill GEMM's split-K form (K slices over workgroups, fp32 partial sums in the
@@ -315,10 +315,13 @@ def test_gemm_split_k_forced(kind, variant, splits, monkeypatch):
         _check_layer("int4", 272, 8192, 300, group=8192, bias=True, seed=3)
 
 
-def test_gemm_split_k_deterministic_and_matches_unsplit(monkeypatch):
-    """Bit-identical on a second call; the unsplit kernel (LSQ_GEMM_SPLITK=0) within the
-    contract (the slices' sums are added in a different order)."""
-    w, s, x = bench.make_int4(3584, 18944, 128, 128, seed=5)
+@pytest.mark.parametrize("m", [128, 2048])
+def test_gemm_split_k_deterministic_and_matches_unsplit(m, monkeypatch):
+    """Qwen2.5-7B down_proj 3584 x 18944 (split by default: 64 x 64 tiles at 128 tokens,
+    256 x 256 at 2048): bit-identical on a second call; the unsplit kernel
+    (LSQ_GEMM_SPLITK=0) within the contract (the slices' sums are added in another order);
+    the oracle on sampled columns and rows."""
+    w, s, x = bench.make_int4(3584, 18944, m, 128, seed=5)
     ql = _layer("int4", w, s, 18944, 128)
     xd = x.to(DEV)
     with torch.no_grad():
@@ -328,8 +331,14 @@ def test_gemm_split_k_deterministic_and_matches_unsplit(monkeypatch):
         y0 = ql(xd).float().cpu().numpy()
     assert np.array_equal(y1.view(np.uint32), y2.view(np.uint32))
     err = qo.rel_err(y1, y0.astype(np.float64))
-    _say(f"  split vs unsplit GEMM: rel={err:.3e}")
+    _say(f"  split vs unsplit GEMM M={m}: rel={err:.3e}")
     assert err <= REL_TOL
+    rng = np.random.default_rng(m)
+    cols = np.sort(rng.choice(3584, 128, replace=False))
+    rows = np.arange(m) if m <= 256 else np.sort(rng.choice(m, 128, replace=False))
+    wd = qo.dequant_int4(w[cols].numpy(), s[cols].float().numpy(), 18944, 128, "bf16")
+    ref = qo.linear_f64(x[rows].float().numpy(), wd, None, "bf16")
+    assert qo.rel_err(y1[np.ix_(rows, cols)], ref) <= REL_TOL
 
 
 def test_int8_single_linear_config():
