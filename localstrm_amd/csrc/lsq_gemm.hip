@@ -855,7 +855,7 @@ template int launch_gemm<LSQ_BF16>(int, const LinearArgs&, hipStream_t);
 template int launch_gemm<LSQ_F16>(int, const LinearArgs&, hipStream_t);
 
 int64_t gemm_split_bytes(int64_t M, int64_t N, int64_t K) {
-  if (M <= 16) return 0;
+  if (M <= 64) return 0;  // (the decode kernels take up to 64 tokens)
   int64_t b = 0;
   for (const bool w4 : {false, true}) b = std::max(b, gemm_split_plan(M, N, K, rw_shape(M, N, w4)).bytes);
   return b;
