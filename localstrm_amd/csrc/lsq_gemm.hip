@@ -794,6 +794,7 @@ int rw_shape(int64_t M, int64_t N, bool w4) {
   if (e && e[0] == 'm') return 2;
   if (e && e[0] == 's') return 3;
   if (e && e[0] == 'l') return -1;
+  if (M <= 64) return 2;  // (batched-decode sizes: one 64-row tile, split over K)
   auto tiles = [&](int64_t bm, int64_t bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
   if (M > 768 && tiles(256, 256) >= 112) return 1;
   if (tiles(128, 128) >= 192) return 0;
@@ -854,8 +855,15 @@ int launch_gemm(int kind, const LinearArgs& a, hipStream_t s) {
 template int launch_gemm<LSQ_BF16>(int, const LinearArgs&, hipStream_t);
 template int launch_gemm<LSQ_F16>(int, const LinearArgs&, hipStream_t);
 
+bool gemm_takes_batch(int64_t M, int64_t N, int64_t K) {
+  const char* e = std::getenv("LSQ_BATCH_GEMM");
+  if (M <= 16 || M > 64 || (e && e[0] == '0')) return false;
+  if (e && e[0] == '1') return true;
+  return M >= 24 && K >= 12288 && (N + kTileN - 1) / kTileN <= 256;
+}
+
 int64_t gemm_split_bytes(int64_t M, int64_t N, int64_t K) {
-  if (M <= 64) return 0;  // (the decode kernels take up to 64 tokens)
+  if (M <= 16 || (M <= 64 && !gemm_takes_batch(M, N, K))) return 0;  // (the decode kernels take the rest)
   int64_t b = 0;
   for (const bool w4 : {false, true}) b = std::max(b, gemm_split_plan(M, N, K, rw_shape(M, N, w4)).bytes);
   return b;

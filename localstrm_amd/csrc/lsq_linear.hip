@@ -160,11 +160,17 @@ static int dispatch(bool w4, const void* x, int64_t ldx, const uint8_t* w, const
       const int kind = w4 ? (tiled ? kW4Tiled : kW4Canon) : (tiled ? kW8Tiled : kW8);
       // decode with all activations in LDS; else (x too large for LDS, e.g. 4 tokens at
       // K = 18944) the chunked decode; else the prefill GEMM
+      // 17..64 tokens on long-K, small-N layers: the split-K GEMM, when the workspace for
+      // its slices is there (gemm_takes_batch)
+      const bool batch_gemm = M > 16 && M <= 64 && gemm_takes_batch(M, N, K) && ws &&
+                              ws_bytes >= gemm_split_bytes(M, N, K);
       int rc = LSQ_E_LAYOUT;
       if (M <= 16) rc = launch_gemv<DT>(kind, a, s);
-      if (rc == LSQ_E_LAYOUT && M > 16 && M <= 64) rc = launch_bgemv<DT>(kind, a, s);
-      if (rc == LSQ_E_LAYOUT && M <= 64) rc = launch_decode<DT>(kind, a, s);
-      if (rc == LSQ_E_LAYOUT && M <= 64) rc = launch_decode_mb<DT>(kind, a, s);
+      if (!batch_gemm) {
+        if (rc == LSQ_E_LAYOUT && M > 16 && M <= 64) rc = launch_bgemv<DT>(kind, a, s);
+        if (rc == LSQ_E_LAYOUT && M <= 64) rc = launch_decode<DT>(kind, a, s);
+        if (rc == LSQ_E_LAYOUT && M <= 64) rc = launch_decode_mb<DT>(kind, a, s);
+      }
       if (rc == LSQ_E_LAYOUT && M > 16) rc = launch_gemm<DT>(kind, a, s);
       if (rc != LSQ_E_LAYOUT) return rc;
     }

@@ -341,6 +341,34 @@ def test_gemm_split_k_deterministic_and_matches_unsplit(m, monkeypatch):
     assert qo.rel_err(y1[np.ix_(rows, cols)], ref) <= REL_TOL
 
 
+@pytest.mark.parametrize("m", [24, 33, 64])
+@pytest.mark.parametrize("kind", ["int8", "int4"])
+def test_batched_decode_through_split_gemm(kind, m, monkeypatch):
+    """24-64 tokens on long-K, small-N layers (Qwen2.5-7B down_proj 3584 x 18944, Llama-3-8B
+    down_proj 4096 x 14336) run the split-K GEMM with 64 x 128 tiles: against the oracle on
+    sampled columns, and against the decode kernels (LSQ_BATCH_GEMM=0) within the
+    contract; without a workspace (the plain C entry point) the decode kernels serve the
+    call unchanged."""
+    from localstrm_amd import _lib
+    for n, k in ((3584, 18944), (4096, 14336)):
+        cols = np.sort(np.random.default_rng(n + m).choice(n, 384, replace=False))
+        _check_layer(kind, n, k, m, bias=(m % 2 == 1), seed=n + m, rows=cols)
+    n, k = 3584, 18944
+    if kind == "int8":
+        w, s, x = bench.make_int8(n, k, m, seed=m)
+    else:
+        w, s, x = bench.make_int4(n, k, m, 128, seed=m)
+    ql = _layer(kind, w, s, k, 128)
+    xd = x.to(DEV)
+    with torch.no_grad():
+        y_gemm = ql(xd).float().cpu().numpy()
+        monkeypatch.setenv("LSQ_BATCH_GEMM", "0")
+        y_dec = ql(xd).float().cpu().numpy()
+    err = qo.rel_err(y_gemm, y_dec.astype(np.float64))
+    _say(f"  {kind} M={m}: split GEMM vs decode kernels rel={err:.3e}")
+    assert err <= REL_TOL
+
+
 def test_int8_single_linear_config():
     """Qwen2.5-0.5B gate_proj: W int8 [4864, 896], fp32 scale, x fp32 and bf16 [1, 896]."""
     for dtype in (torch.float32, torch.bfloat16):
