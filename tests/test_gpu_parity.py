@@ -369,6 +369,54 @@ def test_batched_decode_through_split_gemm(kind, m, monkeypatch):
     assert err <= REL_TOL
 
 
+@pytest.mark.parametrize("kind", ["int8", "int4"])
+def test_gemm_split_k_canonical_layout_through_c_abi(kind, monkeypatch):
+    """The split-K GEMM reading the canonical layouts (int8 [N, K], packed INT4 [N, K/2]:
+    what a C caller passes without building the tiled copy) with a workspace, forced and by
+    default (896 x 4864 at 256 tokens splits), against the oracle and against the plain
+    entry point (no workspace: unsplit)."""
+    from localstrm_amd import _lib
+    lib = _lib.load()
+    n, k, m = 896, 4864, 256
+    if kind == "int8":
+        w, s, x = bench.make_int8(n, k, m, seed=3)
+    else:
+        w, s, x = bench.make_int4(n, k, m, 128, seed=3)
+    wd_, sd, xd = w.to(DEV), s.to(DEV), x.to(DEV)
+    b = torch.randn(n, generator=torch.Generator().manual_seed(4)).to(torch.bfloat16)
+    bd = b.to(DEV)
+    stream = _lib.stream_handle(DEV)
+
+    def call(ws, nbytes):
+        y = torch.empty(m, n, dtype=torch.bfloat16, device=DEV)
+        if kind == "int8":
+            args = (xd.data_ptr(), k, wd_.data_ptr(), None, sd.data_ptr(), _lib.dtype_code(sd.dtype),
+                    bd.data_ptr(), _lib.dtype_code(bd.dtype), y.data_ptr(), n, _lib.dtype_code(torch.bfloat16), m, n, k)
+            rc = lib.lsq_w8_linear_ws(*args, _lib.ptr(ws), nbytes, stream) if ws is not False else lib.lsq_w8_linear(*args, stream)
+        else:
+            args = (xd.data_ptr(), k, wd_.data_ptr(), None, sd.data_ptr(), _lib.dtype_code(sd.dtype), 128,
+                    bd.data_ptr(), _lib.dtype_code(bd.dtype), y.data_ptr(), n, _lib.dtype_code(torch.bfloat16), m, n, k)
+            rc = lib.lsq_w4_linear_ws(*args, _lib.ptr(ws), nbytes, stream) if ws is not False else lib.lsq_w4_linear(*args, stream)
+        _lib.check(rc, "linear_ws")
+        return y.float().cpu().numpy()
+
+    wdq = qo.dequant_int8(w.numpy(), s.numpy(), "bf16") if kind == "int8" else qo.dequant_int4(w.numpy(), s.float().numpy(), k, 128, "bf16")
+    ref = qo.linear_f64(x.float().numpy(), wdq, b.float().numpy(), "bf16")
+    plain = call(False, 0)
+    assert qo.rel_err(plain, ref) <= REL_TOL
+    for forced in (None, "3", "9"):
+        if forced:
+            monkeypatch.setenv("LSQ_GEMM_SPLITK", forced)
+        nws = lib.lsq_linear_workspace_bytes(m, n, k)
+        assert nws > 0
+        ws = torch.empty(nws, dtype=torch.uint8, device=DEV)
+        got = call(ws, nws)
+        err = qo.rel_err(got, ref)
+        _say(f"  {kind} canonical split={forced or 'default'}: rel_err={err:.3e}")
+        assert err <= REL_TOL
+        assert qo.rel_err(got, plain.astype(np.float64)) <= REL_TOL
+
+
 def test_int8_single_linear_config():
     """Qwen2.5-0.5B gate_proj: W int8 [4864, 896], fp32 scale, x fp32 and bf16 [1, 896]."""
     for dtype in (torch.float32, torch.bfloat16):
