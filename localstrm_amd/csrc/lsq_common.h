@@ -179,6 +179,40 @@ __device__ __forceinline__ uint32_t bload4(rsrc_t r, uint32_t off) {
   return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
 }
 
+// Buffer loads into LDS (buffer_load_dwordx4 ... lds: 16 bytes per lane, lane l's bytes
+// at the wave's LDS address + 16 l) that the compiler does not see. Through the builtin,
+// every LDS read after such a load waits for it to land (the compiler cannot tell which
+// LDS bytes it writes), so a DMA issued several pipeline steps ahead is drained at the
+// next step. Written as assembly the load is invisible to that analysis; the caller
+// waits for it itself (s_waitcnt vmcnt with an exact count) before the barrier that
+// publishes the data, and keeps it out of the LDS it reads meanwhile. The compiler's
+// own vmcnt waits stay correct: loads it does not know of only make them wait longer.
+using rsrc4_t = int __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ rsrc4_t make_rsrc4(const void* base, uint32_t bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  return rsrc4_t{static_cast<int>(static_cast<uint32_t>(a)), static_cast<int>((a >> 32) & 0xFFFFu),
+                 static_cast<int>(bytes), kRsrcWord3};
+}
+
+// M0 holds the LDS address. The compiler reserves M0 and warns about the clobber; the
+// kernels using this helper have no other M0 use (they issue no builtin LDS DMA, GWS or
+// LDS-parameter instruction), so nothing live is lost.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma16_async(rsrc4_t r, void* lds, uint32_t voff, uint32_t soff) {
+  const uint32_t m0 = static_cast<uint32_t>(
+      reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) void*)lds));
+  asm volatile(
+      "s_mov_b32 m0, %3\n\t"
+      "s_nop 0\n\t"
+      "buffer_load_dwordx4 %0, %1, %2 offen lds"
+      :
+      : "v"(voff), "s"(r), "s"(soff), "s"(m0)
+      : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
 // Workgroup barrier that orders LDS only: the compiler's __syncthreads() also waits for
 // every outstanding global load, which would drain the weight pipeline.
 __device__ __forceinline__ void lds_barrier() {

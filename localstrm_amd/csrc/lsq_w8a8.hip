@@ -175,19 +175,21 @@ __global__ void w8a8_untile_kernel(const int8_t* __restrict__ tiled, int8_t* __r
 //
 // A workgroup computes a 256 x 256 tile of y with 8 waves in a 2 x 4 layout; each wave
 // owns 128 x 64 outputs as 4 x 2 blocks of v_mfma_i32_32x32x32_i8 (int32 accumulators).
-// K advances 128 columns (one k tile) per step; the x_q tile [256, 128] and the weight
-// tile [256 rows, 128] both go from HBM / L2 into LDS with buffer_load ... lds, one step
-// ahead, double-buffered, one barrier per step. Both LDS tiles store row r's 16-byte
-// chunk c at position c ^ ((r >> 1) & 7), so the 16-byte MFMA operand reads (16 rows at
-// one chunk) spread over all 64 banks. Consecutive workgroups take consecutive M tiles of
-// one N tile (they share its weights in L2), and each starts at a different k step
-// (K rotation) so that the ~32 workgroups resident on one XCD do not all miss on the
-// same activation tile at once; the int32 sums do not depend on the order.
-constexpr int QBM = 256, QBN = 256, QBK = 128, QNT = 512;
+// K advances BK columns per step; the x_q tile [256, BK] and the weight tile [256 rows,
+// BK] both go from HBM / L2 into LDS with buffer_load ... lds into NST stages, the DMA
+// NST - 1 steps ahead, one barrier per step. The barrier sits before the step's last
+// sub-step of MFMAs: right after it the next step's first operands are read from the
+// next stage while those MFMAs run, so the MFMA pipe does not drain at the barrier. Both
+// LDS tiles store row r's 16-byte chunk c at position c ^ ((r / (256 / BK)) % (BK / 16)),
+// so the 16-byte MFMA operand reads (16 rows at one chunk) spread over all 64 banks.
+// Consecutive workgroups take consecutive M tiles of one N tile (they share its weights
+// in L2), and, unless the blocked order below applies, each starts at a different k step
+// (K rotation) so that the ~32 workgroups resident on one XCD do not all miss on the same
+// activation tile at once; the int32 sums do not depend on the order.
+constexpr int QBM = 256, QBN = 256, QNT = 512;
 constexpr int QWTM = 128, QWTN = 64;
 constexpr int QFM = QWTM / 32, QFN = QWTN / 32;
-constexpr int kQTile = QBM * QBK;     // bytes of one operand tile
-constexpr int kQLds = 4 * kQTile;     // {x, w} x 2 stages
+__host__ __device__ constexpr int w8a8_lds(int bk, int nst) { return nst * 2 * QBM * bk; }
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x16 __attribute__((ext_vector_type(16)));
@@ -197,12 +199,25 @@ __device__ __forceinline__ i32x16 mma32_i8(u32x4 a, u32x4 b, i32x16 c) {
                                                __builtin_bit_cast(i32x4, b), c, 0, 0, 0);
 }
 
-template <int DT>
+// s_waitcnt immediate: vmcnt(n), lgkmcnt(0) (expcnt left alone)
+__host__ __device__ constexpr int wait_vm(int n) { return (n & 15) | (7 << 4) | ((n >> 4) << 14); }
+
+template <int DT, int BK, int NST>
 __global__ void __launch_bounds__(QNT) w8a8_gemm_kernel(LinearArgs p) {
+  static_assert(BK == 64 || BK == 128, "k step of 64 or 128 columns");
+  static_assert(NST >= 2 && NST <= 4, "2..4 LDS stages");
+  constexpr int A = NST - 1;         // steps the DMA runs ahead
+  constexpr int KK = BK / 32;        // MFMA sub-steps per step
+  constexpr int CPR = BK / 16;       // 16-byte chunks per tile row
+  constexpr int RPL = 256 / BK;      // tile rows per 256 bytes (one pass over the 64 banks)
+  constexpr int RPI = 1024 / BK;     // tile rows one DMA instruction fills (1 KB)
+  constexpr int kTile = QBM * BK;    // bytes of one operand tile
+  constexpr int kB = QBM / RPI / (QNT / 64);  // DMA instructions per wave per operand and step
   extern __shared__ __align__(16) unsigned char smem[];
   using S = typename Act<DT>::storage;
   const int M = static_cast<int>(p.M), N = static_cast<int>(p.N), K = static_cast<int>(p.K);
-  const int nsteps = K / QBK;  // one k tile per step
+  const int nsteps = K / BK;
+  const int nkt = K / kTileK;  // k tiles of the weight layout
   const int mtiles = (M + QBM - 1) / QBM;
   // Tile order as in the weight-only prefill GEMM (lsq_gemm.hip, gemm_rw_kernel): groups
   // of 4 M tiles, XCD x (workgroups are dealt to the 8 XCDs round-robin) taking the x-th
@@ -227,43 +242,47 @@ __global__ void __launch_bounds__(QNT) w8a8_gemm_kernel(LinearArgs p) {
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wid & 1, wn = wid >> 1;
   const int rot = blocked ? 0 : (((blockIdx.x >> 3) & 31) * nsteps) >> 5;
-  auto gstep = [&](int st) { const int g = st + rot; return g >= nsteps ? g - nsteps : g; };
-  auto xs_at = [&](int buf) { return smem + buf * kQTile; };
-  auto ws_at = [&](int buf) { return smem + (2 + buf) * kQTile; };
+  // k step of pipeline step st; steps past the end repeat the last one (their stage is
+  // never read), so every wave issues the same DMAs in every step and waits exact counts
+  auto gstep = [&](int st) {
+    const int g = min(st, nsteps - 1) + rot;
+    return g >= nsteps ? g - nsteps : g;
+  };
+  auto xs_at = [&](int buf) { return smem + buf * 2 * kTile; };
+  auto ws_at = [&](int buf) { return smem + buf * 2 * kTile + kTile; };
+  auto swz = [](int r) { return (r / RPL) & (CPR - 1); };
 
   // ---- descriptors: rows past M and row tiles past N read zeros (the row part of every
   // offset is in the range-checked per-lane offset; the scalar offset carries the k step)
-  const rsrc_t rx = make_rsrc(static_cast<const int8_t*>(p.x) + static_cast<int64_t>(m0) * p.ldx,
-                              static_cast<uint32_t>((rows_m - 1) * p.ldx + K));
+  const rsrc4_t rx = make_rsrc4(static_cast<const int8_t*>(p.x) + static_cast<int64_t>(m0) * p.ldx,
+                                static_cast<uint32_t>((rows_m - 1) * p.ldx + K));
   const int rt0 = n0 / kTileN;
   const int nrt = (N + kTileN - 1) / kTileN;
-  const rsrc_t rw = make_rsrc(p.w + static_cast<int64_t>(rt0) * nsteps * kTileBytes8,
-                              static_cast<uint32_t>(min(QBN / kTileN, nrt - rt0) * nsteps * kTileBytes8));
+  const rsrc4_t rw = make_rsrc4(p.w + static_cast<int64_t>(rt0) * nkt * kTileBytes8,
+                                static_cast<uint32_t>(min(QBN / kTileN, nrt - rt0) * nkt * kTileBytes8));
 
-  // One wave DMA instruction fills 8 rows of a tile (1 KB): lane l writes row
-  // rb + (l >> 3), position l & 7, i.e. chunk (l & 7) ^ ((b & 1) << 2 | (l >> 4)).
-  constexpr int kB = QBM / 8 / (QNT / 64);  // 4 row blocks of 8 per wave per operand
+  // One wave DMA instruction fills RPI rows of a tile (1 KB): lane l writes row
+  // rb + l / CPR at position l % CPR, i.e. chunk (l % CPR) ^ swz(row). A tiled weight row
+  // r's 16-byte chunk of k tile columns 16 c' .. +15 is lane (r & 15) + 16 (c' >> 1) of
+  // half (c' & 1) of its 2 KB tile; a step starting at column k0 % 128 of its k tile adds
+  // 16 lanes (256 bytes) per 32 columns of that start, through the scalar offset.
   uint32_t xo[kB], wo[kB];
 #pragma unroll
   for (int b = 0; b < kB; ++b) {
-    const int r = (wid * kB + b) * 8 + (lane >> 3);
-    const int c = (lane & 7) ^ (((b & 1) << 2) | (lane >> 4));
+    const int r = (wid * kB + b) * RPI + lane / CPR;
+    const int c = (lane % CPR) ^ swz(r);
     xo[b] = static_cast<uint32_t>(r * p.ldx + c * 16);
-    // tiled weights: row r is lane (r & 15) + 16 (c >> 1) of half (c & 1) of its tile
-    wo[b] = static_cast<uint32_t>((r >> 4) * nsteps * kTileBytes8 + (c & 1) * (kTileBytes8 / 2) +
+    wo[b] = static_cast<uint32_t>((r >> 4) * nkt * kTileBytes8 + (c & 1) * (kTileBytes8 / 2) +
                                   ((r & 15) + 16 * (c >> 1)) * 16);
   }
   auto issue = [&](int st, int buf) {
-    const int g = gstep(st);
+    const int k0 = gstep(st) * BK;
+    const int sw = (k0 >> 7) * kTileBytes8 + ((k0 & 127) >> 5) * 256;
 #pragma unroll
     for (int b = 0; b < kB; ++b) {
-      const int rb = (wid * kB + b) * 8;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          rx, (__attribute__((address_space(3))) void*)(xs_at(buf) + rb * QBK), 16, xo[b],
-          g * QBK, 0, 0);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          rw, (__attribute__((address_space(3))) void*)(ws_at(buf) + rb * QBK), 16, wo[b],
-          g * kTileBytes8, 0, 0);
+      const int rb = (wid * kB + b) * RPI;
+      dma16_async(rx, xs_at(buf) + rb * BK, xo[b], static_cast<uint32_t>(k0));
+      dma16_async(rw, ws_at(buf) + rb * BK, wo[b], static_cast<uint32_t>(sw));
     }
   };
 
@@ -275,44 +294,52 @@ __global__ void __launch_bounds__(QNT) w8a8_gemm_kernel(LinearArgs p) {
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0;
   // MFMA operands: lane l reads row (l & 31) of a 32-row block, 16 columns at
-  // 32 kk + 16 (l >> 5), i.e. chunk 2 kk + (l >> 5), through the swizzle.
+  // 32 kk + 16 (l >> 5), i.e. chunk 2 kk + (l >> 5), through the swizzle (32-row blocks
+  // keep swz: 32 is a multiple of RPL * CPR).
   const int frow = lane & 31;
-  auto frag_off = [&](int kk) {
-    return frow * QBK + (((2 * kk + (lane >> 5)) ^ ((frow >> 1) & 7)) << 4);
+  auto frag_off = [&](int kk) { return frow * BK + (((2 * kk + (lane >> 5)) ^ swz(frow)) << 4); };
+  u32x4 a[2][QFM], b[2][QFN];
+  auto load = [&](int buf, int kk, u32x4 (&aa)[QFM], u32x4 (&bb)[QFN]) {
+    const unsigned char* xb = xs_at(buf) + wm * QWTM * BK;
+    const unsigned char* wb = ws_at(buf) + wn * QWTN * BK;
+    const int off = frag_off(kk);
+#pragma unroll
+    for (int i = 0; i < QFM; ++i) aa[i] = *reinterpret_cast<const u32x4*>(xb + 32 * i * BK + off);
+#pragma unroll
+    for (int j = 0; j < QFN; ++j) bb[j] = *reinterpret_cast<const u32x4*>(wb + 32 * j * BK + off);
   };
-  auto compute = [&](int buf) {
-    const unsigned char* xb = xs_at(buf) + wm * QWTM * QBK;
-    const unsigned char* wb = ws_at(buf) + wn * QWTN * QBK;
-    u32x4 a[2][QFM], b[2][QFN];
-    auto load = [&](int kk, u32x4 (&aa)[QFM], u32x4 (&bb)[QFN]) {
-      const int off = frag_off(kk);
+
+  // prologue: steps 0 .. A-1 in flight, step 0 landed
 #pragma unroll
-      for (int i = 0; i < QFM; ++i) aa[i] = *reinterpret_cast<const u32x4*>(xb + 32 * i * QBK + off);
+  for (int st = 0; st < A; ++st) issue(st, st);
+  __builtin_amdgcn_s_waitcnt(wait_vm((A - 1) * 2 * kB));
+  lds_barrier();
+  load(0, 0, a[0], b[0]);
+  for (int st = 0; st < nsteps; ++st) {
+    const int buf = st % NST;
+    // into the stage read in step st - 1 (all its reads completed before that step's
+    // barrier)
+    issue(st + A, (st + A) % NST);
 #pragma unroll
-      for (int j = 0; j < QFN; ++j) bb[j] = *reinterpret_cast<const u32x4*>(wb + 32 * j * QBK + off);
-    };
-    load(0, a[0], b[0]);
-#pragma unroll
-    for (int kk = 0; kk < QBK / 32; ++kk) {
-      if (kk + 1 < QBK / 32) load(kk + 1, a[(kk + 1) & 1], b[(kk + 1) & 1]);
+    for (int kk = 0; kk < KK; ++kk) {
+      if (kk + 1 < KK) {
+        load(buf, kk + 1, a[(kk + 1) & 1], b[(kk + 1) & 1]);
+      } else {
+        // step st + 1 landed (steps st + 2 .. st + A stay in flight), every wave's reads
+        // of this stage done; then the next step's first operands
+        __builtin_amdgcn_s_waitcnt(wait_vm((A - 1) * 2 * kB));
+        lds_barrier();
+        load((st + 1) % NST, 0, a[(kk + 1) & 1], b[(kk + 1) & 1]);
+      }
 #pragma unroll
       for (int i = 0; i < QFM; ++i)
 #pragma unroll
         for (int j = 0; j < QFN; ++j) acc[i][j] = mma32_i8(a[kk & 1][i], b[kk & 1][j], acc[i][j]);
     }
-  };
-
-  constexpr int kWaitAll = (7 << 4);  // vmcnt(0) lgkmcnt(0)
-  issue(0, 0);
-  __builtin_amdgcn_s_waitcnt(kWaitAll);
-  lds_barrier();
-  for (int st = 0; st < nsteps; ++st) {
-    const int buf = st & 1;
-    if (st + 1 < nsteps) issue(st + 1, buf ^ 1);  // into the stage read one step ago
-    compute(buf);
-    __builtin_amdgcn_s_waitcnt(kWaitAll);
-    lds_barrier();
   }
+  // the DMAs of steps past the end may still be writing their stages
+  __builtin_amdgcn_s_waitcnt(wait_vm(0));
+  lds_barrier();
 
   // ---- epilogue: y = fp32(acc) * (sx[m] * sw[n]) [+ fp32(bias[n])], rounded to T
   float* sxs = reinterpret_cast<float*>(smem);  // the tile's token scales (LDS is free now)
@@ -358,24 +385,37 @@ int max_lds_q() {
   return v;
 }
 
-template <int DT>
-int launch_w8a8_gemm(const LinearArgs& a, hipStream_t s) {
-  if (a.K % QBK != 0 || a.K < QBK || !a.xscale) return LSQ_E_LAYOUT;
-  if (kQLds > max_lds_q()) return LSQ_E_LAYOUT;
-  if ((a.M - 1) * a.ldx + a.K >= (int64_t(1) << 31) || (a.ldx % 16) != 0) return LSQ_E_LAYOUT;
-  if (int64_t(QBN / kTileN) * a.K * kTileN >= (int64_t(1) << 31)) return LSQ_E_LAYOUT;
-  auto kern = w8a8_gemm_kernel<DT>;
+template <int DT, int BK, int NST>
+int launch_w8a8_gemm_as(const LinearArgs& a, hipStream_t s) {
+  constexpr int lds = w8a8_lds(BK, NST);
+  if (lds > max_lds_q()) return LSQ_E_LAYOUT;
+  auto kern = w8a8_gemm_kernel<DT, BK, NST>;
   static std::atomic<int> attr_set{0};
   if (!attr_set.load(std::memory_order_acquire)) {
     const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                             hipFuncAttributeMaxDynamicSharedMemorySize, kQLds);
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, lds);
     if (e != hipSuccess) return static_cast<int>(e);
     attr_set.store(1, std::memory_order_release);
   }
   const int64_t tiles = ((a.M + QBM - 1) / QBM) * ((a.N + QBN - 1) / QBN);
   if (tiles > INT32_MAX) return LSQ_E_SHAPE;
-  kern<<<dim3(static_cast<unsigned>(tiles)), dim3(QNT), kQLds, s>>>(a);
+  kern<<<dim3(static_cast<unsigned>(tiles)), dim3(QNT), lds, s>>>(a);
   return static_cast<int>(hipGetLastError());
+}
+
+template <int DT>
+int launch_w8a8_gemm(const LinearArgs& a, hipStream_t s) {
+  if (a.K % kTileK != 0 || a.K < kTileK || !a.xscale) return LSQ_E_LAYOUT;
+  if ((a.M - 1) * a.ldx + a.K >= (int64_t(1) << 31) || (a.ldx % 16) != 0) return LSQ_E_LAYOUT;
+  if (int64_t(QBN / kTileN) * a.K * kTileN >= (int64_t(1) << 31)) return LSQ_E_LAYOUT;
+  // LSQ_W8A8_GEMM=1: 128-column steps, two stages; =2: 64-column steps, three stages
+  // (tests, comparisons). Default 64 columns, four stages: M=2048 at 14336 x 4096
+  // 157 -> 145 us against the first, M=8192 543 -> 506 us; three stages measured the same.
+  const char* e = std::getenv("LSQ_W8A8_GEMM");
+  const int v = e ? std::atoi(e) : 0;
+  if (v == 1) return launch_w8a8_gemm_as<DT, 128, 2>(a, s);
+  if (v == 2) return launch_w8a8_gemm_as<DT, 64, 3>(a, s);
+  return launch_w8a8_gemm_as<DT, 64, 4>(a, s);
 }
 
 // LSQ_W8A8_PATH selects a path for comparisons and tests: "gemm" sends every M to the

@@ -301,6 +301,23 @@ def test_w8a8_gemm_kernel_on_decode_shapes(monkeypatch, m, n, k):
     assert torch.equal(y_dec.view(torch.int16), y_gemm.view(torch.int16))
 
 
+@pytest.mark.parametrize("variant", ["1", "2", "0"])
+@pytest.mark.parametrize("m,n,k", [(65, 520, 1024), (257, 136, 64), (300, 264, 256), (1024, 2048, 640)])
+def test_w8a8_gemm_pipeline_depths(monkeypatch, variant, m, n, k):
+    # The prefill GEMM's k step and LDS stages (LSQ_W8A8_GEMM: 1 = 128 columns, 2 stages;
+    # 2 = 64 columns, 3 stages; 0 = the default, 64 columns, 4 stages), bit-exact against
+    # the oracle: the XCD-blocked tile order (1024 x 2048: 4 x 8 tiles) and the plain one,
+    # K of 1 to 8 k tiles (fewer steps than the pipeline holds, at K = 64 and 256).
+    _say(f"w8a8 gemm pipeline {variant} M={m} N={n} K={k}")
+    monkeypatch.setenv("LSQ_W8A8_GEMM", variant)
+    x, wq, sw, bias = _lin_inputs("bf16", m, n, k)
+    y, _, _ = _linear(x.to(DEV), wq, sw, bias, monkeypatch, "gemm")
+    ref = qo.w8a8_linear(x.float().numpy(), wq.numpy(), sw.numpy(),
+                         None if bias is None else bias.float().numpy(), "bf16")
+    mism = np.count_nonzero(_bits(y.float().cpu().numpy()) != _bits(ref))
+    assert mism == 0, f"{mism} of {y.numel()} outputs differ"
+
+
 @pytest.mark.parametrize("m,n,k", [(64, 256, 4096), (40, 128, 10240)])
 def test_w8a8_large_k_token_blocks_and_gemm(m, n, k):
     # 64 tokens x K = 4096 do not fit in LDS: blocks of 32; K = 10240 fits no block: GEMM
