@@ -7,9 +7,9 @@
 // heads and calls F.scaled_dot_product_attention. Here nothing is copied:
 //
 //  * paged_attn_i8_kernel (INT8 cache, fp16 / bf16 queries; the default there): one
-//    workgroup per (sequence, KV head, split of one or more 256-token chunks) whose four
-//    waves each take 64 tokens of a chunk with an online softmax of their own (no
-//    barrier until the end); scores and P x V on the MFMA with the probabilities used
+//    workgroup per (sequence, KV head, split of one or more chunks) whose 4 or 8 waves
+//    each take 64 tokens of a 256- or 512-token chunk with an online softmax of their own
+//    (no barrier until the end); scores and P x V on the MFMA with the probabilities used
 //    where the scores leave them and the values read transposed out of LDS
 //    (ds_read_b64_tr_b8); keys and values dequantized in registers; described at the
 //    kernel;
@@ -66,7 +66,7 @@ struct PagedArgs {
   void* out;              // [B, H, D] (dtype DT)
   float* ws;              // [B, H, nsplit, D + 2] partials when nsplit > 1
   int B, H, Hkv, G, BS, nsplit, max_sl, interleaved;
-  int cps;                // chunks of kPaNT tokens per split (MFMA kernel; the VALU kernel: 1)
+  int cps;                // chunks per split (kPaNT tokens, 512 for the 8-wave kernel; VALU kernel: 1)
   int bs_m16;             // ceil(2^16 / BS) for BS < 64 (block / slot of a token, wave kernel)
   float sm_scale;
 };
@@ -607,9 +607,10 @@ __global__ void __launch_bounds__(kPaNT) paged_attn_mfma_kernel(PagedArgs p) {
 
 // ---------------------------------------------------------------------------------------
 // INT8 KV cache, fp16 / bf16 queries (the default for that cache): waves that work on
-// their own. Wave w of a workgroup takes tokens 64 w .. 64 w + 63 of each 256-token chunk
-// of the split (four 16-token tiles) with an online softmax of its own, so the waves meet
-// once, at the end, where their (max, sum, partial output) are merged in LDS.
+// their own. Wave w of a workgroup of NW (4 or 8) takes tokens 64 w .. 64 w + 63 of each
+// 64 NW-token chunk of the split (four 16-token tiles) with an online softmax of its own,
+// so the waves meet once, at the end, where their (max, sum, partial output) are merged in
+// LDS.
 //  * Scores as S^T = K q^T on v_mfma_f32_16x16x32: A = the dequantized keys of a tile
 //    (row = token; lane l loads D / 4 contiguous bytes of token l & 15, so one k step of
 //    the product takes dims D / 4 (l >> 4) + 8 s .. +7, and q is loaded in the same
@@ -629,8 +630,7 @@ __global__ void __launch_bounds__(kPaNT) paged_attn_mfma_kernel(PagedArgs p) {
 //    Other scale / query types go through fp32 as in the kernels above.
 //  * Loads: a chunk's block-table entries one chunk ahead, its keys, values and scales
 //    while the previous chunk's softmax and value sum run.
-constexpr int kI8Waves = 4;
-constexpr int kI8Tok = kPaNT / kI8Waves;  // tokens per wave and chunk (4 tiles of 16)
+constexpr int kI8Tok = 64;  // tokens per wave and chunk (4 tiles of 16)
 
 // Row stride (bytes) of a wave's value tile in LDS.
 __host__ __device__ constexpr int i8_vld(int d) { return d + 16; }
@@ -676,8 +676,8 @@ __device__ __forceinline__ u32x4 i8x8_dequant(uint32_t w0, uint32_t w1, const f1
   return r;
 }
 
-template <int DT, int D, bool FAST>
-__global__ void __launch_bounds__(kPaNT) paged_attn_i8_kernel(PagedArgs p) {
+template <int DT, int D, bool FAST, int NW>
+__global__ void __launch_bounds__(64 * NW) paged_attn_i8_kernel(PagedArgs p) {
   constexpr int KB = D / 4;          // bytes of a token row per lane
   constexpr int NL = KB / 16;        // 16-byte loads per lane per token (1 or 2)
   constexpr int KS = D / 32;         // k steps of the score product
@@ -685,12 +685,14 @@ __global__ void __launch_bounds__(kPaNT) paged_attn_i8_kernel(PagedArgs p) {
   constexpr int VLD = i8_vld(D);
   constexpr float kNegInf = -__builtin_huge_valf();
   constexpr float kLog2e = 1.4426950408889634f;
+  constexpr int NT = 64 * NW;        // threads
+  constexpr int CH = NW * kI8Tok;    // tokens per chunk
   using S = typename Act<DT>::storage;
-  __shared__ __align__(16) unsigned char vt[kI8Waves * kI8Tok * VLD];  // values; merge sums after
-  __shared__ __align__(16) float vsc[kI8Waves * kI8Tok];               // value scales (0: invalid)
-  __shared__ __align__(16) unsigned char vok[kI8Waves * kI8Tok];       // token valid
-  __shared__ float ml[kI8Waves * 16 * 2];                              // per wave and head: max, sum
-  static_assert(kI8Waves * kI8Tok * VLD >= kI8Waves * 16 * D * 4, "merge sums alias the value tiles");
+  __shared__ __align__(16) unsigned char vt[NW * kI8Tok * VLD];  // values; merge sums after
+  __shared__ __align__(16) float vsc[NW * kI8Tok];               // value scales (0: invalid)
+  __shared__ __align__(16) unsigned char vok[NW * kI8Tok];       // token valid
+  __shared__ float ml[NW * 16 * 2];                              // per wave and head: max, sum
+  static_assert(NW * kI8Tok * VLD >= NW * 16 * D * 4, "merge sums alias the value tiles");
 
   const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
@@ -713,7 +715,7 @@ __global__ void __launch_bounds__(kPaNT) paged_attn_i8_kernel(PagedArgs p) {
     }
   }
   const int seq = static_cast<int>(p.sl[b]);
-  const int nchunk = (p.max_sl + kPaNT - 1) / kPaNT;
+  const int nchunk = (p.max_sl + CH - 1) / CH;
   const int c_lo = split * p.cps;
   const int c_hi = min(c_lo + p.cps, nchunk);
   // tokens below `lim` may be attended (a mask decides among them); the table holds
@@ -731,7 +733,7 @@ __global__ void __launch_bounds__(kPaNT) paged_attn_i8_kernel(PagedArgs p) {
   int slot[4] = {0, 0, 0, 0}, slot_n[4] = {0, 0, 0, 0};
   auto load_bt = [&](int c, int (&sl_out)[4]) {
     if (c < c_hi) {  // uniform; then max_seq_len > 0
-      const int T0 = c * kPaNT + wid * kI8Tok;
+      const int T0 = c * CH + wid * kI8Tok;
       const int qb0 = T0 / BS, rb0 = T0 - qb0 * BS;
 #pragma unroll
       for (int tt = 0; tt < 4; ++tt) {
@@ -762,7 +764,7 @@ __global__ void __launch_bounds__(kPaNT) paged_attn_i8_kernel(PagedArgs p) {
   const unsigned char* mrow = usem ? p.mask + static_cast<int64_t>(b * p.mask_rows_per_b + (p.mask_rows_per_b > 1 ? kvh : 0)) * p.ldm
                                    : reinterpret_cast<const unsigned char*>(p.bt);
   auto load_half = [&](int c, int h) {  // (c < c_hi: then max_seq_len > 0)
-    const int T0 = c * kPaNT + wid * kI8Tok;
+    const int T0 = c * CH + wid * kI8Tok;
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       const int tt = 2 * h + u;
@@ -919,15 +921,15 @@ __global__ void __launch_bounds__(kPaNT) paged_attn_i8_kernel(PagedArgs p) {
     ml[(wid * 16 + r16) * 2 + 1] = l_run;
   }
   __syncthreads();
-  for (int i = tid; i < G * D; i += kPaNT) {
+  for (int i = tid; i < G * D; i += NT) {
     const int g = i / D, d = i - (i / D) * D;
     float M = kNegInf;
 #pragma unroll
-    for (int w = 0; w < kI8Waves; ++w) M = fmaxf(M, ml[(w * 16 + g) * 2]);
+    for (int w = 0; w < NW; ++w) M = fmaxf(M, ml[(w * 16 + g) * 2]);
     const float Ms = M == kNegInf ? 0.f : M;
     float a = 0.f, l = 0.f;
 #pragma unroll
-    for (int w = 0; w < kI8Waves; ++w) {
+    for (int w = 0; w < NW; ++w) {
       const float fw = __builtin_amdgcn_exp2f(ml[(w * 16 + g) * 2] - Ms);  // 0 for an empty wave
       a = fmaf(fw, accs[(w * 16 + g) * D + d], a);
       l = fmaf(fw, ml[(w * 16 + g) * 2 + 1], l);
@@ -1016,25 +1018,55 @@ int paged_chunks_per_split(int64_t pairs, int nchunk) {
   return static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(cps, nchunk)));
 }
 
+// Waves per workgroup of the INT8 wave-wise kernel. At ~150 VGPRs a CU holds three
+// 4-wave workgroups (256-token chunks) but one 8-wave workgroup (512-token chunks, two per
+// split: 1024 tokens per workgroup). 8 waves when their grid G8 (pairs x ceil(max_sl /
+// 1024)) fills one round of 256 CUs nearly or exactly (192 < G8 <= 256), or when it needs
+// at most two rounds while the 4-wave grid (`grid4`) needs more than one round of 768.
+// Measured per layer (us, 4 -> 8 waves): batch 64 x 2048 tokens 20.7 -> 19.6, 128 x 1024
+// 20.4 -> 16.6, 16 x 8192 22.3 -> 19.7, 256 x 1024 38.7 -> 31.2; outside the rule 8 waves
+// lost (128 x 2048 31.1 -> 34.1, 256 x 512 17.3 -> 21.2, 32 x 2048 14.8 -> 16.5).
+// LSQ_PAGED_WAVES=4|8 forces one (tuning, tests).
+int paged_i8_waves(int64_t pairs, int max_sl, int64_t grid4) {
+  const char* e = std::getenv("LSQ_PAGED_WAVES");
+  if (e && (std::atoi(e) == 4 || std::atoi(e) == 8)) return std::atoi(e);
+  const int64_t g8 = pairs * ((max_sl + 1023) / 1024);
+  return (g8 > 192 && g8 <= 256) || (g8 <= 512 && grid4 > 768) ? 8 : 4;
+}
+
 template <int DT, bool I8, int D>
 int launch_paged(const PagedArgs& a0, hipStream_t s) {
   PagedArgs a = a0;
-  const int nchunk = a.max_sl > 0 ? (a.max_sl + kPaNT - 1) / kPaNT : 1;
   const bool mfma = DT != LSQ_F32 && !paged_valu();
-  a.cps = mfma ? paged_chunks_per_split(int64_t(a.B) * a.Hkv, nchunk) : 1;
-  a.nsplit = (nchunk + a.cps - 1) / a.cps;
+  // INT8 cache: the wave-wise kernel (its q operand is read 16 bytes at a time)
+  const bool waves = DT != LSQ_F32 && I8 && mfma && !paged_block_mfma() && (reinterpret_cast<uintptr_t>(a.q) & 15) == 0;
+  const int64_t pairs = int64_t(a.B) * a.Hkv;
+  const int nchunk4 = a.max_sl > 0 ? (a.max_sl + kPaNT - 1) / kPaNT : 1;
+  const int cps4 = mfma ? paged_chunks_per_split(pairs, nchunk4) : 1;
+  const int nw = waves ? paged_i8_waves(pairs, a.max_sl, pairs * ((nchunk4 + cps4 - 1) / cps4)) : 4;
+  if (nw == 8) {
+    const int nchunk = a.max_sl > 0 ? (a.max_sl + 511) / 512 : 1;
+    const char* ce = std::getenv("LSQ_PAGED_CHUNKS");  // (forced: n chunks per split)
+    a.cps = ce && std::atoi(ce) > 0 ? std::min(std::atoi(ce), nchunk) : std::min(2, nchunk);
+    a.nsplit = (nchunk + a.cps - 1) / a.cps;
+  } else {
+    a.cps = cps4;
+    a.nsplit = (nchunk4 + cps4 - 1) / cps4;
+  }
   const dim3 grid(static_cast<unsigned>(a.nsplit), static_cast<unsigned>(a.Hkv), static_cast<unsigned>(a.B));
   if constexpr (DT != LSQ_F32) {
-    // INT8 cache: the wave-wise kernel (its q operand is read 16 bytes at a time)
-    const bool waves = I8 && mfma && !paged_block_mfma() && (reinterpret_cast<uintptr_t>(a.q) & 15) == 0;
-    if (waves && DT == LSQ_F16 && a.scale_dt == LSQ_F16)
-      paged_attn_i8_kernel<DT, D, true><<<grid, dim3(kPaNT), 0, s>>>(a);
-    else if (waves)
-      paged_attn_i8_kernel<DT, D, false><<<grid, dim3(kPaNT), 0, s>>>(a);
-    else if (mfma)
+    const bool fast = DT == LSQ_F16 && a.scale_dt == LSQ_F16;
+    if (waves && nw == 8) {
+      if (fast) paged_attn_i8_kernel<DT, D, true, 8><<<grid, dim3(512), 0, s>>>(a);
+      else paged_attn_i8_kernel<DT, D, false, 8><<<grid, dim3(512), 0, s>>>(a);
+    } else if (waves) {
+      if (fast) paged_attn_i8_kernel<DT, D, true, 4><<<grid, dim3(256), 0, s>>>(a);
+      else paged_attn_i8_kernel<DT, D, false, 4><<<grid, dim3(256), 0, s>>>(a);
+    } else if (mfma) {
       paged_attn_mfma_kernel<DT, I8, D><<<grid, dim3(kPaNT), 0, s>>>(a);
-    else
+    } else {
       paged_attn_split_kernel<DT, I8, D><<<grid, dim3(kPaNT), 0, s>>>(a);
+    }
   } else {
     paged_attn_split_kernel<DT, I8, D><<<grid, dim3(kPaNT), 0, s>>>(a);
   }

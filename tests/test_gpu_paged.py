@@ -66,18 +66,22 @@ CASES = [
 ]
 
 
-# kernels: "default" (an INT8 cache with fp16 / bf16 queries: the wave-wise kernel; a T
-# cache: the block-wide MFMA kernel; fp32: the VALU kernel), "block" (LSQ_PAGED_KERNEL=mfma:
-# the block-wide MFMA kernel for an INT8 cache too), "valu" (the VALU kernel throughout)
-KERNEL_ENV = {"default": None, "block": "mfma", "valu": "valu"}
+# kernels: "default" (an INT8 cache with fp16 / bf16 queries: the wave-wise kernel, 4 waves
+# at these sizes; a T cache: the block-wide MFMA kernel; fp32: the VALU kernel), "waves8"
+# (the wave-wise kernel with 8 waves and 512-token chunks, LSQ_PAGED_WAVES=8), "block"
+# (LSQ_PAGED_KERNEL=mfma: the block-wide MFMA kernel for an INT8 cache too), "valu" (the
+# VALU kernel throughout)
+KERNEL_ENV = {"default": None, "waves8": None, "block": "mfma", "valu": "valu"}
 
 
 def _kernel(monkeypatch, kernel):
     if KERNEL_ENV[kernel]:
         monkeypatch.setenv("LSQ_PAGED_KERNEL", KERNEL_ENV[kernel])
+    if kernel == "waves8":
+        monkeypatch.setenv("LSQ_PAGED_WAVES", "8")
 
 
-@pytest.mark.parametrize("kernel", ["default", "block", "valu"])
+@pytest.mark.parametrize("kernel", ["default", "waves8", "block", "valu"])
 @pytest.mark.parametrize("b,h,hkv,d,bs,seqs,int8,dt,mapping", CASES)
 def test_paged_attention_matches_oracle(monkeypatch, kernel, b, h, hkv, d, bs, seqs, int8, dt, mapping):
     _kernel(monkeypatch, kernel)
@@ -90,15 +94,15 @@ def test_paged_attention_matches_oracle(monkeypatch, kernel, b, h, hkv, d, bs, s
     assert err <= 1e-2
 
 
-@pytest.mark.parametrize("kernel", ["default", "block"])
+@pytest.mark.parametrize("kernel", ["default", "waves8", "block"])
 @pytest.mark.parametrize("chunks", ["2", "3", "8"])
 @pytest.mark.parametrize("b,h,hkv,d,bs,seqs,int8,dt,mapping", [c for c in CASES if c[7] != "f32"])
 def test_paged_attention_multi_chunk_splits(monkeypatch, kernel, chunks, b, h, hkv, d, bs, seqs, int8, dt, mapping):
     # workgroups that loop over several 256-token chunks (online softmax across chunks,
     # next chunk's loads in flight), forced for every MFMA case; a split count that does not
     # divide the chunks leaves a short last split, and 8 chunks puts whole sequences in one
-    if kernel == "block" and not int8:
-        pytest.skip("a T cache runs the block-wide kernel by default")
+    if kernel in ("block", "waves8") and not int8:
+        pytest.skip("a T cache runs the block-wide kernel")
     _kernel(monkeypatch, kernel)
     print(f"paged {kernel} chunks={chunks} B={b} H={h} Hkv={hkv} D={d} seqs={seqs} int8={int8} {dt} {mapping}",
           flush=True)
@@ -247,6 +251,22 @@ def test_paged_attention_fp32_scales(monkeypatch, kernel, d, dt):
     assert qo.rel_err(got, ref) <= 1e-2
     half = _run(q, kp, vp, ks, vs, bt, sl, 16, dt)
     assert qo.rel_err(got, half) <= 1e-2
+
+
+def test_paged_attention_eight_wave_choice(monkeypatch):
+    """Batch 64 x 2048 tokens, 2 KV heads: 256 workgroups of 8 waves and 1024 tokens, no
+    combine (the default there); the 4-wave kernel with its split and combine forced for
+    comparison; both against the oracle. Ragged lengths inside the chunks."""
+    b, h, hkv, d, bs = 64, 14, 2, 64, 16
+    seqs = [2048 - 23 * i for i in range(b)]
+    q, kp, vp, ks, vs, bt, sl = _case(77, b, h, hkv, d, bs, seqs, True, "f16")
+    got8 = _run(q, kp, vp, ks, vs, bt, sl, bs, "f16")
+    monkeypatch.setenv("LSQ_PAGED_WAVES", "4")
+    got4 = _run(q, kp, vp, ks, vs, bt, sl, bs, "f16")
+    ref = qo.paged_attention(q, kp, vp, bt, sl, bs, "f16", ks, vs, "contiguous")
+    e8, e4 = qo.rel_err(got8, ref), qo.rel_err(got4, ref)
+    print(f"  8 waves {e8:.2e} 4 waves {e4:.2e}", flush=True)
+    assert e8 <= 1e-2 and e4 <= 1e-2
 
 
 def test_paged_attention_wave_kernel_matches_block_kernel(monkeypatch):
