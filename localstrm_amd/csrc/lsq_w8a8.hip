@@ -98,14 +98,31 @@ __global__ void __launch_bounds__(kAqNT) act_quant_kernel(const void* __restrict
   const float rs = __builtin_amdgcn_rcpf(s);
   if (tid == 0) sx[m] = s;
 
-  // pass 2: quantize, E int8 per chunk
+  // pass 2: quantize, E int8 per chunk. The product with rcp(s) decides every element
+  // that is not within 2^-10 of a half-integer (the argument of quant_i8_fast); a chunk
+  // holding any other element (a near-tie, s = 0, a non-finite value) takes the exact
+  // division for all its elements, which agrees with the product wherever that decides,
+  // so the common case runs without a branch per element.
   auto put = [&](int c, u32x4 w) {
+    int qv[E];
+    bool exact = false;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      const float t = mul_nc(elem(w, e), rs);
+      const float q = __builtin_rintf(t);
+      exact |= !(__builtin_fabsf(t - q) < 0.5f - 0x1p-10f);
+      qv[e] = static_cast<int>(__builtin_amdgcn_fmed3f(q, -128.f, 127.f));
+    }
+    if (exact) {
+#pragma unroll
+      for (int e = 0; e < E; ++e) qv[e] = quant_i8(elem(w, e), s);
+    }
     uint32_t o[E / 4];
 #pragma unroll
     for (int d = 0; d < E / 4; ++d) {
       uint32_t b = 0;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) b |= (static_cast<uint32_t>(quant_i8_fast(elem(w, 4 * d + e), s, rs)) & 0xFFu) << (8 * e);
+      for (int e = 0; e < 4; ++e) b |= (static_cast<uint32_t>(qv[4 * d + e]) & 0xFFu) << (8 * e);
       o[d] = b;
     }
     if constexpr (E == 8) *reinterpret_cast<uint2*>(qr + c * E) = make_uint2(o[0], o[1]);
