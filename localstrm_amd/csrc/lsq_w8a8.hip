@@ -203,10 +203,8 @@ __global__ void w8a8_untile_kernel(const int8_t* __restrict__ tiled, int8_t* __r
 // in L2), and, unless the blocked order below applies, each starts at a different k step
 // (K rotation) so that the ~32 workgroups resident on one XCD do not all miss on the same
 // activation tile at once; the int32 sums do not depend on the order.
-constexpr int QBM = 256, QBN = 256, QNT = 512;
-constexpr int QWTM = 128, QWTN = 64;
-constexpr int QFM = QWTM / 32, QFN = QWTN / 32;
-__host__ __device__ constexpr int w8a8_lds(int bk, int nst) { return nst * 2 * QBM * bk; }
+constexpr int QNT = 512;  // 8 waves, 2 (M) x 4 (N)
+__host__ __device__ constexpr int w8a8_lds(int bm, int bn, int bk, int nst) { return nst * (bm + bn) * bk; }
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x16 __attribute__((ext_vector_type(16)));
@@ -219,17 +217,22 @@ __device__ __forceinline__ i32x16 mma32_i8(u32x4 a, u32x4 b, i32x16 c) {
 // s_waitcnt immediate: vmcnt(n), lgkmcnt(0) (expcnt left alone)
 __host__ __device__ constexpr int wait_vm(int n) { return (n & 15) | (7 << 4) | ((n >> 4) << 14); }
 
-template <int DT, int BK, int NST>
+template <int DT, int QBM, int QBN, int BK, int NST>
 __global__ void __launch_bounds__(QNT) w8a8_gemm_kernel(LinearArgs p) {
   static_assert(BK == 64 || BK == 128, "k step of 64 or 128 columns");
-  static_assert(NST >= 2 && NST <= 4, "2..4 LDS stages");
+  static_assert(NST >= 2 && NST <= 8, "2..8 LDS stages");
   constexpr int A = NST - 1;         // steps the DMA runs ahead
   constexpr int KK = BK / 32;        // MFMA sub-steps per step
   constexpr int CPR = BK / 16;       // 16-byte chunks per tile row
   constexpr int RPL = 256 / BK;      // tile rows per 256 bytes (one pass over the 64 banks)
   constexpr int RPI = 1024 / BK;     // tile rows one DMA instruction fills (1 KB)
-  constexpr int kTile = QBM * BK;    // bytes of one operand tile
-  constexpr int kB = QBM / RPI / (QNT / 64);  // DMA instructions per wave per operand and step
+  constexpr int QWTM = QBM / 2, QWTN = QBN / 4;  // a wave's outputs
+  constexpr int QFM = QWTM / 32, QFN = QWTN / 32;  // its 32 x 32 MFMA blocks
+  constexpr int kXT = QBM * BK, kWT = QBN * BK;    // bytes of the two operand tiles
+  constexpr int kBx = QBM / RPI / (QNT / 64);      // DMA instructions per wave and step: x
+  constexpr int kBw = QBN / RPI / (QNT / 64);      // and weights
+  constexpr int kB = kBx + kBw;
+  static_assert(kBx >= 1 && kBw >= 1 && QFM >= 1 && QFN >= 1, "tile too small for 8 waves");
   extern __shared__ __align__(16) unsigned char smem[];
   using S = typename Act<DT>::storage;
   const int M = static_cast<int>(p.M), N = static_cast<int>(p.N), K = static_cast<int>(p.K);
@@ -265,8 +268,8 @@ __global__ void __launch_bounds__(QNT) w8a8_gemm_kernel(LinearArgs p) {
     const int g = min(st, nsteps - 1) + rot;
     return g >= nsteps ? g - nsteps : g;
   };
-  auto xs_at = [&](int buf) { return smem + buf * 2 * kTile; };
-  auto ws_at = [&](int buf) { return smem + buf * 2 * kTile + kTile; };
+  auto xs_at = [&](int buf) { return smem + buf * (kXT + kWT); };
+  auto ws_at = [&](int buf) { return smem + buf * (kXT + kWT) + kXT; };
   auto swz = [](int r) { return (r / RPL) & (CPR - 1); };
 
   // ---- descriptors: rows past M and row tiles past N read zeros (the row part of every
@@ -283,12 +286,16 @@ __global__ void __launch_bounds__(QNT) w8a8_gemm_kernel(LinearArgs p) {
   // r's 16-byte chunk of k tile columns 16 c' .. +15 is lane (r & 15) + 16 (c' >> 1) of
   // half (c' & 1) of its 2 KB tile; a step starting at column k0 % 128 of its k tile adds
   // 16 lanes (256 bytes) per 32 columns of that start, through the scalar offset.
-  uint32_t xo[kB], wo[kB];
+  uint32_t xo[kBx], wo[kBw];
 #pragma unroll
-  for (int b = 0; b < kB; ++b) {
-    const int r = (wid * kB + b) * RPI + lane / CPR;
+  for (int b = 0; b < kBx; ++b) {
+    const int r = (wid * kBx + b) * RPI + lane / CPR;
+    xo[b] = static_cast<uint32_t>(r * p.ldx + ((lane % CPR) ^ swz(r)) * 16);
+  }
+#pragma unroll
+  for (int b = 0; b < kBw; ++b) {
+    const int r = (wid * kBw + b) * RPI + lane / CPR;
     const int c = (lane % CPR) ^ swz(r);
-    xo[b] = static_cast<uint32_t>(r * p.ldx + c * 16);
     wo[b] = static_cast<uint32_t>((r >> 4) * nkt * kTileBytes8 + (c & 1) * (kTileBytes8 / 2) +
                                   ((r & 15) + 16 * (c >> 1)) * 16);
   }
@@ -296,11 +303,13 @@ __global__ void __launch_bounds__(QNT) w8a8_gemm_kernel(LinearArgs p) {
     const int k0 = gstep(st) * BK;
     const int sw = (k0 >> 7) * kTileBytes8 + ((k0 & 127) >> 5) * 256;
 #pragma unroll
-    for (int b = 0; b < kB; ++b) {
-      const int rb = (wid * kB + b) * RPI;
-      dma16_async(rx, xs_at(buf) + rb * BK, xo[b], static_cast<uint32_t>(k0));
-      dma16_async(rw, ws_at(buf) + rb * BK, wo[b], static_cast<uint32_t>(sw));
+    for (int b = 0; b < kBw; ++b) {
+      if (b < kBx) dma16_async(rx, xs_at(buf) + (wid * kBx + b) * RPI * BK, xo[b], static_cast<uint32_t>(k0));
+      dma16_async(rw, ws_at(buf) + (wid * kBw + b) * RPI * BK, wo[b], static_cast<uint32_t>(sw));
     }
+#pragma unroll
+    for (int b = kBw; b < kBx; ++b)
+      dma16_async(rx, xs_at(buf) + (wid * kBx + b) * RPI * BK, xo[b], static_cast<uint32_t>(k0));
   };
 
   i32x16 acc[QFM][QFN];
@@ -329,7 +338,7 @@ __global__ void __launch_bounds__(QNT) w8a8_gemm_kernel(LinearArgs p) {
   // prologue: steps 0 .. A-1 in flight, step 0 landed
 #pragma unroll
   for (int st = 0; st < A; ++st) issue(st, st);
-  __builtin_amdgcn_s_waitcnt(wait_vm((A - 1) * 2 * kB));
+  __builtin_amdgcn_s_waitcnt(wait_vm((A - 1) * kB));
   lds_barrier();
   load(0, 0, a[0], b[0]);
   for (int st = 0; st < nsteps; ++st) {
@@ -344,7 +353,7 @@ __global__ void __launch_bounds__(QNT) w8a8_gemm_kernel(LinearArgs p) {
       } else {
         // step st + 1 landed (steps st + 2 .. st + A stay in flight), every wave's reads
         // of this stage done; then the next step's first operands
-        __builtin_amdgcn_s_waitcnt(wait_vm((A - 1) * 2 * kB));
+        __builtin_amdgcn_s_waitcnt(wait_vm((A - 1) * kB));
         lds_barrier();
         load((st + 1) % NST, 0, a[(kk + 1) & 1], b[(kk + 1) & 1]);
       }
@@ -402,11 +411,12 @@ int max_lds_q() {
   return v;
 }
 
-template <int DT, int BK, int NST>
+template <int DT, int BM, int BN, int BK, int NST>
 int launch_w8a8_gemm_as(const LinearArgs& a, hipStream_t s) {
-  constexpr int lds = w8a8_lds(BK, NST);
+  constexpr int lds = w8a8_lds(BM, BN, BK, NST);
   if (lds > max_lds_q()) return LSQ_E_LAYOUT;
-  auto kern = w8a8_gemm_kernel<DT, BK, NST>;
+  if (int64_t(BN / kTileN) * a.K * kTileN >= (int64_t(1) << 31)) return LSQ_E_LAYOUT;
+  auto kern = w8a8_gemm_kernel<DT, BM, BN, BK, NST>;
   static std::atomic<int> attr_set{0};
   if (!attr_set.load(std::memory_order_acquire)) {
     const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
@@ -414,7 +424,7 @@ int launch_w8a8_gemm_as(const LinearArgs& a, hipStream_t s) {
     if (e != hipSuccess) return static_cast<int>(e);
     attr_set.store(1, std::memory_order_release);
   }
-  const int64_t tiles = ((a.M + QBM - 1) / QBM) * ((a.N + QBN - 1) / QBN);
+  const int64_t tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
   if (tiles > INT32_MAX) return LSQ_E_SHAPE;
   kern<<<dim3(static_cast<unsigned>(tiles)), dim3(QNT), lds, s>>>(a);
   return static_cast<int>(hipGetLastError());
@@ -424,15 +434,20 @@ template <int DT>
 int launch_w8a8_gemm(const LinearArgs& a, hipStream_t s) {
   if (a.K % kTileK != 0 || a.K < kTileK || !a.xscale) return LSQ_E_LAYOUT;
   if ((a.M - 1) * a.ldx + a.K >= (int64_t(1) << 31) || (a.ldx % 16) != 0) return LSQ_E_LAYOUT;
-  if (int64_t(QBN / kTileN) * a.K * kTileN >= (int64_t(1) << 31)) return LSQ_E_LAYOUT;
-  // LSQ_W8A8_GEMM=1: 128-column steps, two stages; =2: 64-column steps, three stages
-  // (tests, comparisons). Default 64 columns, four stages: M=2048 at 14336 x 4096
+  // LSQ_W8A8_GEMM=1: 256 x 256 tiles, 128-column steps, two stages; =2: 256 x 256, 64-column
+  // steps, three stages; =3: 64 x 128 tiles, 128-column steps, six stages (tests,
+  // comparisons). Default 256 x 256, 64 columns, four stages: M=2048 at 14336 x 4096
   // 157 -> 145 us against the first, M=8192 543 -> 506 us; three stages measured the same.
+  // Up to 192 tokens where 256 x 256 tiles leave fewer than 256 workgroups, the 64 x 128
+  // tiles (18944 x 3584: M=96 50.4 -> 45.3 us, M=128 56.1 -> 46.8, M=192 59.7 -> 48.5;
+  // M=256 equal, M=512 67 -> 104).
   const char* e = std::getenv("LSQ_W8A8_GEMM");
   const int v = e ? std::atoi(e) : 0;
-  if (v == 1) return launch_w8a8_gemm_as<DT, 128, 2>(a, s);
-  if (v == 2) return launch_w8a8_gemm_as<DT, 64, 3>(a, s);
-  return launch_w8a8_gemm_as<DT, 64, 4>(a, s);
+  if (v == 1) return launch_w8a8_gemm_as<DT, 256, 256, 128, 2>(a, s);
+  if (v == 2) return launch_w8a8_gemm_as<DT, 256, 256, 64, 3>(a, s);
+  const int64_t tiles256 = ((a.M + 255) / 256) * ((a.N + 255) / 256);
+  if (v == 3 || (v == 0 && a.M <= 192 && tiles256 < 256)) return launch_w8a8_gemm_as<DT, 64, 128, 128, 6>(a, s);
+  return launch_w8a8_gemm_as<DT, 256, 256, 64, 4>(a, s);
 }
 
 // LSQ_W8A8_PATH selects a path for comparisons and tests: "gemm" sends every M to the
@@ -456,9 +471,9 @@ bool fuse_quant(int64_t M, int64_t K) {
 
 // M <= 64: the decode kernel quantizing x itself when x is small (above) and fits its
 // first load batch; otherwise x is quantized by act_quant_kernel and the decode kernel
-// streams x_q while it fits in LDS, else runs in blocks of 32, 16, 8, 4 or 2 tokens (the
-// weights are streamed once per block, at most 8 blocks). M > 64, or no block fits: the
-// GEMM on x_q.
+// streams x_q while it fits in LDS; else, past 16 tokens, the GEMM (64 x 128 tiles), and up
+// to 16 the decode kernel in blocks of 8, 4 or 2 tokens (the weights are streamed once per
+// block, at most 8 blocks). M > 64, or no block fits: the GEMM on x_q.
 template <int DT>
 int run_w8a8(const LinearArgs& ax, const LinearArgs& a, hipStream_t s) {
   const bool gemm = path_is("gemm");
@@ -475,6 +490,10 @@ int run_w8a8(const LinearArgs& ax, const LinearArgs& a, hipStream_t s) {
   if (a.M <= 64 && !gemm) {
     rc = launch_decode_a8<DT>(a, false, s);
     if (rc != LSQ_E_LAYOUT) return rc;
+    // x_q does not fit the decode kernel's LDS: past 16 tokens the GEMM's 64 x 128 tiles
+    // read W once (18944 x 3584: M=48 33.1 -> 26.8 us, M=64 34.4 -> 28.1; 3584 x 18944:
+    // M=32 121 -> 92, M=64 185 -> 95); up to 16, token blocks of the decode kernel.
+    if (a.M > 16) return launch_w8a8_gemm<DT>(a, s);
     using Sy = typename Act<DT>::storage;
     // At most 8 passes over W: at small N the GEMM launches few workgroups (14 at
     // N = 3584), and 8 passes of the decode kernel still beat it (3584 x 18944, 8 tokens

@@ -246,7 +246,7 @@ def test_w8a8_linear_bit_exact_large_n(m):
 def test_w8a8_large_k_token_blocks(m, n, k):
     # 1-2 long rows: quantized inside the decode kernel; x_q of 8+ tokens at K = 18944
     # exceeds LDS: blocks of 4 (2 passes at M = 8, 4 at M = 13 with a ragged last
-    # block), of 8 at K = 14336
+    # block), of 8 at K = 14336 (16 tokens); 64 tokens there: the GEMM's 64 x 128 tiles
     _say(f"w8a8 large K blocks bf16 M={m} N={n} K={k}")
     x, wq, sw, bias = _lin_inputs("bf16", m, n, k)
     y, _, _ = _linear(x.to(DEV), wq, sw, bias)
@@ -301,13 +301,16 @@ def test_w8a8_gemm_kernel_on_decode_shapes(monkeypatch, m, n, k):
     assert torch.equal(y_dec.view(torch.int16), y_gemm.view(torch.int16))
 
 
-@pytest.mark.parametrize("variant", ["1", "2", "0"])
-@pytest.mark.parametrize("m,n,k", [(65, 520, 1024), (257, 136, 64), (300, 264, 256), (1024, 2048, 640)])
+@pytest.mark.parametrize("variant", ["1", "2", "3", "0"])
+@pytest.mark.parametrize("m,n,k", [(65, 520, 1024), (257, 136, 64), (300, 264, 256), (1024, 2048, 640),
+                                   (40, 1000, 1920)])
 def test_w8a8_gemm_pipeline_depths(monkeypatch, variant, m, n, k):
-    # The prefill GEMM's k step and LDS stages (LSQ_W8A8_GEMM: 1 = 128 columns, 2 stages;
-    # 2 = 64 columns, 3 stages; 0 = the default, 64 columns, 4 stages), bit-exact against
-    # the oracle: the XCD-blocked tile order (1024 x 2048: 4 x 8 tiles) and the plain one,
-    # K of 1 to 8 k tiles (fewer steps than the pipeline holds, at K = 64 and 256).
+    # The GEMM's tile, k step and LDS stages (LSQ_W8A8_GEMM: 1 = 256 x 256 tiles, 128
+    # columns, 2 stages; 2 = 256 x 256, 64 columns, 3 stages; 3 = 64 x 128 tiles, 128
+    # columns, 6 stages; 0 = 256 x 256, 64 columns, 4 stages), bit-exact against the
+    # oracle: the XCD-blocked tile order (1024 x 2048) and the plain one, K of 1 to 15
+    # k tiles (fewer steps than the pipeline holds at K = 64 and 256), partial tiles in M
+    # and N.
     _say(f"w8a8 gemm pipeline {variant} M={m} N={n} K={k}")
     monkeypatch.setenv("LSQ_W8A8_GEMM", variant)
     x, wq, sw, bias = _lin_inputs("bf16", m, n, k)
@@ -320,7 +323,8 @@ def test_w8a8_gemm_pipeline_depths(monkeypatch, variant, m, n, k):
 
 @pytest.mark.parametrize("m,n,k", [(64, 256, 4096), (40, 128, 10240)])
 def test_w8a8_large_k_token_blocks_and_gemm(m, n, k):
-    # 64 tokens x K = 4096 do not fit in LDS: blocks of 32; K = 10240 fits no block: GEMM
+    # 64 tokens x K = 4096 and 40 x 10240 do not fit the decode kernel's LDS: the GEMM
+    # (64 x 128 tiles past 16 tokens)
     _say(f"w8a8 large K M={m} N={n} K={k}")
     g = torch.Generator().manual_seed(k)
     x = torch.randn(m, k, generator=g).to(torch.bfloat16)
