@@ -5,14 +5,15 @@
 // chain of elementwise kernels (:411-414), pads M to a multiple of 32 (:416-422), calls
 // torch._int_mm (:425) and rescales in fp32 (:431-440). Here:
 //
-//  * the decode kernel's W8A8 modes (lsq_decode_impl.h) for M <= 64: int8 weights streamed
-//    once from the tiled layout straight into v_mfma_i32_16x16x64_i8, no conversion;
-//    for small x (M * K <= 16384) every workgroup quantizes x itself while staging it,
-//    so the layer is one launch;
+//  * the decode kernel's W8A8 modes (lsq_decode_impl.h) for M <= 64 while x_q fits its
+//    LDS: int8 weights streamed once from the tiled layout straight into
+//    v_mfma_i32_16x16x64_i8, no conversion; for small x (M * K <= 16384) every workgroup
+//    quantizes x itself while staging it, so the layer is one launch;
 //  * act_quant_kernel otherwise: one workgroup per token row: max|x| (exact in the input
 //    type), the scale, and the int8 row, from x held in registers;
-//  * w8a8_gemm_kernel for larger M: both operands DMA'd from HBM into LDS and fed to
-//    v_mfma_i32_32x32x32_i8; the fp32 rescale and bias are the epilogue.
+//  * w8a8_gemm_kernel for larger M (and 17..64 tokens whose x_q exceeds that LDS): both
+//    operands DMA'd from HBM into LDS (64 x 128 or 256 x 256 tiles, several stages ahead)
+//    and fed to v_mfma_i32_32x32x32_i8; the fp32 rescale and bias are the epilogue.
 //
 // Exactness. The int32 sum of int8 products is exact in any order (|sum| < 2^31 for
 // K < 131072), so the only roundings are the reference's own elementwise ones:
