@@ -218,6 +218,23 @@ int lsq_w8a8_linear(const void* x, int64_t ldx, const int8_t* tiled, const void*
                     int dtype, int64_t M, int64_t N, int64_t K, int8_t* x_q, float* scale_x,
                     void* stream);
 
+/* lsq_w8a8_linear with a caller-provided workspace (the same reference lines,
+ * quantization.py:404-447, and the same result bit for bit): `workspace` (device memory,
+ * 16-byte aligned, or NULL) of `workspace_bytes`. With at least
+ * lsq_w8a8_workspace_bytes(M, N, K) bytes, calls whose int8 GEMM would leave the GPU short
+ * of workgroups on a long K (up to 192 tokens, fewer than 128 tiles of 64 x 128 outputs,
+ * 16+ 128-column tiles: e.g. 3584 x 18944) split K over workgroups; each slice's int32
+ * sums go to the workspace and a second kernel adds them (exact), rescales, adds the bias
+ * and rounds to T, as the unsplit GEMM does. Such calls then also take the GEMM below 17
+ * tokens when x_q does not fit the decode kernel. With a smaller or NULL workspace they
+ * behave exactly like lsq_w8a8_linear. The workspace is scratch for the duration of the
+ * call on `stream`. lsq_w8a8_workspace_bytes is 0 for shapes that never split. */
+int64_t lsq_w8a8_workspace_bytes(int64_t M, int64_t N, int64_t K);
+int lsq_w8a8_linear_ws(const void* x, int64_t ldx, const int8_t* tiled, const void* scale_w,
+                       int scale_w_dtype, const void* bias, int bias_dtype, void* y, int64_t ldy,
+                       int dtype, int64_t M, int64_t N, int64_t K, int8_t* x_q, float* scale_x,
+                       void* workspace, int64_t workspace_bytes, void* stream);
+
 /* Bytes of the fixed device array behind lsq_w8a8_linear_noalloc, one per GPU. */
 #define LSQ_NOALLOC_SCRATCH_BYTES (8 * 1024 * 1024)
 

@@ -79,6 +79,12 @@ SIGNATURES = {
         _int,
         [_vp, _i64, _vp, _vp, _int, _vp, _int, _vp, _i64, _int, _i64, _i64, _i64, _vp, _vp, _vp],
     ),
+    "lsq_w8a8_workspace_bytes": (_i64, [_i64, _i64, _i64]),
+    "lsq_w8a8_linear_ws": (
+        _int,
+        [_vp, _i64, _vp, _vp, _int, _vp, _int, _vp, _i64, _int, _i64, _i64, _i64, _vp, _vp, _vp, _i64,
+         _vp],
+    ),
     "lsq_quantize_w8": (_int, [_vp, _int, _i64, _i64, _i64, _vp, _vp, _vp, _vp]),
     "lsq_quantize_w4": (_int, [_vp, _int, _i64, _i64, _i64, _i64, _vp, _int, _vp, _vp, _vp]),
     "lsq_probe_empty": (_int, [_vp]),

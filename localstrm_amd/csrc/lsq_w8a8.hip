@@ -218,7 +218,7 @@ __device__ __forceinline__ i32x16 mma32_i8(u32x4 a, u32x4 b, i32x16 c) {
 // s_waitcnt immediate: vmcnt(n), lgkmcnt(0) (expcnt left alone)
 __host__ __device__ constexpr int wait_vm(int n) { return (n & 15) | (7 << 4) | ((n >> 4) << 14); }
 
-template <int DT, int QBM, int QBN, int BK, int NST>
+template <int DT, int QBM, int QBN, int BK, int NST, bool SPLIT>
 __global__ void __launch_bounds__(QNT) w8a8_gemm_kernel(LinearArgs p) {
   static_assert(BK == 64 || BK == 128, "k step of 64 or 128 columns");
   static_assert(NST >= 2 && NST <= 8, "2..8 LDS stages");
@@ -237,7 +237,15 @@ __global__ void __launch_bounds__(QNT) w8a8_gemm_kernel(LinearArgs p) {
   extern __shared__ __align__(16) unsigned char smem[];
   using S = typename Act<DT>::storage;
   const int M = static_cast<int>(p.M), N = static_cast<int>(p.N), K = static_cast<int>(p.K);
-  const int nsteps = K / BK;
+  // split-K (SPLIT): workgroup b takes K slice b % NS of tile b / NS, steps
+  // [st_lo, st_lo + nsteps) of the layer's nsteps_all, and writes its int32 sums to the
+  // workspace p.part [NS][M][N]; the merge kernel adds the slices and rescales
+  const int NS = SPLIT ? p.ksplit : 1;
+  const int tile = SPLIT ? static_cast<int>(blockIdx.x) / NS : static_cast<int>(blockIdx.x);
+  const int sl = SPLIT ? static_cast<int>(blockIdx.x) % NS : 0;
+  const int nsteps_all = K / BK;
+  const int st_lo = sl * nsteps_all / NS;
+  const int nsteps = (sl + 1) * nsteps_all / NS - st_lo;
   const int nkt = K / kTileK;  // k tiles of the weight layout
   const int mtiles = (M + QBM - 1) / QBM;
   // Tile order as in the weight-only prefill GEMM (lsq_gemm.hip, gemm_rw_kernel): groups
@@ -245,10 +253,10 @@ __global__ void __launch_bounds__(QNT) w8a8_gemm_kernel(LinearArgs p) {
   // eighth of that order, so the workgroups resident on one XCD form a 4 x 8 block of
   // tiles and, with no K rotation, share activation and weight tiles in that XCD's L2
   // (14336 x 4096: M=2048 155 -> 146 us, M=8192 535 -> 519 us); M fastest otherwise.
-  int mt = blockIdx.x % mtiles;
-  int nt = blockIdx.x / mtiles;
+  int mt = tile % mtiles;
+  int nt = tile / mtiles;
   const int ntiles = (N + QBN - 1) / QBN;
-  const bool blocked = mtiles % 4 == 0 && (mtiles * ntiles) % 8 == 0;
+  const bool blocked = !SPLIT && mtiles % 4 == 0 && (mtiles * ntiles) % 8 == 0;
   if (blocked) {
     const int L = (blockIdx.x & 7) * (mtiles * ntiles / 8) + (blockIdx.x >> 3);
     const int r = L % (4 * ntiles);
@@ -262,12 +270,12 @@ __global__ void __launch_bounds__(QNT) w8a8_gemm_kernel(LinearArgs p) {
   const int lane = tid & 63;
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wid & 1, wn = wid >> 1;
-  const int rot = blocked ? 0 : (((blockIdx.x >> 3) & 31) * nsteps) >> 5;
+  const int rot = blocked || SPLIT ? 0 : (((blockIdx.x >> 3) & 31) * nsteps) >> 5;
   // k step of pipeline step st; steps past the end repeat the last one (their stage is
   // never read), so every wave issues the same DMAs in every step and waits exact counts
   auto gstep = [&](int st) {
     const int g = min(st, nsteps - 1) + rot;
-    return g >= nsteps ? g - nsteps : g;
+    return st_lo + (g >= nsteps ? g - nsteps : g);
   };
   auto xs_at = [&](int buf) { return smem + buf * (kXT + kWT); };
   auto ws_at = [&](int buf) { return smem + buf * (kXT + kWT) + kXT; };
@@ -368,6 +376,22 @@ __global__ void __launch_bounds__(QNT) w8a8_gemm_kernel(LinearArgs p) {
   __builtin_amdgcn_s_waitcnt(wait_vm(0));
   lds_barrier();
 
+  if constexpr (SPLIT) {  // this slice's exact int32 sums
+    int* part = reinterpret_cast<int*>(p.part) + static_cast<int64_t>(sl) * M * N;
+#pragma unroll
+    for (int i = 0; i < QFM; ++i)
+#pragma unroll
+      for (int j = 0; j < QFN; ++j) {
+        const int n = n0 + wn * QWTN + 32 * j + (lane & 31);
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int m = m0 + wm * QWTM + 32 * i + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+          if (m < M && n < N) part[static_cast<int64_t>(m) * N + n] = acc[i][j][v];
+        }
+      }
+    return;
+  }
+
   // ---- epilogue: y = fp32(acc) * (sx[m] * sw[n]) [+ fp32(bias[n])], rounded to T
   float* sxs = reinterpret_cast<float*>(smem);  // the tile's token scales (LDS is free now)
   if (tid < QBM) sxs[tid] = tid < rows_m ? p.xscale[m0 + tid] : 0.f;
@@ -412,12 +436,63 @@ int max_lds_q() {
   return v;
 }
 
-template <int DT, int BM, int BN, int BK, int NST>
+// y[m, n] = round_T(fp32(sum over the S slices of part[s][m][n]) * (sx[m] * sw[n])
+// [+ fp32(bias[n])]): the split GEMM's merge. The int32 sum is exact in any order, and the
+// rescale is the GEMM epilogue's, operation for operation, so the result is the unsplit
+// kernel's bit for bit. Every slice's load is issued before the first add.
+template <int DT>
+__global__ void __launch_bounds__(256) w8a8_merge_kernel(const int* __restrict__ part, int S, int M, int N,
+                                                         const float* __restrict__ sx, const void* sw, int sw_dt,
+                                                         const void* bias, int bias_dt,
+                                                         typename Act<DT>::storage* __restrict__ y, int64_t ldy) {
+  constexpr int kMaxS = 16;
+  const int64_t MN = int64_t(M) * N;
+  const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= MN) return;
+  const int m = static_cast<int>(i / N), n = static_cast<int>(i - int64_t(m) * N);
+  int v[kMaxS];
+#pragma unroll
+  for (int s = 0; s < kMaxS; ++s) v[s] = s < S ? part[s * MN + i] : 0;
+  int acc = 0;
+#pragma unroll
+  for (int s = 0; s < kMaxS; ++s) acc += v[s];
+  float r = mul_nc(static_cast<float>(acc), mul_nc(sx[m], load_as_f32(sw, sw_dt, n)));
+  if (bias) r = add_nc(r, load_as_f32(bias, bias_dt, n));
+  y[static_cast<int64_t>(m) * ldy + n] = Act<DT>::from_f32(opaque(r));
+}
+
+// Split-K plan for the 64 x 128 tiles (up to 192 tokens where 256 x 256 tiles leave fewer
+// than 256 workgroups) when those tiles are fewer than 128 and K is long (16+ k tiles):
+// S slices (2..16, at least 4 k tiles each) bring the grid to about 256 workgroups; the
+// workspace holds S x M x N int32 sums. 3584 x 18944 (28 tiles of 128 output columns):
+// S = 9. LSQ_W8A8_SPLITK=0 turns it off, =n forces n slices (tests, sweeps).
+struct W8a8Split {
+  int64_t S, bytes;
+};
+
+W8a8Split w8a8_split_plan(int64_t M, int64_t N, int64_t Kp) {
+  W8a8Split sp{1, 0};
+  const char* e = std::getenv("LSQ_W8A8_SPLITK");
+  if (e && e[0] == '0') return sp;
+  const int64_t forced = e ? std::atoi(e) : 0;
+  const int64_t tiles256 = ((M + 255) / 256) * ((N + 255) / 256);
+  if (M < 1 || M > 192 || tiles256 >= 256 || Kp % kTileK != 0) return sp;
+  const int64_t tiles = ((M + 63) / 64) * ((N + 127) / 128);
+  const int64_t steps = Kp / kTileK;
+  int64_t S = forced >= 2 ? forced : (tiles < 128 && steps >= 16 ? std::min<int64_t>(16, 256 / tiles) : 1);
+  if (forced < 2) S = std::min<int64_t>(S, steps / 4);
+  if (S < 2 || S > 16 || S > steps) return sp;
+  sp.S = S;
+  sp.bytes = S * M * N * 4;
+  return sp;
+}
+
+template <int DT, int BM, int BN, int BK, int NST, bool SPLIT = false>
 int launch_w8a8_gemm_as(const LinearArgs& a, hipStream_t s) {
   constexpr int lds = w8a8_lds(BM, BN, BK, NST);
   if (lds > max_lds_q()) return LSQ_E_LAYOUT;
   if (int64_t(BN / kTileN) * a.K * kTileN >= (int64_t(1) << 31)) return LSQ_E_LAYOUT;
-  auto kern = w8a8_gemm_kernel<DT, BM, BN, BK, NST>;
+  auto kern = w8a8_gemm_kernel<DT, BM, BN, BK, NST, SPLIT>;
   static std::atomic<int> attr_set{0};
   if (!attr_set.load(std::memory_order_acquire)) {
     const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
@@ -425,7 +500,7 @@ int launch_w8a8_gemm_as(const LinearArgs& a, hipStream_t s) {
     if (e != hipSuccess) return static_cast<int>(e);
     attr_set.store(1, std::memory_order_release);
   }
-  const int64_t tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
+  const int64_t tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN) * (SPLIT ? a.ksplit : 1);
   if (tiles > INT32_MAX) return LSQ_E_SHAPE;
   kern<<<dim3(static_cast<unsigned>(tiles)), dim3(QNT), lds, s>>>(a);
   return static_cast<int>(hipGetLastError());
@@ -447,7 +522,23 @@ int launch_w8a8_gemm(const LinearArgs& a, hipStream_t s) {
   if (v == 1) return launch_w8a8_gemm_as<DT, 256, 256, 128, 2>(a, s);
   if (v == 2) return launch_w8a8_gemm_as<DT, 256, 256, 64, 3>(a, s);
   const int64_t tiles256 = ((a.M + 255) / 256) * ((a.N + 255) / 256);
-  if (v == 3 || (v == 0 && a.M <= 192 && tiles256 < 256)) return launch_w8a8_gemm_as<DT, 64, 128, 128, 6>(a, s);
+  if (v == 3 || (v == 0 && a.M <= 192 && tiles256 < 256)) {
+    // with the caller's workspace, split K where the tiles are few (long-K layers)
+    const W8a8Split sp = w8a8_split_plan(a.M, a.N, a.K);
+    if (sp.S >= 2 && a.part && a.part_bytes >= sp.bytes && (reinterpret_cast<uintptr_t>(a.part) & 3) == 0) {
+      LinearArgs as = a;
+      as.ksplit = static_cast<int>(sp.S);
+      int rc = launch_w8a8_gemm_as<DT, 64, 128, 128, 6, true>(as, s);
+      if (rc != LSQ_OK) return rc;
+      const int64_t outs = a.M * a.N;
+      using St = typename Act<DT>::storage;
+      w8a8_merge_kernel<DT><<<dim3(static_cast<unsigned>((outs + 255) / 256)), dim3(256), 0, s>>>(
+          reinterpret_cast<const int*>(a.part), static_cast<int>(sp.S), static_cast<int>(a.M),
+          static_cast<int>(a.N), a.xscale, a.scale, a.scale_dt, a.bias, a.bias_dt, static_cast<St*>(a.y), a.ldy);
+      return static_cast<int>(hipGetLastError());
+    }
+    return launch_w8a8_gemm_as<DT, 64, 128, 128, 6>(a, s);
+  }
   return launch_w8a8_gemm_as<DT, 256, 256, 64, 4>(a, s);
 }
 
@@ -472,9 +563,9 @@ bool fuse_quant(int64_t M, int64_t K) {
 
 // M <= 64: the decode kernel quantizing x itself when x is small (above) and fits its
 // first load batch; otherwise x is quantized by act_quant_kernel and the decode kernel
-// streams x_q while it fits in LDS; else, past 16 tokens, the GEMM (64 x 128 tiles), and up
-// to 16 the decode kernel in blocks of 8, 4 or 2 tokens (the weights are streamed once per
-// block, at most 8 blocks). M > 64, or no block fits: the GEMM on x_q.
+// streams x_q while it fits in LDS; else the GEMM (64 x 128 tiles, split over K with the
+// caller's workspace), or the decode kernel in token blocks (the weights are streamed
+// once per block, at most 8 blocks). M > 64, or no block fits: the GEMM on x_q.
 template <int DT>
 int run_w8a8(const LinearArgs& ax, const LinearArgs& a, hipStream_t s) {
   const bool gemm = path_is("gemm");
@@ -491,10 +582,16 @@ int run_w8a8(const LinearArgs& ax, const LinearArgs& a, hipStream_t s) {
   if (a.M <= 64 && !gemm) {
     rc = launch_decode_a8<DT>(a, false, s);
     if (rc != LSQ_E_LAYOUT) return rc;
-    // x_q does not fit the decode kernel's LDS: past 16 tokens the GEMM's 64 x 128 tiles
-    // read W once (18944 x 3584: M=48 33.1 -> 26.8 us, M=64 34.4 -> 28.1; 3584 x 18944:
-    // M=32 121 -> 92, M=64 185 -> 95); up to 16, token blocks of the decode kernel.
-    if (a.M > 16) return launch_w8a8_gemm<DT>(a, s);
+    // x_q does not fit the decode kernel's LDS. With the workspace, the split-K GEMM
+    // (3584 x 18944: M=16 66.6 -> 33.0 us, M=32 121 -> 34.0, M=64 185 -> 35.5; 896 x 4864
+    // M=32 18.5 -> 15.9). Without it, the GEMM's 64 x 128 tiles past 32 tokens, or past 16
+    // on layers of 16+ such tiles (18944 x 3584: M=48 33.0 -> 27.1 us; 3584 x 18944 M=32
+    // 121 -> 92); else token blocks of the decode kernel (896 x 4864 M=32: 18.5 us blocks,
+    // 30.2 unsplit GEMM over 7 tiles).
+    const W8a8Split sp = w8a8_split_plan(a.M, a.N, a.K);
+    const bool split = sp.S >= 2 && a.part && a.part_bytes >= sp.bytes;
+    const int64_t tiles = ((a.M + 63) / 64) * ((a.N + 127) / 128);
+    if (split || (a.M > 16 && (a.M > 32 || tiles >= 16))) return launch_w8a8_gemm<DT>(a, s);
     using Sy = typename Act<DT>::storage;
     // At most 8 passes over W: at small N the GEMM launches few workgroups (14 at
     // N = 3584), and 8 passes of the decode kernel still beat it (3584 x 18944, 8 tokens
@@ -576,10 +673,12 @@ extern "C" int lsq_act_quant_i8(const void* x, int64_t ldx, int dtype, int64_t M
   }
 }
 
-extern "C" int lsq_w8a8_linear(const void* x, int64_t ldx, const int8_t* tiled,
-                               const void* scale_w, int scale_w_dtype, const void* bias,
-                               int bias_dtype, void* y, int64_t ldy, int dtype, int64_t M,
-                               int64_t N, int64_t K, int8_t* x_q, float* scale_x, void* stream) {
+namespace {
+
+// lsq_w8a8_linear with an optional split-K workspace (part / part_bytes; NULL / 0: none).
+int w8a8_linear(const void* x, int64_t ldx, const int8_t* tiled, const void* scale_w, int scale_w_dtype,
+                const void* bias, int bias_dtype, void* y, int64_t ldy, int dtype, int64_t M, int64_t N,
+                int64_t K, int8_t* x_q, float* scale_x, void* part, int64_t part_bytes, void* stream) {
   if (M < 0 || N < 0 || K < 1 || ldx < K || ldy < N) return LSQ_E_SHAPE;
   if (M > INT32_MAX / 2 || N > INT32_MAX / 2 || K >= 131072) return LSQ_E_SHAPE;
   if (!valid_dt(dtype) || !valid_dt(scale_w_dtype) || (bias && !valid_dt(bias_dtype))) return LSQ_E_DTYPE;
@@ -595,6 +694,10 @@ extern "C" int lsq_w8a8_linear(const void* x, int64_t ldx, const int8_t* tiled,
   const uint8_t* tw = reinterpret_cast<const uint8_t*>(tiled);
   LinearArgs ax{x, ldx, tw, scale_w, scale_w_dtype, bias, bias_dtype, y, ldy, M, N, K, kp, 1, nullptr};
   LinearArgs a{x_q, kp, tw, scale_w, scale_w_dtype, bias, bias_dtype, y, ldy, M, N, kp, kp, 1, scale_x};
+  if (part && part_bytes > 0) {
+    a.part = static_cast<float*>(part);
+    a.part_bytes = part_bytes;
+  }
   int rc;
   switch (dtype) {
     case LSQ_F32: rc = run_w8a8<LSQ_F32>(ax, a, s); break;
@@ -602,6 +705,31 @@ extern "C" int lsq_w8a8_linear(const void* x, int64_t ldx, const int8_t* tiled,
     default: rc = run_w8a8<LSQ_BF16>(ax, a, s); break;
   }
   return rc == LSQ_E_LAYOUT ? LSQ_E_SHAPE : rc;
+}
+
+}  // namespace
+
+extern "C" int lsq_w8a8_linear(const void* x, int64_t ldx, const int8_t* tiled,
+                               const void* scale_w, int scale_w_dtype, const void* bias,
+                               int bias_dtype, void* y, int64_t ldy, int dtype, int64_t M,
+                               int64_t N, int64_t K, int8_t* x_q, float* scale_x, void* stream) {
+  return w8a8_linear(x, ldx, tiled, scale_w, scale_w_dtype, bias, bias_dtype, y, ldy, dtype, M, N, K, x_q,
+                     scale_x, nullptr, 0, stream);
+}
+
+extern "C" int64_t lsq_w8a8_workspace_bytes(int64_t M, int64_t N, int64_t K) {
+  if (M < 1 || N < 1 || K < 1 || M > INT32_MAX / 2 || N > INT32_MAX / 2 || K >= 131072) return 0;
+  const int64_t b = w8a8_split_plan(M, N, pad_k(K)).bytes;
+  return b > 0 ? (b + 255) / 256 * 256 : 0;
+}
+
+extern "C" int lsq_w8a8_linear_ws(const void* x, int64_t ldx, const int8_t* tiled, const void* scale_w,
+                                  int scale_w_dtype, const void* bias, int bias_dtype, void* y, int64_t ldy,
+                                  int dtype, int64_t M, int64_t N, int64_t K, int8_t* x_q, float* scale_x,
+                                  void* workspace, int64_t workspace_bytes, void* stream) {
+  if (workspace && (reinterpret_cast<uintptr_t>(workspace) & 15)) return LSQ_E_ALIGN;
+  return w8a8_linear(x, ldx, tiled, scale_w, scale_w_dtype, bias, bias_dtype, y, ldy, dtype, M, N, K, x_q,
+                     scale_x, workspace, workspace ? workspace_bytes : 0, stream);
 }
 
 // ---- Allocation-free W8A8 entry point ----

@@ -247,6 +247,7 @@ def test_w8a8_large_k_token_blocks(m, n, k):
     # 1-2 long rows: quantized inside the decode kernel; x_q of 8+ tokens at K = 18944
     # exceeds LDS: blocks of 4 (2 passes at M = 8, 4 at M = 13 with a ragged last
     # block), of 8 at K = 14336 (16 tokens); 64 tokens there: the GEMM's 64 x 128 tiles
+    # (no workspace here: the unsplit GEMM)
     _say(f"w8a8 large K blocks bf16 M={m} N={n} K={k}")
     x, wq, sw, bias = _lin_inputs("bf16", m, n, k)
     y, _, _ = _linear(x.to(DEV), wq, sw, bias)
@@ -321,10 +322,120 @@ def test_w8a8_gemm_pipeline_depths(monkeypatch, variant, m, n, k):
     assert mism == 0, f"{mism} of {y.numel()} outputs differ"
 
 
+def _linear_ws(x2, wq, sw, bias, nws=None, misalign=False):
+    """lsq_w8a8_linear_ws with lsq_w8a8_workspace_bytes of workspace (or nws bytes)."""
+    m, k = x2.shape
+    n = wq.shape[0]
+    lib = _lib.load()
+    wt = wq.t().contiguous().to(DEV)
+    tiled = torch.empty(lib.lsq_w8a8_tiled_bytes(n, k), dtype=torch.int8, device=DEV)
+    _lib.check(lib.lsq_w8a8_retile(wt.data_ptr(), tiled.data_ptr(), n, k, _lib.stream_handle(DEV)), "retile")
+    y = torch.empty((m, n), dtype=x2.dtype, device=DEV)
+    xq = torch.empty((m, _pad_k(k)), dtype=torch.int8, device=DEV)
+    sx = torch.empty(m, dtype=torch.float32, device=DEV)
+    swd = sw.to(DEV).contiguous()
+    b = bias.to(DEV).contiguous() if bias is not None else None
+    nws = lib.lsq_w8a8_workspace_bytes(m, n, k) if nws is None else nws
+    ws = torch.full((nws + 16,), 0x7F, dtype=torch.uint8, device=DEV)  # stale contents
+    wp = ws.data_ptr() + (4 if misalign else 0)
+    rc = lib.lsq_w8a8_linear_ws(x2.data_ptr(), x2.stride(0), tiled.data_ptr(), swd.data_ptr(),
+                                _lib.dtype_code(swd.dtype), _lib.ptr(b),
+                                _lib.dtype_code(b.dtype) if b is not None else 0, y.data_ptr(), n,
+                                _lib.dtype_code(x2.dtype), m, n, k, xq.data_ptr(), sx.data_ptr(),
+                                wp if nws > 0 else None, nws, _lib.stream_handle(DEV))
+    torch.cuda.synchronize()
+    return rc, y
+
+
+@pytest.mark.parametrize("m,n,k", [(64, 512, 18944), (33, 640, 4864), (16, 384, 18944), (8, 3584, 18944),
+                                   (5, 256, 10240), (100, 520, 8192), (64, 3584, 18944)])
+def test_w8a8_split_k_bit_exact(m, n, k):
+    # The split-K GEMM (int32 slices in the workspace, exact merge, the GEMM's rescale):
+    # bit-exact against the oracle and bit-identical to the workspace-free entry point.
+    # Below 17 tokens the workspace also moves long rows from the decode kernel's token
+    # blocks to the split GEMM (16 and 8 tokens at K = 18944); 5 x 10240 fits the decode
+    # kernel and leaves the workspace unused.
+    _say(f"w8a8 split-K M={m} N={n} K={k}")
+    x, wq, sw, bias = _lin_inputs("bf16", m, n, k)
+    xd = x.to(DEV)
+    nws = _lib.load().lsq_w8a8_workspace_bytes(m, n, k)
+    assert nws > 0
+    rc, y = _linear_ws(xd, wq, sw, bias)
+    _lib.check(rc, "lsq_w8a8_linear_ws")
+    plain, _, _ = _linear(xd, wq, sw, bias)
+    ref = qo.w8a8_linear(x.float().numpy(), wq.numpy(), sw.numpy(),
+                         None if bias is None else bias.float().numpy(), "bf16")
+    got = y.float().cpu().numpy()
+    mism = np.count_nonzero(_bits(got) != _bits(ref))
+    assert mism == 0, f"{mism} of {got.size} outputs differ from the oracle"
+    assert torch.equal(y.view(torch.int16), plain.view(torch.int16))
+
+
+@pytest.mark.parametrize("forced", ["2", "7", "16"])
+@pytest.mark.parametrize("dt", ["bf16", "f16", "f32"])
+def test_w8a8_split_k_forced_slices_and_dtypes(monkeypatch, forced, dt):
+    # LSQ_W8A8_SPLITK=n forces n slices (ragged: 32 k tiles over 7); every activation type
+    m, n, k = 40, 1000, 4096
+    monkeypatch.setenv("LSQ_W8A8_SPLITK", forced)
+    _say(f"w8a8 split-K forced={forced} {dt} M={m} N={n} K={k}")
+    x, wq, sw, bias = _lin_inputs(dt, m, n, k)
+    nws = _lib.load().lsq_w8a8_workspace_bytes(m, n, k)
+    assert nws >= int(forced) * m * n * 4
+    rc, y = _linear_ws(x.to(DEV), wq, sw, bias)
+    _lib.check(rc, "lsq_w8a8_linear_ws")
+    ref = qo.w8a8_linear(x.float().numpy(), wq.numpy(), sw.numpy(),
+                         None if bias is None else bias.float().numpy(), dt)
+    assert np.array_equal(_bits(y.float().cpu().numpy()), _bits(ref))
+
+
+def test_w8a8_workspace_contract(monkeypatch):
+    lib = _lib.load()
+    assert lib.lsq_w8a8_workspace_bytes(64, 3584, 18944) == 9 * 64 * 3584 * 4  # 28 tiles: 9 slices
+    assert lib.lsq_w8a8_workspace_bytes(64, 18944, 3584) == 0   # 148 tiles: no split
+    assert lib.lsq_w8a8_workspace_bytes(256, 3584, 18944) == 0  # past 192 tokens
+    assert lib.lsq_w8a8_workspace_bytes(64, 3584, 1024) == 0    # 8 k tiles: too short
+    assert lib.lsq_w8a8_workspace_bytes(0, 3584, 18944) == 0
+    monkeypatch.setenv("LSQ_W8A8_SPLITK", "0")
+    assert lib.lsq_w8a8_workspace_bytes(64, 3584, 18944) == 0
+    monkeypatch.delenv("LSQ_W8A8_SPLITK")
+    # a misaligned workspace is refused; a short one runs the unsplit GEMM, same bits
+    m, n, k = 33, 640, 4864
+    x, wq, sw, bias = _lin_inputs("bf16", m, n, k)
+    xd = x.to(DEV)
+    rc, _ = _linear_ws(xd, wq, sw, bias, misalign=True)
+    assert rc == -6  # LSQ_E_ALIGN
+    rc, y_short = _linear_ws(xd, wq, sw, bias, nws=1024)
+    _lib.check(rc, "lsq_w8a8_linear_ws")
+    rc, y_split = _linear_ws(xd, wq, sw, bias)
+    _lib.check(rc, "lsq_w8a8_linear_ws")
+    assert torch.equal(y_short.view(torch.int16), y_split.view(torch.int16))
+
+
+def test_w8a8_module_split_k_down_projection():
+    # Int8GEMMLinear on a 3584 x 18944 down projection at 32 tokens: the module takes the
+    # workspace from torch's allocator; two calls in a row give the same bits
+    n, k, m = 3584, 18944, 32
+    g = torch.Generator().manual_seed(5)
+    lin = nn.Linear(k, n, bias=True)
+    with torch.no_grad():
+        lin.weight.copy_(torch.randn(n, k, generator=g) * 0.02)
+        lin.bias.copy_(torch.randn(n, generator=g) * 0.1)
+    q = Int8GEMMLinear.from_float(lin.to(torch.bfloat16)).to(DEV)
+    x = torch.randn(m, k, generator=g).to(torch.bfloat16).to(DEV)
+    with torch.no_grad():
+        y1 = q(x)
+        y2 = q(x)
+    assert torch.equal(y1.view(torch.int16), y2.view(torch.int16))
+    wq = q.weight_q_t.t().contiguous().cpu()
+    ref = qo.w8a8_linear(x.float().cpu().numpy(), wq.numpy(), q.scale_w_t.reshape(-1).float().cpu().numpy(),
+                         q.bias.detach().float().cpu().numpy(), "bf16")
+    assert np.array_equal(_bits(y1.float().cpu().numpy()), _bits(ref))
+
+
 @pytest.mark.parametrize("m,n,k", [(64, 256, 4096), (40, 128, 10240)])
 def test_w8a8_large_k_token_blocks_and_gemm(m, n, k):
-    # 64 tokens x K = 4096 and 40 x 10240 do not fit the decode kernel's LDS: the GEMM
-    # (64 x 128 tiles past 16 tokens)
+    # 64 tokens x K = 4096 and 40 x 10240 do not fit the decode kernel's LDS: without a
+    # workspace the GEMM's 64 x 128 tiles (past 32 tokens, or 16 on layers of 16+ tiles)
     _say(f"w8a8 large K M={m} N={n} K={k}")
     g = torch.Generator().manual_seed(k)
     x = torch.randn(m, k, generator=g).to(torch.bfloat16)

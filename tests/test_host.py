@@ -389,6 +389,16 @@ def test_library_rejects_bad_arguments_without_gpu():
     bad[4] = 9
     assert lib.lsq_w8a8_linear(*bad) == -3
     assert lib.lsq_w8a8_linear(*args[:10], 0, *args[11:]) == 0  # M = 0
+    # the workspace form: a misaligned workspace is refused before any HIP call; its size
+    # (host arithmetic only): S x M x N int32 sums where the 64 x 128 tiles are few and K long
+    assert lib.lsq_w8a8_linear_ws(*args[:15], (1 << 20) + 4, 4096, None) == -6
+    assert lib.lsq_w8a8_linear_ws(*args[:10], 0, *args[11:15], None, 0, None) == 0  # M = 0
+    assert lib.lsq_w8a8_workspace_bytes(64, 3584, 18944) == 9 * 64 * 3584 * 4
+    assert lib.lsq_w8a8_workspace_bytes(16, 384, 18944) == 16 * 16 * 384 * 4
+    assert lib.lsq_w8a8_workspace_bytes(64, 18944, 3584) == 0  # 148 tiles
+    assert lib.lsq_w8a8_workspace_bytes(256, 3584, 18944) == 0  # past 192 tokens
+    assert lib.lsq_w8a8_workspace_bytes(64, 3584, 1024) == 0  # 8 k tiles
+    assert lib.lsq_w8a8_workspace_bytes(0, 3584, 18944) == 0
     for code in (-1, -2, -3, -4, -5, -6):
         assert lib.lsq_status_string(code).startswith(b"lsq:")
     with pytest.raises(_lib.LsqError, match="group_size"):
