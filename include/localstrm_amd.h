@@ -222,8 +222,9 @@ int lsq_w8a8_linear(const void* x, int64_t ldx, const int8_t* tiled, const void*
  * quantization.py:404-447, and the same result bit for bit): `workspace` (device memory,
  * 16-byte aligned, or NULL) of `workspace_bytes`. With at least
  * lsq_w8a8_workspace_bytes(M, N, K) bytes, calls whose int8 GEMM would leave the GPU short
- * of workgroups on a long K (up to 192 tokens, fewer than 128 tiles of 64 x 128 outputs,
- * 16+ 128-column tiles: e.g. 3584 x 18944) split K over workgroups; each slice's int32
+ * of workgroups on a long K (fewer than 128 output tiles of 64 x 128, up to 192 tokens, or
+ * of 256 x 256 above, with 2048+ columns: e.g. 3584 x 18944 at any M up to ~2048) split K
+ * over workgroups; each slice's int32
  * sums go to the workspace and a second kernel adds them (exact), rescales, adds the bias
  * and rounds to T, as the unsplit GEMM does. Such calls then also take the GEMM below 17
  * tokens when x_q does not fit the decode kernel. With a smaller or NULL workspace they

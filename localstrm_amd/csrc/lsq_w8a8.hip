@@ -461,26 +461,33 @@ __global__ void __launch_bounds__(256) w8a8_merge_kernel(const int* __restrict__
   y[static_cast<int64_t>(m) * ldy + n] = Act<DT>::from_f32(opaque(r));
 }
 
-// Split-K plan for the 64 x 128 tiles (up to 192 tokens where 256 x 256 tiles leave fewer
-// than 256 workgroups) when those tiles are fewer than 128 and K is long (16+ k tiles):
-// S slices (2..16, at least 4 k tiles each) bring the grid to about 256 workgroups; the
-// workspace holds S x M x N int32 sums. 3584 x 18944 (28 tiles of 128 output columns):
-// S = 9. LSQ_W8A8_SPLITK=0 turns it off, =n forces n slices (tests, sweeps).
+// Split-K plan for the GEMM's tiles when they are fewer than 128 and K is long: the 64 x
+// 128 tiles (up to 192 tokens where 256 x 256 tiles leave fewer than 256 workgroups) with
+// 16+ k tiles, slices of at least 4 k tiles; the 256 x 256 tiles with 64+ steps of 64
+// columns, slices of at least 8 steps. S = min(16, 256 / tiles) slices bring the grid to
+// about 256 workgroups; the workspace holds S x M x N int32 sums. 3584 x 18944: 28 small
+// tiles at M = 64, S = 9; 112 large tiles at M = 2048, S = 2. LSQ_W8A8_SPLITK=0 turns it
+// off, =n forces n slices (tests, sweeps).
 struct W8a8Split {
   int64_t S, bytes;
 };
+
+bool w8a8_small_tiles(int64_t M, int64_t N) {
+  return M <= 192 && ((M + 255) / 256) * ((N + 255) / 256) < 256;
+}
 
 W8a8Split w8a8_split_plan(int64_t M, int64_t N, int64_t Kp) {
   W8a8Split sp{1, 0};
   const char* e = std::getenv("LSQ_W8A8_SPLITK");
   if (e && e[0] == '0') return sp;
   const int64_t forced = e ? std::atoi(e) : 0;
-  const int64_t tiles256 = ((M + 255) / 256) * ((N + 255) / 256);
-  if (M < 1 || M > 192 || tiles256 >= 256 || Kp % kTileK != 0) return sp;
-  const int64_t tiles = ((M + 63) / 64) * ((N + 127) / 128);
-  const int64_t steps = Kp / kTileK;
-  int64_t S = forced >= 2 ? forced : (tiles < 128 && steps >= 16 ? std::min<int64_t>(16, 256 / tiles) : 1);
-  if (forced < 2) S = std::min<int64_t>(S, steps / 4);
+  if (M < 1 || Kp % kTileK != 0) return sp;
+  const bool small = w8a8_small_tiles(M, N);
+  const int64_t tiles = small ? ((M + 63) / 64) * ((N + 127) / 128) : ((M + 255) / 256) * ((N + 255) / 256);
+  const int64_t steps = small ? Kp / 128 : Kp / 64;  // pipeline steps of the tile shape
+  const int64_t min_steps = small ? 4 : 8;          // per slice
+  int64_t S = forced >= 2 ? forced : (tiles < 128 && steps >= 4 * min_steps ? std::min<int64_t>(16, 256 / tiles) : 1);
+  if (forced < 2) S = std::min<int64_t>(S, steps / min_steps);
   if (S < 2 || S > 16 || S > steps) return sp;
   sp.S = S;
   sp.bytes = S * M * N * 4;
@@ -521,25 +528,23 @@ int launch_w8a8_gemm(const LinearArgs& a, hipStream_t s) {
   const int v = e ? std::atoi(e) : 0;
   if (v == 1) return launch_w8a8_gemm_as<DT, 256, 256, 128, 2>(a, s);
   if (v == 2) return launch_w8a8_gemm_as<DT, 256, 256, 64, 3>(a, s);
-  const int64_t tiles256 = ((a.M + 255) / 256) * ((a.N + 255) / 256);
-  if (v == 3 || (v == 0 && a.M <= 192 && tiles256 < 256)) {
-    // with the caller's workspace, split K where the tiles are few (long-K layers)
-    const W8a8Split sp = w8a8_split_plan(a.M, a.N, a.K);
-    if (sp.S >= 2 && a.part && a.part_bytes >= sp.bytes && (reinterpret_cast<uintptr_t>(a.part) & 3) == 0) {
-      LinearArgs as = a;
-      as.ksplit = static_cast<int>(sp.S);
-      int rc = launch_w8a8_gemm_as<DT, 64, 128, 128, 6, true>(as, s);
-      if (rc != LSQ_OK) return rc;
-      const int64_t outs = a.M * a.N;
-      using St = typename Act<DT>::storage;
-      w8a8_merge_kernel<DT><<<dim3(static_cast<unsigned>((outs + 255) / 256)), dim3(256), 0, s>>>(
-          reinterpret_cast<const int*>(a.part), static_cast<int>(sp.S), static_cast<int>(a.M),
-          static_cast<int>(a.N), a.xscale, a.scale, a.scale_dt, a.bias, a.bias_dt, static_cast<St*>(a.y), a.ldy);
-      return static_cast<int>(hipGetLastError());
-    }
-    return launch_w8a8_gemm_as<DT, 64, 128, 128, 6>(a, s);
+  const bool small = v == 3 || (v == 0 && w8a8_small_tiles(a.M, a.N));
+  // with the caller's workspace, split K where the tiles are few (long-K layers)
+  const W8a8Split sp = v == 0 ? w8a8_split_plan(a.M, a.N, a.K) : W8a8Split{1, 0};
+  if (sp.S >= 2 && a.part && a.part_bytes >= sp.bytes && (reinterpret_cast<uintptr_t>(a.part) & 3) == 0) {
+    LinearArgs as = a;
+    as.ksplit = static_cast<int>(sp.S);
+    const int rc = small ? launch_w8a8_gemm_as<DT, 64, 128, 128, 6, true>(as, s)
+                         : launch_w8a8_gemm_as<DT, 256, 256, 64, 4, true>(as, s);
+    if (rc != LSQ_OK) return rc;
+    const int64_t outs = a.M * a.N;
+    using St = typename Act<DT>::storage;
+    w8a8_merge_kernel<DT><<<dim3(static_cast<unsigned>((outs + 255) / 256)), dim3(256), 0, s>>>(
+        reinterpret_cast<const int*>(a.part), static_cast<int>(sp.S), static_cast<int>(a.M),
+        static_cast<int>(a.N), a.xscale, a.scale, a.scale_dt, a.bias, a.bias_dt, static_cast<St*>(a.y), a.ldy);
+    return static_cast<int>(hipGetLastError());
   }
-  return launch_w8a8_gemm_as<DT, 256, 256, 64, 4>(a, s);
+  return small ? launch_w8a8_gemm_as<DT, 64, 128, 128, 6>(a, s) : launch_w8a8_gemm_as<DT, 256, 256, 64, 4>(a, s);
 }
 
 // LSQ_W8A8_PATH selects a path for comparisons and tests: "gemm" sends every M to the

@@ -348,13 +348,15 @@ def _linear_ws(x2, wq, sw, bias, nws=None, misalign=False):
 
 
 @pytest.mark.parametrize("m,n,k", [(64, 512, 18944), (33, 640, 4864), (16, 384, 18944), (8, 3584, 18944),
-                                   (5, 256, 10240), (100, 520, 8192), (64, 3584, 18944)])
+                                   (5, 256, 10240), (100, 520, 8192), (64, 3584, 18944),
+                                   (256, 520, 8192), (600, 1000, 8192), (1024, 3584, 18944)])
 def test_w8a8_split_k_bit_exact(m, n, k):
     # The split-K GEMM (int32 slices in the workspace, exact merge, the GEMM's rescale):
     # bit-exact against the oracle and bit-identical to the workspace-free entry point.
     # Below 17 tokens the workspace also moves long rows from the decode kernel's token
     # blocks to the split GEMM (16 and 8 tokens at K = 18944); 5 x 10240 fits the decode
-    # kernel and leaves the workspace unused.
+    # kernel and leaves the workspace unused. Past 192 tokens the 256 x 256 tiles split
+    # (256 x 520 x 8192: 3 tiles, 16 slices; 1024 x 3584 x 18944: 56 tiles, 4 slices).
     _say(f"w8a8 split-K M={m} N={n} K={k}")
     x, wq, sw, bias = _lin_inputs("bf16", m, n, k)
     xd = x.to(DEV)
@@ -392,7 +394,8 @@ def test_w8a8_workspace_contract(monkeypatch):
     lib = _lib.load()
     assert lib.lsq_w8a8_workspace_bytes(64, 3584, 18944) == 9 * 64 * 3584 * 4  # 28 tiles: 9 slices
     assert lib.lsq_w8a8_workspace_bytes(64, 18944, 3584) == 0   # 148 tiles: no split
-    assert lib.lsq_w8a8_workspace_bytes(256, 3584, 18944) == 0  # past 192 tokens
+    assert lib.lsq_w8a8_workspace_bytes(256, 3584, 18944) == 16 * 256 * 3584 * 4  # 14 large tiles
+    assert lib.lsq_w8a8_workspace_bytes(2048, 14336, 4096) == 0  # 448 large tiles: no split
     assert lib.lsq_w8a8_workspace_bytes(64, 3584, 1024) == 0    # 8 k tiles: too short
     assert lib.lsq_w8a8_workspace_bytes(0, 3584, 18944) == 0
     monkeypatch.setenv("LSQ_W8A8_SPLITK", "0")

@@ -396,7 +396,9 @@ def test_library_rejects_bad_arguments_without_gpu():
     assert lib.lsq_w8a8_workspace_bytes(64, 3584, 18944) == 9 * 64 * 3584 * 4
     assert lib.lsq_w8a8_workspace_bytes(16, 384, 18944) == 16 * 16 * 384 * 4
     assert lib.lsq_w8a8_workspace_bytes(64, 18944, 3584) == 0  # 148 tiles
-    assert lib.lsq_w8a8_workspace_bytes(256, 3584, 18944) == 0  # past 192 tokens
+    assert lib.lsq_w8a8_workspace_bytes(256, 3584, 18944) == 16 * 256 * 3584 * 4  # 14 large tiles
+    assert lib.lsq_w8a8_workspace_bytes(2048, 3584, 18944) == 2 * 2048 * 3584 * 4  # 112 large tiles
+    assert lib.lsq_w8a8_workspace_bytes(2048, 14336, 4096) == 0  # 448 large tiles
     assert lib.lsq_w8a8_workspace_bytes(64, 3584, 1024) == 0  # 8 k tiles
     assert lib.lsq_w8a8_workspace_bytes(0, 3584, 18944) == 0
     for code in (-1, -2, -3, -4, -5, -6):
