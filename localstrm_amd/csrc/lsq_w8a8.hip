@@ -463,8 +463,8 @@ __global__ void __launch_bounds__(256) w8a8_merge_kernel(const int* __restrict__
 
 // Split-K plan for the GEMM's tiles when they are fewer than 128 and K is long: the 64 x
 // 128 tiles (up to 192 tokens where 256 x 256 tiles leave fewer than 256 workgroups) with
-// 16+ k tiles, slices of at least 4 k tiles; the 256 x 256 tiles with 64+ steps of 64
-// columns, slices of at least 8 steps. S = min(16, 256 / tiles) slices bring the grid to
+// 16+ k tiles, slices of at least 4 k tiles; the 256 x 256 tiles with 32+ steps of 64
+// columns, slices of at least 8 steps (both: K >= 2048). S = min(16, 256 / tiles) slices bring the grid to
 // about 256 workgroups; the workspace holds S x M x N int32 sums. 3584 x 18944: 28 small
 // tiles at M = 64, S = 9; 112 large tiles at M = 2048, S = 2. LSQ_W8A8_SPLITK=0 turns it
 // off, =n forces n slices (tests, sweeps).
