@@ -532,6 +532,8 @@ def main() -> int:
             sweep.append(bench_decode("int4", K, N, m, args.steps, args.warmup, device))
         for m in (1, 64):
             sweep.append(bench_decode("w8a8", N, K, m, args.steps, args.warmup, device))
+        # W8A8 on the down-projection shape (split-K GEMM with the module's workspace)
+        sweep.append(bench_decode("w8a8", K, N, 64, args.steps, args.warmup, device))
         sweep.append(bench_decode("w8a8", 14336, 4096, 2048, max(10, args.steps // 20),
                                   max(2, args.warmup // 4), device))
         sweep.append(bench_stack(max(5, args.steps // 20), 2, device))
