@@ -46,20 +46,22 @@ __host__ __device__ constexpr int64_t pad_k(int64_t K) { return (K + kTileK - 1)
 
 // ============================================================ activation quantization
 
-constexpr int kAqNT = 256;  // threads per token row
 constexpr int kAqR = 4;     // 16-byte chunks per thread kept in registers between passes
 
 // NaN-propagating max (torch.max returns NaN for a row holding one).
 __device__ __forceinline__ float nan_max(float a, float b) { return (b > a || b != b) ? b : a; }
 
-template <int DT>
-__global__ void __launch_bounds__(kAqNT) act_quant_kernel(const void* __restrict__ x, int64_t ldx,
+// NT threads per token row: 256, or 1024 for rows longer than 256 threads hold in
+// registers (more than 8192 bf16 / fp16 or 4096 fp32 values, which would otherwise be read
+// twice) when the rows are few.
+template <int DT, int NT>
+__global__ void __launch_bounds__(NT) act_quant_kernel(const void* __restrict__ x, int64_t ldx,
                                                           int K, int Kz, bool vec,
                                                           int8_t* __restrict__ xq, int64_t ldq,
                                                           float* __restrict__ sx) {
   using S = typename Act<DT>::storage;
   constexpr int E = 16 / static_cast<int>(sizeof(S));  // elements per 16-byte chunk
-  __shared__ float wmax[kAqNT / 64];
+  __shared__ float wmax[NT / 64];
   const int m = blockIdx.x;
   const int tid = threadIdx.x;
   const S* xr = static_cast<const S*>(x) + static_cast<int64_t>(m) * ldx;
@@ -75,25 +77,25 @@ __global__ void __launch_bounds__(kAqNT) act_quant_kernel(const void* __restrict
   float mx = 0.f;
 #pragma unroll
   for (int r = 0; r < kAqR; ++r) {
-    const int c = tid + r * kAqNT;
+    const int c = tid + r * NT;
     if (c < nch) {
       v[r] = *reinterpret_cast<const u32x4*>(xr + c * E);
 #pragma unroll
       for (int e = 0; e < E; ++e) mx = nan_max(mx, fabsf(elem(v[r], e)));
     }
   }
-  for (int c = tid + kAqR * kAqNT; c < nch; c += kAqNT) {
+  for (int c = tid + kAqR * NT; c < nch; c += NT) {
     const u32x4 w = *reinterpret_cast<const u32x4*>(xr + c * E);
 #pragma unroll
     for (int e = 0; e < E; ++e) mx = nan_max(mx, fabsf(elem(w, e)));
   }
-  for (int k = nch * E + tid; k < K; k += kAqNT) mx = nan_max(mx, fabsf(Act<DT>::to_f32(xr[k])));
+  for (int k = nch * E + tid; k < K; k += NT) mx = nan_max(mx, fabsf(Act<DT>::to_f32(xr[k])));
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) mx = nan_max(mx, __shfl_xor(mx, off, 64));
   if ((tid & 63) == 0) wmax[tid >> 6] = mx;
   __syncthreads();
 #pragma unroll
-  for (int w = 0; w < kAqNT / 64; ++w) mx = nan_max(mx, wmax[w]);
+  for (int w = 0; w < NT / 64; ++w) mx = nan_max(mx, wmax[w]);
 
   const float s = a8_scale<DT>(mx);
   const float rs = __builtin_amdgcn_rcpf(s);
@@ -131,12 +133,12 @@ __global__ void __launch_bounds__(kAqNT) act_quant_kernel(const void* __restrict
   };
 #pragma unroll
   for (int r = 0; r < kAqR; ++r) {
-    const int c = tid + r * kAqNT;
+    const int c = tid + r * NT;
     if (c < nch) put(c, v[r]);
   }
-  for (int c = tid + kAqR * kAqNT; c < nch; c += kAqNT) put(c, *reinterpret_cast<const u32x4*>(xr + c * E));
-  for (int k = nch * E + tid; k < K; k += kAqNT) qr[k] = static_cast<int8_t>(quant_i8_fast(Act<DT>::to_f32(xr[k]), s, rs));
-  for (int k = K + tid; k < Kz; k += kAqNT) qr[k] = 0;  // padding columns
+  for (int c = tid + kAqR * NT; c < nch; c += NT) put(c, *reinterpret_cast<const u32x4*>(xr + c * E));
+  for (int k = nch * E + tid; k < K; k += NT) qr[k] = static_cast<int8_t>(quant_i8_fast(Act<DT>::to_f32(xr[k]), s, rs));
+  for (int k = K + tid; k < Kz; k += NT) qr[k] = 0;  // padding columns
 }
 
 template <int DT>
@@ -146,8 +148,15 @@ int launch_act_quant(const void* x, int64_t ldx, int64_t M, int64_t K, int64_t K
   constexpr int E = 16 / static_cast<int>(sizeof(S));
   const bool vec = (reinterpret_cast<uintptr_t>(x) & 15) == 0 && ldx % E == 0 &&
                    (reinterpret_cast<uintptr_t>(xq) & 7) == 0 && ldq % 8 == 0;
-  act_quant_kernel<DT><<<dim3(static_cast<unsigned>(M)), dim3(kAqNT), 0, s>>>(
-      x, ldx, static_cast<int>(K), static_cast<int>(Kz), vec, xq, ldq, sx);
+  // rows past what 256 threads keep in registers, on few rows: 1024 threads (K = 18944
+  // bf16, M = 64: 12.8 -> 7.1 us; at M = 2048, where 256-thread rows already fill the GPU,
+  // 31.1 -> 33.7, so those keep 256)
+  if (K > int64_t(256) * kAqR * E && M <= 512)
+    act_quant_kernel<DT, 1024><<<dim3(static_cast<unsigned>(M)), dim3(1024), 0, s>>>(
+        x, ldx, static_cast<int>(K), static_cast<int>(Kz), vec, xq, ldq, sx);
+  else
+    act_quant_kernel<DT, 256><<<dim3(static_cast<unsigned>(M)), dim3(256), 0, s>>>(
+        x, ldx, static_cast<int>(K), static_cast<int>(Kz), vec, xq, ldq, sx);
   return static_cast<int>(hipGetLastError());
 }
 

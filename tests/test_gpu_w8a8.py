@@ -110,7 +110,7 @@ def test_act_scale_matches_torch_on_the_device(dt):
 
 
 ACT_CASES = [(1, 896, 896), (7, 100, 100), (64, 3584, 3584), (300, 1024, 1024), (5, 8, 8),
-             (9, 72, 200), (3, 9000, 9000)]
+             (9, 72, 200), (3, 9000, 9000), (520, 8300, 8300)]  # long rows: 1024 / 256 threads
 
 
 @pytest.mark.parametrize("dt", ["bf16", "f16", "f32"])
