@@ -349,14 +349,16 @@ def _linear_ws(x2, wq, sw, bias, nws=None, misalign=False):
 
 @pytest.mark.parametrize("m,n,k", [(64, 512, 18944), (33, 640, 4864), (16, 384, 18944), (8, 3584, 18944),
                                    (5, 256, 10240), (100, 520, 8192), (64, 3584, 18944),
-                                   (256, 520, 8192), (600, 1000, 8192), (1024, 3584, 18944)])
+                                   (256, 520, 8192), (600, 1000, 8192), (1024, 3584, 18944),
+                                   (24, 1002, 8192)])
 def test_w8a8_split_k_bit_exact(m, n, k):
     # The split-K GEMM (int32 slices in the workspace, exact merge, the GEMM's rescale):
     # bit-exact against the oracle and bit-identical to the workspace-free entry point.
     # Below 17 tokens the workspace also moves long rows from the decode kernel's token
     # blocks to the split GEMM (16 and 8 tokens at K = 18944); 5 x 10240 fits the decode
     # kernel and leaves the workspace unused. Past 192 tokens the 256 x 256 tiles split
-    # (256 x 520 x 8192: 3 tiles, 16 slices; 1024 x 3584 x 18944: 56 tiles, 4 slices).
+    # (256 x 520 x 8192: 3 tiles, 16 slices; 1024 x 3584 x 18944: 56 tiles, 4 slices);
+    # N = 1002: a partial last tile of output columns.
     _say(f"w8a8 split-K M={m} N={n} K={k}")
     x, wq, sw, bias = _lin_inputs("bf16", m, n, k)
     xd = x.to(DEV)
