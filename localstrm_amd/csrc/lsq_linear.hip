@@ -175,11 +175,20 @@ static int dispatch(bool w4, const void* x, int64_t ldx, const uint8_t* w, const
       if (rc != LSQ_E_LAYOUT) return rc;
     }
   } else {
-    // fp32 activations, 1..8 tokens, tiled weights: the VALU decode GEMV
-    if (tiled && act == LSQ_ACT_NONE && K % kTileK == 0 && M >= 1 && M <= 8) {
-      LinearArgs a{x, ldx, tiled, scale, scale_dt, bias, bias_dt, y, ldy, M, N, K, group, ng};
-      const int rc = launch_gemv32(w4 ? kW4Tiled : kW8Tiled, a, s);
-      if (rc != LSQ_E_LAYOUT) return rc;
+    // fp32 activations on tiled weights: the VALU decode GEMV, in blocks of 8 tokens past 8
+    // (18944 x 3584 INT4, against the generic kernel: M=9 449 -> 52 us, M=16 606 -> 76,
+    // M=64 2196 -> 276; 14336 x 4096 M=256 7902 -> 966); a block that does not fit (the
+    // first: nothing has run) leaves the layer to the generic kernel
+    if (tiled && act == LSQ_ACT_NONE && K % kTileK == 0 && M >= 1) {
+      for (int64_t m0 = 0; m0 < M; m0 += 8) {
+        const int64_t mb = M - m0 < 8 ? M - m0 : 8;
+        LinearArgs a{static_cast<const float*>(x) + m0 * ldx, ldx, tiled, scale, scale_dt, bias, bias_dt,
+                     static_cast<float*>(y) + m0 * ldy, ldy, mb, N, K, group, ng};
+        const int rc = launch_gemv32(w4 ? kW4Tiled : kW8Tiled, a, s);
+        if (rc == LSQ_E_LAYOUT && m0 == 0) break;
+        if (rc != LSQ_OK) return rc == LSQ_E_LAYOUT ? LSQ_E_SHAPE : rc;
+        if (m0 + mb == M) return LSQ_OK;
+      }
     }
   }
   if (act != LSQ_ACT_NONE) return LSQ_E_LAYOUT;

@@ -1,6 +1,6 @@
-"""GPU parity of the fp32-activation decode GEMV (lsq_gemv32.hip: 1..8 fp32 tokens on the
-tiled INT8 / INT4 layouts, each weight formed as round_fp32(q * s) like the reference's
-dequantize(), products summed in fp32 on the VALU). The reference's CPU path runs in fp32
+"""GPU parity of the fp32-activation decode GEMV (lsq_gemv32.hip: 1..8 fp32 tokens per
+launch, more in blocks of 8, on the tiled INT8 / INT4 layouts, each weight formed as
+round_fp32(q * s) like the reference's dequantize(), products summed in fp32 on the VALU). The reference's CPU path runs in fp32
 (src/kernels/quantization.py:104-141), and BASELINE config 1 allows fp32 activations.
 
 Bar: rel = max|y - y_ref| / max|y_ref| <= 1e-5 against the float64 oracle
@@ -77,10 +77,11 @@ def _check(kind, n, k, m, group=128, seed=0, scale_dtype=None, bias=False, ldx=N
     return ql, xd, y
 
 
-@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 8])
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 8, 9, 16, 23, 64])
 @pytest.mark.parametrize("kind", ["int8", "int4"])
 def test_fp32_decode_baseline_shape(kind, m):
-    """18944 x 3584 (1184 row tiles: 237 workgroups of 16 waves), bias on even M."""
+    """18944 x 3584 (1184 row tiles: 237 workgroups of 16 waves), bias on even M; past 8
+    tokens in blocks of 8 (23: two full blocks and one of 7)."""
     _check(kind, 18944, 3584, m, bias=(m % 2 == 0), seed=m)
 
 
@@ -120,8 +121,8 @@ def test_fp32_strided_activations():
 
 def test_fp32_deterministic_and_matches_generic_kernel(monkeypatch):
     """Bit-identical on a second call (fixed summation order); the generic kernel
-    (LSQ_GEMV32=0, one wave per output row) within the bar; nine tokens (past this kernel)
-    go to the generic kernel and still meet it."""
+    (LSQ_GEMV32=0, one wave per output row) within the bar; nine tokens (a block of 8 and
+    one of 1) meet it too."""
     for kind in ("int8", "int4"):
         ql, xd, y1 = _check(kind, 18944, 3584, 4, bias=True, seed=21)
         with torch.no_grad():
