@@ -85,7 +85,8 @@ int launch_bgemv(int kind, const LinearArgs& a, hipStream_t s);
 template <int DT>
 int launch_decode_mb(int kind, const LinearArgs& a, hipStream_t s);
 
-// Decode GEMV for fp32 activations and outputs, 1..8 tokens, on the tiled layouts
+// Decode GEMV for fp32 activations and outputs, 1..8 tokens per launch (the dispatcher
+// runs more tokens in blocks of 8), on the tiled layouts
 // (lsq_gemv32.hip): each weight formed as round_fp32(q * s), products summed with fmaf on
 // the VALU. Returns LSQ_E_LAYOUT without launching anything for what it does not cover
 // (canonical layouts, more tokens, activations or scales too large for LDS).

@@ -1,11 +1,13 @@
-// Decode GEMV for fp32 activations, 1..8 tokens, on the tiled INT4 / INT8 layouts (gfx950).
+// Decode GEMV for fp32 activations, 1..8 tokens per launch, on the tiled INT4 / INT8 layouts
+// (gfx950).
 //
 // GPU form of QuantizedLinear.forward (src/kernels/quantization.py:104-141) when x is fp32,
 // the type the reference's CPU path runs in: y = x W^T + b with every weight formed as the
 // reference's dequantize() forms it, W = round_fp32(q * s) (q = u - 8 for INT4), and the
-// products summed in fp32 with fmaf. fp32 operands have no MFMA form that keeps that
-// per-weight rounding; at a few tokens the arithmetic (a conversion, the scale product and
-// one FMA per token and weight) keeps pace with the weight stream on the VALU.
+// products summed in fp32 with fmaf. At one or two tokens the arithmetic (a conversion, the
+// scale product and one FMA per token and weight) keeps pace with the weight stream on the
+// VALU; at 8 tokens it bounds the kernel (an fp32 MFMA taking the rounded weights as its B
+// operand would take over the FMAs there).
 //
 // Work split as the 1..16-token GEMV (lsq_gemv.hip): balanced ranges of whole 16-row tiles
 // per workgroup, the workgroup's (row tile, k tile) units cut into W contiguous runs, one
