@@ -523,8 +523,8 @@ def main() -> int:
             sweep.append(bench_decode("int4", 14336, 4096, m, max(10, args.steps // 20),
                                       max(2, args.warmup // 4), device))
         sweep.append(bench_decode("int8", 4864, 896, 1, args.steps, args.warmup, device))
-        # fp32 activations (the reference's CPU type; config 1 allows them): config 1 and
-        # the headline shape
+        # fp32 activations (the reference's CPU type, allowed for the single INT8 layer): that
+        # layer (4864x896) and the headline shape
         sweep.append(bench_decode("int8", 4864, 896, 1, args.steps, args.warmup, device, x_dtype=torch.float32))
         sweep.append(bench_decode("int4", N, K, 1, args.steps, args.warmup, device, group=G, x_dtype=torch.float32))
         # the transposed (down-projection) shape, whose activations exceed LDS from 4 tokens

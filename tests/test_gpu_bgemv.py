@@ -89,8 +89,8 @@ def _check(kind, n, k, m, group=128, dtype=torch.bfloat16, bias=False, seed=0, s
 @pytest.mark.parametrize("m", [17, 24, 32, 33, 48, 64])
 @pytest.mark.parametrize("kind", ["int4", "int8"])
 def test_bgemv_decode_shape(kind, m):
-    """The BASELINE batched decode shape, 18944 x 3584 (1184 row tiles: 237 workgroups),
-    bias on odd M."""
+    """The Qwen2.5-7B MLP's batched decode shape, 18944 x 3584 (1184 row tiles: 237
+    workgroups), bias on odd M."""
     _check(kind, 18944, 3584, m, bias=(m % 2 == 1), seed=m)
 
 

@@ -1,7 +1,8 @@
 """GPU parity of the fp32-activation decode GEMV (lsq_gemv32.hip: 1..8 fp32 tokens per
 launch, more in blocks of 8, on the tiled INT8 / INT4 layouts, each weight formed as
-round_fp32(q * s) like the reference's dequantize(), products summed in fp32 on the VALU). The reference's CPU path runs in fp32
-(src/kernels/quantization.py:104-141), and BASELINE config 1 allows fp32 activations.
+round_fp32(q * s) like the reference's dequantize(), products summed in fp32 on the VALU).
+The reference's CPU path runs in fp32 (src/kernels/quantization.py:104-141), and the
+single-layer INT8 4864 x 896 workload allows fp32 activations.
 
 Bar: rel = max|y - y_ref| / max|y_ref| <= 1e-5 against the float64 oracle
 (oracle.quant_oracle.linear_f64 on the oracle's fp32-dequantized weights), the bar the
@@ -87,7 +88,8 @@ def test_fp32_decode_baseline_shape(kind, m):
 
 @pytest.mark.parametrize("kind", ["int8", "int4"])
 def test_fp32_config1_shape(kind):
-    """Qwen2.5-0.5B gate_proj 4864 x 896 (config 1: 152 workgroups of 8 waves)."""
+    """Qwen2.5-0.5B gate_proj 4864 x 896, the single-layer INT8 workload (152 workgroups of
+    8 waves)."""
     for m in (1, 4, 8):
         _check(kind, 4864, 896, m, seed=11 + m)
 

@@ -104,7 +104,7 @@ def test_int4_unpack_and_dequant_bit_exact(k):
 
 @pytest.mark.parametrize("dt", ["f32", "f16", "bf16"])
 def test_full_size_dequant_bit_exact(dt):
-    """BASELINE shapes: INT8 18944x3584 per-channel and INT4 group-128 18944x3584."""
+    """The Qwen2.5-7B MLP shapes: INT8 18944x3584 per-channel and INT4 group-128 18944x3584."""
     _say(f"full-size dequant {dt}")
     w, s, _ = bench.make_int8(18944, 3584, 1)
     ql = _layer("int8", w, s)

@@ -105,7 +105,7 @@ def test_canonical_views_state_dict_and_moves(kind):
 
 def test_fp32_activations_read_the_tiled_copy():
     """fp32 activations run the generic kernel, which reads the tiled copy (there is no
-    other copy on the GPU): reference config 1 (INT8 4864 x 896, x fp32 [1, 896])."""
+    other copy on the GPU): the single-layer INT8 workload (4864 x 896, x fp32 [1, 896])."""
     w, s, x = bench.make_int8(4864, 896, 1, x_dtype=torch.float32)
     ql = QuantizedLinear.from_quantized(w.to(DEV), s.to(DEV), quant_type="int8")
     assert ql._buffers["weight_q"].numel() == 0
